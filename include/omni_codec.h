@@ -1,0 +1,248 @@
+/*
+ * omni_codec.h — C ABI of the MI355X (gfx950) codec/vocoder decode kernels.
+ *
+ * Every entry point takes device pointers, explicit int64 sizes and element strides, scalar
+ * parameters and a hipStream_t; it enqueues work on that stream, never synchronises with the
+ * host, never allocates device memory, and returns an int status (OMNI_OK = 0, otherwise one of
+ * the OMNI_ERR_* codes below; omni_codec_error_string names it). Arguments are validated before
+ * any launch, so an error leaves every buffer untouched. All entry points are capturable into a
+ * hipGraph.
+ *
+ * Activations are channels-last: element (b, t, c) of a [B, T, C] tensor sits at
+ * b * stride_b + t * stride_t + c (channel stride 1) unless an entry point says otherwise.
+ *
+ * Reference interfaces replaced (paths relative to the SGLang-Omni checkout):
+ *   omni_rvq_gather_sum          F.embedding + per-codebook sum: DAC ResidualVectorQuantize
+ *                                .from_codes via sglang_omni/models/fishaudio_s2_pro/fish_speech/
+ *                                models/dac/rvq.py:374-388; sglang_omni/models/personaplex/
+ *                                components/mimi.py:275-280; sglang_omni/models/higgs_tts/
+ *                                audio_codec.py:60-78; mean form sglang_omni/models/qwen3_omni/
+ *                                components/code2wav.py:443; ordered gather-sum
+ *                                sglang_omni/models/moss_tts/channel_embedding.py:13-50
+ *   omni_conv1d_fused            channels_last_conv1d / channels_last_conv_transpose1d
+ *                                (sglang_omni/utils/channels_last_conv.py:45-120) with the
+ *                                epilogue of fused_bias_snake_beta
+ *                                (sglang_omni/kernels/bias_snake_beta.py:102-151) and the slot
+ *                                history of history_exchange (sglang_omni/kernels/
+ *                                codec_state.py:150-181) folded in
+ *   omni_single_output_conv      clamped_single_output_conv (sglang_omni/kernels/
+ *                                single_output_conv.py:62-102); tanh form modded_dac.py:829
+ *   omni_history_exchange        history_exchange (sglang_omni/kernels/codec_state.py:150-181)
+ *   omni_overlap_exchange        overlap_exchange (sglang_omni/kernels/codec_state.py:184-210)
+ *   omni_bias_snake_beta         fused_bias_snake_beta (sglang_omni/kernels/bias_snake_beta.py:
+ *                                102-151)
+ *   omni_snake                   snake_channels_last_kernel (sglang_omni/models/fishaudio_drama3/
+ *                                channels_last_decoder.py:35-67,157-184) and fused_snake_beta
+ *                                (sglang_omni/utils/snake_beta.py:200-234)
+ *   omni_advance_slots           pool.frame_positions.index_put_ at the end of decode_slots
+ *                                (sglang_omni/models/qwen3_omni/components/code2wav.py:459)
+ *   omni_codec_capabilities      no kernel counterpart; the platform query of
+ *                                sglang_omni/platforms/rocm.py:22-131
+ */
+#ifndef OMNI_CODEC_H_
+#define OMNI_CODEC_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef struct ihipStream_t* omni_stream_t;
+
+enum {
+  OMNI_OK = 0,
+  OMNI_ERR_INVALID_ARG = 1, /* a shape, stride, pointer or flag outside the documented contract */
+  OMNI_ERR_UNSUPPORTED = 2, /* a valid request this build has no kernel for */
+  OMNI_ERR_LAUNCH = 3,      /* the HIP runtime refused the launch */
+  OMNI_ERR_DEVICE = 4       /* a HIP device query failed */
+};
+
+enum {
+  OMNI_DTYPE_F32 = 0,
+  OMNI_DTYPE_BF16 = 1,
+  OMNI_DTYPE_F16 = 2,
+  OMNI_DTYPE_FP8_E4M3 = 3, /* OCP e4m3fn, the torch.float8_e4m3fn encoding */
+  OMNI_DTYPE_I32 = 4,
+  OMNI_DTYPE_I64 = 5
+};
+
+enum {
+  OMNI_ACTIVATION_NONE = 0,
+  OMNI_ACTIVATION_SNAKE = 1, /* v + b[c] * sin(a[c] * v)^2: Snake1d (a = alpha, b = 1/(alpha+1e-9))
+                                or SnakeBeta (a = exp(alpha), b = 1/(exp(beta)+1e-9)) */
+  OMNI_ACTIVATION_LEAKY_RELU = 2,
+  OMNI_ACTIVATION_TANH = 3,
+  OMNI_ACTIVATION_CLAMP = 4 /* clamp(v, -1, 1), NaN propagated */
+};
+
+/* omni_rvq_gather_sum flags */
+enum {
+  OMNI_RVQ_MEAN = 1,  /* divide the float32 sum by the number of codebooks once at the end */
+  OMNI_RVQ_CLAMP = 2  /* codes above V-1 read entry V-1 (rvq.py:374-388); without it, and for
+                         negative codes always, an out-of-range code adds nothing */
+};
+
+const char* omni_codec_error_string(int status);
+int omni_codec_abi_version(void);
+
+/* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
+   bytes per workgroup and compute-unit count. */
+int omni_codec_capabilities(int device, char* arch, int arch_capacity, int64_t* lds_bytes,
+                            int64_t* compute_units);
+
+/*
+ * RVQ dequantize: out[b, t, :] = sum_{k=0}^{K-1} E_k[codes[b, k, t]], accumulated in float32 in
+ * the order k = 0 .. K-1 (bit-identical to the sequential float32 sum), rounded once to
+ * out_dtype. codes int32/int64 with strides (b, k, t); codebooks [K, V, D] contiguous, float32 or
+ * bf16; out float32 or bf16 at b * out_stride_b + t * out_stride_t + d * out_stride_d.
+ */
+int omni_rvq_gather_sum(const void* codes, int codes_dtype, int64_t batch, int64_t num_codebooks,
+                        int64_t frames, int64_t codes_stride_b, int64_t codes_stride_k,
+                        int64_t codes_stride_t, const void* codebooks, int table_dtype,
+                        int64_t codebook_size, int64_t dim, void* out, int out_dtype,
+                        int64_t out_stride_b, int64_t out_stride_t, int64_t out_stride_d,
+                        int flags, omni_stream_t stream);
+
+/*
+ * One fused convolution over channels-last bf16 activations, on bf16 MFMA:
+ *
+ *   acc[b, i, n] = sum_{j < taps} sum_{ci < c_in} W[n, j, ci] * x[b, i + j * dilation - left_pad, ci]
+ *   v = acc * weight_scale[n] (fp8 weights only) + bias[n % c_out] (+ residual[b, i, n])
+ *   v = ((mix_a[b, i, n] + mix_b[b, i, n]) + v) * mix_scale      (optional, mix_a != NULL)
+ *   sum_out[b, i, n] = v            (float32, optional)
+ *   out[b, i, n] = act(v)           (bf16 or float32; optional when sum_out is given)
+ *
+ * for i < length and n < n_cols. x holds x_length positions (x_length = 0 means length); the
+ * residual, mix and sum_out tensors share the residual strides. A causal Conv1d is taps = k, left_pad = (k-1)*d; a
+ * ConvTranspose1d of stride s is its polyphase form (n = phase * c_out + co, so out viewed as
+ * [B, length * s, c_out] is the transposed conv's output), see the packing helpers of the host
+ * layer. Inputs left of position 0 come from the slot history (below) or are zero; inputs at or
+ * past x_length are zero.
+ *
+ * weight: packed [ceil(c_in/32)][n_cols][taps][32] (ci = 32 * chunk + lane, zero past c_in),
+ * bf16, or fp8-e4m3 with weight_scale[n_cols] float32.
+ *
+ * Streaming history (hist_pool != NULL; requires left_pad == (taps-1)*dilation): the pool is
+ * bf16 [slots][2][left_pad][c_in]; row b reads the copy (slot_parity[s] & 1) of slot
+ * s = slot_index[b] (zeros instead when history_cold) as positions -left_pad .. -1, and writes the
+ * last left_pad samples of (history ++ x) to the other copy. omni_advance_slots flips the parity
+ * once every conv of a decode step has run.
+ */
+typedef struct omni_conv_args {
+  const void* x;
+  int64_t x_stride_b, x_stride_t;
+  int64_t batch, length, c_in;
+  int64_t x_length;
+  const void* weight;
+  int weight_dtype;
+  const float* weight_scale;
+  int64_t n_cols, c_out, taps, dilation, left_pad;
+  const float* bias;
+  const void* hist_pool;
+  const int64_t* slot_index;
+  const int64_t* slot_parity;
+  int64_t hist_num_slots;   /* slots in the pool; a row whose slot is outside [0, slots) reads
+                               zeros and writes no history */
+  int64_t hist_slot_stride; /* elements between consecutive slots (= 2 * left_pad * c_in) */
+  int history_cold;
+  const float* residual;
+  int64_t residual_stride_b, residual_stride_t;
+  const float* mix_a;
+  const float* mix_b;
+  float mix_scale;
+  float* sum_out;
+  void* out;
+  int out_dtype;
+  int64_t out_stride_b, out_stride_t;
+  int activation;
+  const float* act_a;
+  const float* act_b;
+  float act_slope;
+} omni_conv_args;
+
+int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
+
+/*
+ * Conv from channels-last activations to one output channel, stride 1, undilated:
+ *   out[b, i] = act(bias + sum_{j < taps} sum_c weight[j * channels + c] * x[b, i + j - left_pad, c])
+ * accumulated in float32 in one fixed order per position (so any split of positions or rows gives
+ * identical bits) and rounded once. x points at position 0 and holds `length` positions (later
+ * ones read as zero); when context_in_buffer is set, the left_pad positions before it are valid
+ * memory (the reference's padded input); otherwise they come from the slot history (bf16 pool
+ * [slots][2][taps-1][channels], same parity rule as omni_conv1d_fused; needs left_pad = taps-1)
+ * or are zero. activation is OMNI_ACTIVATION_TANH or _CLAMP or _NONE.
+ * x dtype bf16, f16 or f32; out [B, 1, length] at b * out_stride_b + i, dtype of out_dtype.
+ */
+int omni_single_output_conv(const void* x, int x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                            int64_t batch, int64_t length, int64_t channels, int context_in_buffer,
+                            const float* weight, const float* bias, int64_t taps, int64_t left_pad,
+                            const void* hist_pool, const int64_t* slot_index,
+                            const int64_t* slot_parity, int64_t hist_num_slots,
+                            int64_t hist_slot_stride, int history_cold, int activation,
+                            void* out, int out_dtype,
+                            int64_t out_stride_b, omni_stream_t stream);
+
+/*
+ * history_exchange, in place, any element strides: padded[r, :H] = pool[slot_index[r]] (zeros
+ * when cold), padded[r, H + new_samples:] = 0, then pool[slot_index[r]] = padded[r, new_samples :
+ * new_samples + H] (the values before this call's writes). dtype bf16, f16 or f32; bitwise.
+ * Rows whose slot is outside [0, num_slots) are left untouched.
+ */
+int omni_history_exchange(void* padded, int dtype, int64_t rows, int64_t padded_samples,
+                          int64_t channels, int64_t padded_stride_row,
+                          int64_t padded_stride_sample, int64_t padded_stride_channel,
+                          void* history_pool, int64_t num_slots, int64_t history_samples,
+                          int64_t pool_stride_slot,
+                          int64_t pool_stride_sample, int64_t pool_stride_channel,
+                          const int64_t* slot_index, int64_t new_samples, int is_cold,
+                          omni_stream_t stream);
+
+/*
+ * overlap_exchange, in place: output[r, :O] += pool[slot_index[r]] (in float32, rounded once; not
+ * when cold), then pool[slot_index[r]] = output[r, emitted : emitted + O] (values before the add).
+ * Requires emitted_samples >= O. dtype bf16, f16 or f32; bitwise. Rows whose slot is outside
+ * [0, num_slots) are left untouched.
+ */
+int omni_overlap_exchange(void* output, int dtype, int64_t rows, int64_t channels,
+                          int64_t output_stride_row, int64_t output_stride_sample,
+                          int64_t output_stride_channel, void* overlap_pool, int64_t num_slots,
+                          int64_t overlap_samples, int64_t pool_stride_slot,
+                          int64_t pool_stride_sample, int64_t pool_stride_channel,
+                          const int64_t* slot_index, int64_t emitted_samples, int is_cold,
+                          omni_stream_t stream);
+
+/*
+ * fused_bias_snake_beta: t = round(conv + bias); if residual: t = round(t + residual);
+ * sum_out = t; out = round(t + round(inverse_beta * round(round(sin(round(t * alpha_scale)))^2)))
+ * with every round to `dtype` (bf16 or f16), as the eager op chain rounds. conv and out rows
+ * (stride_b apart) are [length, channels] contiguous; residual and sum_out are contiguous
+ * [batch, length, channels]; bias / alpha_scale / inverse_beta are [channels] of param_dtype.
+ */
+int omni_bias_snake_beta(const void* conv, int64_t conv_stride_b, int64_t batch, int64_t length,
+                         int64_t channels, const void* bias, const void* alpha_scale,
+                         const void* inverse_beta, int param_dtype, const void* residual,
+                         void* sum_out, void* out, int64_t out_stride_b, int dtype,
+                         omni_stream_t stream);
+
+/*
+ * Standalone Snake family on [B, T, C] (channels_last != 0) or [B, C, T] rows, dtype bf16, f16 or
+ * f32: y = x + b[c] * sin(a[c] * x)^2. round_intermediates = 0 computes in float32 and rounds once
+ * (Snake1d's channels-last kernel); 1 rounds after every op like the eager SnakeBeta chain.
+ * x and y have identical contiguous layouts.
+ */
+int omni_snake(const void* x, void* y, int dtype, int64_t batch, int64_t frames,
+               int64_t channels, int channels_last, const float* a, const float* b,
+               int round_intermediates, omni_stream_t stream);
+
+/* slot_parity[slot_index[r]] += 1 for r < rows whose slot is in [0, num_slots), ending a decode
+   step (graph-capturable). */
+int omni_advance_slots(int64_t* slot_parity, int64_t num_slots, const int64_t* slot_index,
+                       int64_t rows, omni_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNI_CODEC_H_ */

@@ -1,0 +1,329 @@
+"""CPU oracle for the codec/vocoder decode path: a float32 PyTorch restatement of the reference.
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
+leg of ``bench.py`` may import this module, and only as the checker (or, for the CPU baseline,
+as the timed CPU port of the reference path). The product path never routes through it.
+
+Every function follows the reference's op order on channels-first ``[B, C, T]`` float32 tensors
+and cites the reference file:line it restates (paths relative to the reference checkout;
+``TF/`` is the installed ``transformers`` package, whose DAC/Qwen3-Omni classes the reference
+imports or vendors).
+
+Parity pins (what fixes each function independently of this file's own formulas) live in
+``tests/test_oracle.py``:
+
+* ``rvq_gather_sum``      — brute-force Python loop on tiny inputs; K=1 equals ``F.embedding``;
+                            the mean form equals the sum divided by K; the C restatement
+                            ``oracle/rvq_oracle.c`` agrees bit for bit.
+* ``snake``/``snake_beta`` — float64 closed form; ``transformers`` ``Snake1d`` (installed);
+                            alpha -> 0 limit; x = 0 fixed point.
+* ``causal_conv1d``       — float64 brute-force direct summation; split invariance.
+* ``causal_conv_transpose1d`` — brute-force scatter in float64; streaming split invariance with
+                            the reference's overlap-exchange restatement.
+* decoder composition     — built from the pinned pieces; ``transformers`` ``DacResidualUnit``
+                            agrees on the non-causal padding variant of the residual unit.
+* ``history_exchange_reference`` / ``overlap_exchange_reference`` — the reference's own
+                            pure-torch reference functions (tests/unit_test/kernels/
+                            test_codec_state.py:17-49), pinned by the whole-stream invariants of
+                            the same test file (:52-130).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+SNAKE_EPS = 1e-9
+
+
+# --------------------------------------------------------------------------------------------
+# a1: RVQ dequantize (gather-and-sum of code embeddings)
+# --------------------------------------------------------------------------------------------
+
+
+def clamp_codes(codes: torch.Tensor, codebook_size: int) -> torch.Tensor:
+    """Codes clamped to the last codebook entry, as the DAC quantizer decode does
+    (sglang_omni/models/fishaudio_s2_pro/fish_speech/models/dac/rvq.py:374-388)."""
+    return torch.clamp(codes, max=codebook_size - 1)
+
+
+def rvq_gather_sum(
+    codes: torch.Tensor, codebooks: torch.Tensor, *, mean: bool = False
+) -> torch.Tensor:
+    """out[b, :, t] = sum_k E_k[codes[b, k, t]] accumulated k = 0 -> K-1 in float32, starting
+    from 0.0, as ``from_codes`` does (TF/models/dac/modeling_dac.py:362-371) and as the sequential
+    forms of sglang_omni/models/personaplex/components/mimi.py:275-280 and
+    sglang_omni/models/higgs_tts/audio_codec.py:60-78 do. ``mean`` divides the float32 sum by K
+    once, the Qwen3-Omni form (sglang_omni/models/qwen3_omni/components/code2wav.py:443).
+
+    codes [B, K, T] integer, codebooks [K, V, D] float32 -> [B, D, T] float32.
+    """
+    batch, num_codebooks, frames = codes.shape
+    assert codebooks.shape[0] == num_codebooks
+    total = torch.zeros(batch, frames, codebooks.shape[2], dtype=torch.float32)
+    for k in range(num_codebooks):
+        total = total + codebooks[k].float()[codes[:, k, :].long()]
+    if mean:
+        total = total / num_codebooks
+    return total.transpose(1, 2).contiguous()
+
+
+# --------------------------------------------------------------------------------------------
+# a4: Snake / SnakeBeta / LeakyReLU
+# --------------------------------------------------------------------------------------------
+
+
+def snake(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
+    """DAC ``Snake1d``: x + (alpha + 1e-9)^-1 * sin(alpha * x)^2 per channel
+    (TF/models/dac/modeling_dac.py:86-99; the channels-last Triton form computes the same
+    formula in fp32 at sglang_omni/models/fishaudio_drama3/channels_last_decoder.py:58-62)."""
+    a = alpha.reshape(1, -1, 1).float()
+    return x + (a + SNAKE_EPS).reciprocal() * torch.sin(a * x).pow(2)
+
+
+def snake_beta(
+    x: torch.Tensor, alpha_log: torch.Tensor, beta_log: torch.Tensor
+) -> torch.Tensor:
+    """SnakeBeta with log-scale parameters: x + (exp(beta) + 1e-9)^-1 * sin(exp(alpha) * x)^2
+    (TF/models/qwen3_omni_moe/modeling_qwen3_omni_moe.py:3566-3581; coefficients precomputed once
+    at sglang_omni/kernels/bias_snake_beta.py:29-42)."""
+    a = torch.exp(alpha_log.reshape(1, -1, 1).float())
+    inv_b = 1.0 / (torch.exp(beta_log.reshape(1, -1, 1).float()) + SNAKE_EPS)
+    return x + inv_b * torch.sin(x * a).pow(2)
+
+
+def leaky_relu(x: torch.Tensor, slope: float) -> torch.Tensor:
+    """F.leaky_relu as the HiFT generator applies it
+    (sglang_omni/models/minicpm_o/components/token2wav/hift.py:262,277)."""
+    return F.leaky_relu(x, slope)
+
+
+# --------------------------------------------------------------------------------------------
+# a2 / a3: causal convs
+# --------------------------------------------------------------------------------------------
+
+
+def causal_conv1d(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, dilation: int = 1
+) -> torch.Tensor:
+    """``CausalConvNet.forward`` at stride 1: pad (k-1)*d zeros on the left (the extra right
+    padding is zero at stride 1), then Conv1d
+    (sglang_omni/models/fishaudio_s2_pro/fish_speech/models/dac/modded_dac.py:541-572)."""
+    k = weight.shape[-1]
+    pad = (k - 1) * dilation
+    return F.conv1d(F.pad(x, (pad, 0)), weight, bias, dilation=dilation)
+
+
+def causal_conv_transpose1d(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, stride: int
+) -> torch.Tensor:
+    """``CausalTransConvNet.forward``: ConvTranspose1d, then drop k - s samples on the right
+    only, so T inputs give T * s outputs (modded_dac.py:583-600)."""
+    k = weight.shape[-1]
+    y = F.conv_transpose1d(x, weight, bias, stride=stride)
+    trim = k - stride
+    return y[..., : y.shape[-1] - trim]
+
+
+def same_conv1d(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, dilation: int = 1
+) -> torch.Tensor:
+    """Non-causal Conv1d with padding (k*d - d)//2, as HiFiGAN's get_padding gives
+    (sglang_omni/models/minicpm_o/components/token2wav/hift_layers.py:67-92)."""
+    k = weight.shape[-1]
+    pad = (k * dilation - dilation) // 2
+    return F.conv1d(x, weight, bias, dilation=dilation, padding=pad)
+
+
+def padded_conv_transpose1d(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, stride: int
+) -> torch.Tensor:
+    """HiFT upsampling ConvTranspose1d with padding (k - u)//2
+    (sglang_omni/models/minicpm_o/components/token2wav/hift.py:143-156)."""
+    k = weight.shape[-1]
+    return F.conv_transpose1d(x, weight, bias, stride=stride, padding=(k - stride) // 2)
+
+
+# --------------------------------------------------------------------------------------------
+# a5 / a6: DAC decoder composition
+# --------------------------------------------------------------------------------------------
+
+
+def residual_unit(x: torch.Tensor, unit: dict[str, Any]) -> torch.Tensor:
+    """``ResidualUnit.forward`` (causal): x + conv1x1(Snake(conv7_d(Snake(x)))); the causal conv
+    keeps the length, so the residual is not trimmed (modded_dac.py:619-642)."""
+    y = snake(x, unit["alpha1"])
+    y = causal_conv1d(y, unit["conv1"]["weight"], unit["conv1"]["bias"], unit["dilation"])
+    y = snake(y, unit["alpha2"])
+    y = causal_conv1d(y, unit["conv2"]["weight"], unit["conv2"]["bias"], 1)
+    return x + y
+
+
+def decoder_block(x: torch.Tensor, block: dict[str, Any]) -> torch.Tensor:
+    """``DecoderBlock``: Snake -> causal ConvTranspose1d(k = 2s) -> residual units with
+    dilations 1, 3, 9 (modded_dac.py:742-787)."""
+    x = snake(x, block["alpha"])
+    x = causal_conv_transpose1d(x, block["up"]["weight"], block["up"]["bias"], block["stride"])
+    for unit in block["units"]:
+        x = residual_unit(x, unit)
+    return x
+
+
+def dac_decoder(z: torch.Tensor, weights: dict[str, Any]) -> torch.Tensor:
+    """``Decoder.forward``: causal conv k=7 -> decoder blocks -> Snake -> causal conv to one
+    channel k=7 -> tanh (modded_dac.py:790-835). z [B, D, T] -> [B, 1, T * prod(rates)]."""
+    x = causal_conv1d(z, weights["in_conv"]["weight"], weights["in_conv"]["bias"])
+    for block in weights["blocks"]:
+        x = decoder_block(x, block)
+    x = snake(x, weights["final"]["alpha"])
+    x = causal_conv1d(x, weights["final"]["conv"]["weight"], weights["final"]["conv"]["bias"])
+    return torch.tanh(x)
+
+
+def dac_from_indices(codes: torch.Tensor, weights: dict[str, Any]) -> torch.Tensor:
+    """``DAC.from_indices``: quantizer decode (clamped gather-sum) then the decoder
+    (modded_dac.py:990-992, rvq.py:374-388)."""
+    codebooks = weights["codebooks"]
+    z = rvq_gather_sum(clamp_codes(codes, codebooks.shape[1]), codebooks)
+    return dac_decoder(z, weights)
+
+
+def conv_block(
+    codes: torch.Tensor,
+    codebooks: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    alpha: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The RVQ dequant followed by one causal conv block: x = gather-sum; y = x + Snake(conv(x)),
+    the conv -> Snake -> residual-add order of the single-block workload. Returns (x, y)."""
+    x = rvq_gather_sum(codes, codebooks)
+    y = x + snake(causal_conv1d(x, weight, bias), alpha)
+    return x, y
+
+
+# --------------------------------------------------------------------------------------------
+# a7: streaming state, restated from the reference's pure-torch test references
+# --------------------------------------------------------------------------------------------
+
+
+def history_exchange_reference(
+    padded: torch.Tensor,
+    history_pool: torch.Tensor,
+    slot_index: torch.Tensor,
+    new_samples: int,
+    is_cold: bool,
+) -> None:
+    """In place: history in front of the new samples (zeros when cold), zeros after them, and the
+    last ``history`` samples of history + new saved to the slots
+    (tests/unit_test/kernels/test_codec_state.py:17-34; kernels/codec_state.py:150-181)."""
+    history = int(history_pool.shape[1])
+    if is_cold:
+        padded[:, :history].zero_()
+    else:
+        padded[:, :history].copy_(history_pool.index_select(0, slot_index))
+    padded[:, history + new_samples :].zero_()
+    history_pool.index_copy_(0, slot_index, padded[:, new_samples : new_samples + history])
+
+
+def overlap_exchange_reference(
+    output: torch.Tensor,
+    overlap_pool: torch.Tensor,
+    slot_index: torch.Tensor,
+    emitted_samples: int,
+    is_cold: bool,
+) -> None:
+    """In place: the slot's overlap added to the front of the output (not when cold), and the
+    samples past the emitted ones saved as the slot's overlap
+    (tests/unit_test/kernels/test_codec_state.py:37-49; kernels/codec_state.py:184-210)."""
+    overlap = int(overlap_pool.shape[1])
+    if not is_cold:
+        output[:, :overlap] += overlap_pool.index_select(0, slot_index)
+    overlap_pool.index_copy_(
+        0, slot_index, output[:, emitted_samples : emitted_samples + overlap]
+    )
+
+
+def clamped_single_output_conv(
+    padded: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, length: int
+) -> torch.Tensor:
+    """(B, 1, length) = clamp(bias + conv over a (B, length + k - 1, C) channels-last activation,
+    -1, 1), computed in float64 and rounded once, the expectation of
+    tests/unit_test/kernels/test_single_output_conv.py:32-44."""
+    y = F.conv1d(padded.double().transpose(1, 2), weight.double(), bias.double())
+    return y[..., :length].clamp(-1.0, 1.0)
+
+
+# --------------------------------------------------------------------------------------------
+# cfg4: HiFiGAN mel -> wave body
+# --------------------------------------------------------------------------------------------
+
+
+def hifigan_resblock(x: torch.Tensor, block: dict[str, Any], slope: float) -> torch.Tensor:
+    """HiFiGAN ``ResBlock``: for each dilation, x = x + conv2(act(conv1_d(act(x)))), with 'same'
+    padding and conv2 at dilation 1 (hift_layers.py:57-110; LeakyReLU(slope) as the activation,
+    the classic HiFiGAN choice, where the reference HiFT uses Snake)."""
+    for conv1, conv2, dilation in zip(block["convs1"], block["convs2"], block["dilations"]):
+        xt = leaky_relu(x, slope)
+        xt = same_conv1d(xt, conv1["weight"], conv1["bias"], dilation)
+        xt = leaky_relu(xt, slope)
+        xt = same_conv1d(xt, conv2["weight"], conv2["bias"], 1)
+        x = xt + x
+    return x
+
+
+def hifigan_generator(mel: torch.Tensor, weights: dict[str, Any]) -> torch.Tensor:
+    """The HiFT ``decode_body`` layer order up to the output conv
+    (sglang_omni/models/minicpm_o/components/token2wav/hift.py:255-281): conv_pre k=7 -> per stage
+    LeakyReLU(0.1) -> ConvTranspose1d(padding (k-u)//2) -> mean of the MRF ResBlocks ->
+    LeakyReLU(0.01) -> conv_post to one channel k=7 -> tanh. mel [B, 80, T] -> [B, 1, T * prod(u)].
+    """
+    slope = weights["slope"]
+    x = same_conv1d(mel, weights["conv_pre"]["weight"], weights["conv_pre"]["bias"])
+    for stage in weights["stages"]:
+        x = leaky_relu(x, slope)
+        x = padded_conv_transpose1d(x, stage["up"]["weight"], stage["up"]["bias"], stage["rate"])
+        xs = None
+        for block in stage["resblocks"]:
+            y = hifigan_resblock(x, block, slope)
+            xs = y if xs is None else xs + y
+        x = xs / len(stage["resblocks"])
+    x = leaky_relu(x, weights["final_slope"])
+    x = same_conv1d(x, weights["conv_post"]["weight"], weights["conv_post"]["bias"])
+    return torch.tanh(x)
+
+
+# --------------------------------------------------------------------------------------------
+# a8: fp8 weights (no reference implementation; defined by this build)
+# --------------------------------------------------------------------------------------------
+
+FP8_E4M3_MAX = 448.0
+
+
+def quantize_fp8_per_channel(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel E4M3 quantization: s[co] = max|W[co]| / 448, q = e4m3(W / s).
+    ``weight`` is [C_out, ...]; returns (q float8_e4m3fn, s float32 [C_out])."""
+    flat = weight.float().reshape(weight.shape[0], -1)
+    scale = flat.abs().amax(dim=1) / FP8_E4M3_MAX
+    scale = torch.where(scale > 0, scale, torch.ones_like(scale))
+    q = (flat / scale[:, None]).to(torch.float8_e4m3fn)
+    return q.reshape(weight.shape), scale
+
+
+def dequantize_fp8_per_channel(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """W_deq[co] = float(q[co]) * s[co]."""
+    shape = [-1] + [1] * (q.dim() - 1)
+    return q.float() * scale.reshape(shape)
+
+
+def snr_db(reference: torch.Tensor, actual: torch.Tensor) -> float:
+    """10 log10(sum ref^2 / sum (ref - actual)^2) in float64."""
+    ref = reference.double()
+    noise = (ref - actual.double()).pow(2).sum().item()
+    signal = ref.pow(2).sum().item()
+    if noise == 0:
+        return math.inf
+    return 10.0 * math.log10(signal / noise)

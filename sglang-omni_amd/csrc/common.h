@@ -1,0 +1,78 @@
+// Shared device helpers for the codec decode kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "omni_codec.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16;
+
+#define OMNI_DEVICE __device__ __forceinline__
+
+// Round-to-nearest-even float -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+OMNI_DEVICE __bf16 to_bf16(float x) { return (__bf16)x; }
+OMNI_DEVICE float from_bf16(__bf16 x) { return (float)x; }
+
+OMNI_DEVICE float bits_to_float_bf16(u16 b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+OMNI_DEVICE u16 float_to_bits_bf16(float x) {
+  __bf16 h = to_bf16(x);
+  return *reinterpret_cast<u16*>(&h);
+}
+
+// IEEE half conversions (round to nearest even) for the fp16 variants of the reference kernels.
+OMNI_DEVICE float bits_to_float_f16(u16 b) {
+  _Float16 h = *reinterpret_cast<_Float16*>(&b);
+  return (float)h;
+}
+OMNI_DEVICE u16 float_to_bits_f16(float x) {
+  _Float16 h = (_Float16)x;
+  return *reinterpret_cast<u16*>(&h);
+}
+
+// sin(x) for the Snake family: reduce x to revolutions r = x / (2 pi) - rint(x / (2 pi)) in
+// [-0.5, 0.5] (Payne-Hanek is unnecessary: the activations are bounded), then the hardware
+// v_sin_f32, which takes its argument in revolutions.
+OMNI_DEVICE float snake_sin(float x) {
+  const float inv_two_pi = 0.15915494309189535f;
+  float r = x * inv_two_pi;
+  r = r - __builtin_rintf(r);
+  return __builtin_amdgcn_sinf(r);
+}
+
+// Activations applied in the conv epilogues.
+enum {
+  OMNI_ACT_NONE = 0,
+  OMNI_ACT_SNAKE = 1,       // x + b * sin(a * x)^2 with per-channel a, b
+  OMNI_ACT_LEAKY_RELU = 2,  // x >= 0 ? x : slope * x
+  OMNI_ACT_TANH = 3,
+  OMNI_ACT_CLAMP = 4,       // clamp(x, -1, 1), NaN propagated
+};
+
+OMNI_DEVICE float apply_act(int act, float v, float a, float b, float slope) {
+  switch (act) {
+    case OMNI_ACT_SNAKE: {
+      float s = snake_sin(a * v);
+      return v + b * (s * s);
+    }
+    case OMNI_ACT_LEAKY_RELU:
+      return v >= 0.f ? v : v * slope;
+    case OMNI_ACT_TANH:
+      return tanhf(v);
+    case OMNI_ACT_CLAMP:
+      return v != v ? v : fminf(fmaxf(v, -1.f), 1.f);
+    default:
+      return v;
+  }
+}
+
+#define OMNI_LAUNCH_CHECK()                                   \
+  do {                                                        \
+    hipError_t _e = hipGetLastError();                        \
+    if (_e != hipSuccess) return OMNI_ERR_LAUNCH;             \
+  } while (0)

@@ -1,0 +1,166 @@
+"""ctypes binding of the in-tree ``libomni_codec.so`` (the gfx950 HIP kernels' C ABI).
+
+The library is built by ``sglang-omni_amd/csrc/build.py`` (``__graft_entry__.build()``). There is
+no fallback: if the library is missing, fails to load, or a call returns a nonzero status, the
+caller gets an exception — the decode path never silently runs anything else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libomni_codec.so"
+
+OK = 0
+DTYPE_F32, DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_I32, DTYPE_I64 = range(6)
+ACT_NONE, ACT_SNAKE, ACT_LEAKY_RELU, ACT_TANH, ACT_CLAMP = range(5)
+RVQ_MEAN, RVQ_CLAMP = 1, 2
+
+TORCH_TO_OMNI = {
+    torch.float32: DTYPE_F32,
+    torch.bfloat16: DTYPE_BF16,
+    torch.float16: DTYPE_F16,
+    torch.float8_e4m3fn: DTYPE_FP8_E4M3,
+    torch.int32: DTYPE_I32,
+    torch.int64: DTYPE_I64,
+}
+
+
+class OmniCodecError(RuntimeError):
+    """A nonzero status from the native library."""
+
+
+class ConvArgs(ctypes.Structure):
+    """Mirror of ``omni_conv_args`` in include/omni_codec.h (field order and types match)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_stride_b", ctypes.c_int64),
+        ("x_stride_t", ctypes.c_int64),
+        ("batch", ctypes.c_int64),
+        ("length", ctypes.c_int64),
+        ("c_in", ctypes.c_int64),
+        ("x_length", ctypes.c_int64),
+        ("weight", ctypes.c_void_p),
+        ("weight_dtype", ctypes.c_int),
+        ("weight_scale", ctypes.c_void_p),
+        ("n_cols", ctypes.c_int64),
+        ("c_out", ctypes.c_int64),
+        ("taps", ctypes.c_int64),
+        ("dilation", ctypes.c_int64),
+        ("left_pad", ctypes.c_int64),
+        ("bias", ctypes.c_void_p),
+        ("hist_pool", ctypes.c_void_p),
+        ("slot_index", ctypes.c_void_p),
+        ("slot_parity", ctypes.c_void_p),
+        ("hist_num_slots", ctypes.c_int64),
+        ("hist_slot_stride", ctypes.c_int64),
+        ("history_cold", ctypes.c_int),
+        ("residual", ctypes.c_void_p),
+        ("residual_stride_b", ctypes.c_int64),
+        ("residual_stride_t", ctypes.c_int64),
+        ("mix_a", ctypes.c_void_p),
+        ("mix_b", ctypes.c_void_p),
+        ("mix_scale", ctypes.c_float),
+        ("sum_out", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int),
+        ("out_stride_b", ctypes.c_int64),
+        ("out_stride_t", ctypes.c_int64),
+        ("activation", ctypes.c_int),
+        ("act_a", ctypes.c_void_p),
+        ("act_b", ctypes.c_void_p),
+        ("act_slope", ctypes.c_float),
+    ]
+
+
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_PTR = ctypes.c_void_p
+
+# name -> argtypes (every entry point returns int status unless listed in _RESTYPES)
+SIGNATURES: dict[str, list] = {
+    "omni_codec_error_string": [_INT],
+    "omni_codec_abi_version": [],
+    "omni_codec_capabilities": [_INT, ctypes.c_char_p, _INT, ctypes.POINTER(_I64),
+                                ctypes.POINTER(_I64)],
+    "omni_rvq_gather_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _INT, _I64, _I64,
+                            _PTR, _INT, _I64, _I64, _I64, _INT, _PTR],
+    "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
+    "omni_single_output_conv": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _PTR, _PTR, _I64,
+                                _I64, _PTR, _PTR, _PTR, _I64, _I64, _INT, _INT, _PTR, _INT, _I64,
+                                _PTR],
+    "omni_history_exchange": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _I64, _I64,
+                              _I64, _I64, _I64, _PTR, _I64, _INT, _PTR],
+    "omni_overlap_exchange": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _PTR, _I64, _I64, _I64,
+                              _I64, _I64, _PTR, _I64, _INT, _PTR],
+    "omni_bias_snake_beta": [_PTR, _I64, _I64, _I64, _I64, _PTR, _PTR, _PTR, _INT, _PTR, _PTR,
+                             _PTR, _I64, _INT, _PTR],
+    "omni_snake": [_PTR, _PTR, _INT, _I64, _I64, _I64, _INT, _PTR, _PTR, _INT, _PTR],
+    "omni_advance_slots": [_PTR, _I64, _PTR, _I64, _PTR],
+}
+_RESTYPES = {"omni_codec_error_string": ctypes.c_char_p}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load_library(path: Path | str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and bind the native library; raises if it is absent or incomplete."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(path)
+    if not path.exists():
+        raise OmniCodecError(
+            f"{path} is missing: build the HIP kernels first (python sglang-omni_amd/csrc/build.py)"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if a declared symbol is not exported
+        fn.argtypes = argtypes
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
+    _lib = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        msg = load_library().omni_codec_error_string(status).decode()
+        raise OmniCodecError(f"{what}: status {status} ({msg})")
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    """The kernels run on the GPU only: refuse CPU tensors instead of falling back."""
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise OmniCodecError(
+                f"the HIP codec kernels need GPU tensors; got a tensor on {t.device}"
+            )
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def omni_dtype(dtype: torch.dtype) -> int:
+    try:
+        return TORCH_TO_OMNI[dtype]
+    except KeyError:
+        raise OmniCodecError(f"dtype {dtype} has no kernel") from None
+
+
+def capabilities(device: int = 0) -> dict[str, object]:
+    lib = load_library()
+    arch = ctypes.create_string_buffer(64)
+    lds = _I64()
+    cus = _I64()
+    check(lib.omni_codec_capabilities(device, arch, 64, ctypes.byref(lds), ctypes.byref(cus)),
+          "omni_codec_capabilities")
+    return {"arch": arch.value.decode(), "lds_bytes": lds.value, "compute_units": cus.value}

@@ -1,0 +1,230 @@
+"""Fused polyphase convolution on bf16 MFMA: weight packing and the ``omni_conv1d_fused`` launch.
+
+A stride-one Conv1d (any dilation, causal or 'same' padding) and a ConvTranspose1d (any stride
+and padding) are both computed as
+
+    out[b, i, n] = act(sum_j sum_ci Wp[n, j, ci] * x[b, i + j*d - left_pad, ci] + bias[n % C_out] ...)
+
+with ``n`` running over ``phases * C_out`` columns. For the transposed conv, output sample
+``s*i + r`` of channel ``co`` is column ``n = r*C_out + co`` of position ``i``, so the kernel's
+``[B, L, s*C_out]`` output *is* the transposed conv's ``[B, L*s, C_out]`` output (channels-last).
+This replaces ``channels_last_conv1d`` / ``channels_last_conv_transpose1d``
+(sglang_omni/utils/channels_last_conv.py:45-120) and, with history, the exchange kernels around
+them (sglang_omni/kernels/codec_state.py:150-210).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from .. import _native as N
+
+CHUNK = 32
+
+
+@dataclass
+class PackedConv:
+    """A conv's weights in the kernel's layout plus its geometry.
+
+    weight: [ceil(C_in/32), n_cols, taps, 32] bf16 (or float8_e4m3fn with ``scale[n_cols]``).
+    """
+
+    weight: torch.Tensor
+    scale: torch.Tensor | None
+    bias: torch.Tensor | None  # float32 [C_out]
+    c_in: int
+    c_out: int
+    n_cols: int
+    taps: int
+    dilation: int
+    left_pad: int
+    phases: int
+
+    @property
+    def history(self) -> int:
+        """Input samples a streaming (causal) decode keeps per slot."""
+        return self.left_pad
+
+    def to(self, device: torch.device) -> "PackedConv":
+        return PackedConv(
+            weight=self.weight.to(device),
+            scale=None if self.scale is None else self.scale.to(device),
+            bias=None if self.bias is None else self.bias.to(device),
+            c_in=self.c_in, c_out=self.c_out, n_cols=self.n_cols, taps=self.taps,
+            dilation=self.dilation, left_pad=self.left_pad, phases=self.phases,
+        )
+
+
+def _chunked(w: torch.Tensor) -> torch.Tensor:
+    """[n_cols, taps, C_in] -> [ceil(C_in/32), n_cols, taps, 32], zero-padded channels."""
+    n_cols, taps, c_in = w.shape
+    chunks = (c_in + CHUNK - 1) // CHUNK
+    padded = torch.zeros(n_cols, taps, chunks * CHUNK, dtype=w.dtype, device=w.device)
+    padded[..., :c_in] = w
+    return padded.view(n_cols, taps, chunks, CHUNK).permute(2, 0, 1, 3).contiguous()
+
+
+def polyphase_taps(weight: torch.Tensor, stride: int, padding: int) -> tuple[torch.Tensor, int]:
+    """A ConvTranspose1d weight [C_in, C_out, k] of stride s and padding p as the stride-one
+    weight [s*C_out, taps, C_in] over the input: output s*i + r takes input i + delta through tap
+    j = j0 + s*m (j0 = (r + p) mod s, delta = floor((r + p)/s) - m). Returns (weight, left_pad)."""
+    c_in, c_out, k = weight.shape
+    s = stride
+    entries = []  # (r, delta, j)
+    for r in range(s):
+        j0 = (r + padding) % s
+        c_r = (r + padding) // s
+        m = 0
+        while j0 + s * m < k:
+            entries.append((r, c_r - m, j0 + s * m))
+            m += 1
+    d_min = min(e[1] for e in entries)
+    d_max = max(e[1] for e in entries)
+    taps = d_max - d_min + 1
+    out = torch.zeros(s * c_out, taps, c_in, dtype=weight.dtype, device=weight.device)
+    wt = weight.permute(1, 0, 2)  # [C_out, C_in, k]
+    for r, delta, j in entries:
+        out[r * c_out:(r + 1) * c_out, delta - d_min, :] = wt[:, :, j]
+    return out, -d_min
+
+
+def _finish(w_ntc: torch.Tensor, bias: torch.Tensor | None, *, c_in: int, c_out: int, taps: int,
+            dilation: int, left_pad: int, phases: int, fp8: bool) -> PackedConv:
+    if fp8:
+        # per-output-channel scales (shared by every phase of a transposed conv's channel)
+        w = w_ntc.float().contiguous()
+        amax = w.view(phases, c_out, -1).abs().amax(dim=(0, 2))
+        scale_co = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+        scale = scale_co.repeat(phases)
+        q = (w / scale[:, None, None]).to(torch.float8_e4m3fn)
+        return PackedConv(_chunked(q), scale.contiguous(), None if bias is None else bias.float(),
+                          c_in, c_out, phases * c_out, taps, dilation, left_pad, phases)
+    return PackedConv(_chunked(w_ntc.to(torch.bfloat16)), None,
+                      None if bias is None else bias.float(), c_in, c_out, phases * c_out, taps,
+                      dilation, left_pad, phases)
+
+
+def pack_conv1d(weight: torch.Tensor, bias: torch.Tensor | None, *, dilation: int = 1,
+                causal: bool = True, fp8: bool = False) -> PackedConv:
+    """Conv1d weight [C_out, C_in, k]: causal (left pad (k-1)*d, ``CausalConvNet``,
+    modded_dac.py:541-572) or 'same' (pad (k*d-d)//2, hift_layers.py:67-92)."""
+    c_out, c_in, k = weight.shape
+    left = (k - 1) * dilation if causal else (k * dilation - dilation) // 2
+    return _finish(weight.permute(0, 2, 1), bias, c_in=c_in, c_out=c_out, taps=k,
+                   dilation=dilation, left_pad=left, phases=1, fp8=fp8)
+
+
+def pack_conv_transpose1d(weight: torch.Tensor, bias: torch.Tensor | None, *, stride: int,
+                          padding: int = 0, fp8: bool = False) -> PackedConv:
+    """ConvTranspose1d weight [C_in, C_out, k] in its polyphase form. ``padding = 0`` with a
+    right trim of k - s is ``CausalTransConvNet`` (modded_dac.py:583-600); ``padding = (k-s)//2``
+    is the HiFT upsampler (hift.py:143-156). Either way L inputs give L*s outputs."""
+    c_in, c_out, k = weight.shape
+    w, left = polyphase_taps(weight, stride, padding)
+    return _finish(w, bias, c_in=c_in, c_out=c_out, taps=w.shape[1], dilation=1,
+                   left_pad=left, phases=stride, fp8=fp8)
+
+
+def fused_conv(
+    x: torch.Tensor,
+    conv: PackedConv,
+    out: torch.Tensor | None,
+    *,
+    length: int | None = None,
+    x_length: int | None = None,
+    activation: int = N.ACT_NONE,
+    act_a: torch.Tensor | None = None,
+    act_b: torch.Tensor | None = None,
+    slope: float = 0.0,
+    residual: torch.Tensor | None = None,
+    sum_out: torch.Tensor | None = None,
+    mix: tuple[torch.Tensor, torch.Tensor, float] | None = None,
+    history: torch.Tensor | None = None,
+    slot_index: torch.Tensor | None = None,
+    slot_parity: torch.Tensor | None = None,
+    history_cold: bool = False,
+) -> torch.Tensor:
+    """Launch ``omni_conv1d_fused`` on the current stream.
+
+    x [B, >=x_length, C_in] bf16 (rows may sit in longer buffers; channel stride 1);
+    out [B, length, n_cols] bf16 or float32; residual / sum_out / mix tensors float32 with out's
+    logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16.
+    """
+    N.require_device(x, out, sum_out)
+    if out is None and sum_out is None:
+        raise ValueError("nothing to write: give out or sum_out")
+    batch = x.shape[0]
+    if length is None:
+        length = x.shape[1]
+    if x_length is None:
+        x_length = x.shape[1] if history is None else length
+    if x.dtype != torch.bfloat16 or x.stride(2) != 1:
+        raise ValueError("x must be bf16 with channel stride 1")
+    if x.shape[2] != conv.c_in:
+        raise ValueError(f"x has {x.shape[2]} channels, the conv takes {conv.c_in}")
+    for t in (out, sum_out):
+        if t is None:
+            continue
+        if t.dim() != 3 or t.shape[0] != batch or t.shape[2] != conv.n_cols or t.stride(2) != 1:
+            raise ValueError(f"outputs must be [B, {length}, {conv.n_cols}] with channel stride 1")
+        if t.shape[1] < length:
+            raise ValueError("an output holds fewer positions than length")
+    aux = [t for t in (residual, sum_out) if t is not None]
+    if mix is not None:
+        aux += [mix[0], mix[1]]
+    for t in aux:
+        if t.dtype != torch.float32 or t.stride() != aux[0].stride():
+            raise ValueError("residual / sum_out / mix must be float32 with one shared stride")
+    r_strides = aux[0].stride() if aux else (0, 0, 1)
+    args = N.ConvArgs()
+    args.x = x.data_ptr()
+    args.x_stride_b = x.stride(0)
+    args.x_stride_t = x.stride(1)
+    args.batch = batch
+    args.length = length
+    args.c_in = conv.c_in
+    args.x_length = x_length
+    args.weight = conv.weight.data_ptr()
+    args.weight_dtype = N.omni_dtype(conv.weight.dtype)
+    args.weight_scale = N.ptr(conv.scale)
+    args.n_cols = conv.n_cols
+    args.c_out = conv.c_out
+    args.taps = conv.taps
+    args.dilation = conv.dilation
+    args.left_pad = conv.left_pad
+    args.bias = N.ptr(conv.bias)
+    if history is not None:
+        if slot_index is None or slot_parity is None:
+            raise ValueError("a history pool needs slot_index and slot_parity")
+        args.hist_pool = history.data_ptr()
+        args.slot_index = slot_index.data_ptr()
+        args.slot_parity = slot_parity.data_ptr()
+        args.hist_num_slots = history.shape[0]
+        args.hist_slot_stride = history.stride(0)
+        args.history_cold = int(history_cold)
+    args.residual = N.ptr(residual)
+    args.residual_stride_b = r_strides[0]
+    args.residual_stride_t = r_strides[1]
+    if mix is not None:
+        args.mix_a = mix[0].data_ptr()
+        args.mix_b = mix[1].data_ptr()
+        args.mix_scale = float(mix[2])
+    args.sum_out = N.ptr(sum_out)
+    if out is not None:
+        args.out = out.data_ptr()
+        args.out_dtype = N.omni_dtype(out.dtype)
+        args.out_stride_b = out.stride(0)
+        args.out_stride_t = out.stride(1)
+    else:
+        args.out_dtype = N.DTYPE_BF16
+    args.activation = activation
+    args.act_a = N.ptr(act_a)
+    args.act_b = N.ptr(act_b)
+    args.act_slope = slope
+    lib = N.load_library()
+    N.check(lib.omni_conv1d_fused(ctypes.byref(args), N.stream_handle(x.device)),
+            "omni_conv1d_fused")
+    return out

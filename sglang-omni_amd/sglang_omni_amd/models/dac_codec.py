@@ -1,0 +1,309 @@
+"""The DAC-style causal codec decoder on HIP kernels: ``from_indices`` and streaming slot decodes.
+
+Drop-in for the vocoder stage's codec (the ``AudioCodec`` protocol of
+sglang_omni/scheduling/audio_stream.py:15-20: ``sample_rate``, ``frame_length``, ``delay``,
+``from_indices``) and for the slot-decode API of
+sglang_omni/models/qwen3_omni/components/code2wav.py:417-460 (``decode_slots(codes, pool,
+slot_index, first_decode=...)``) with a ``CodecStatePool``-shaped state pool
+(sglang_omni/models/qwen3_omni/components/codec_state_pool.py:63-145).
+
+The decoder follows ``Decoder`` / ``DecoderBlock`` / ``ResidualUnit`` / ``CausalConvNet`` /
+``CausalTransConvNet`` of sglang_omni/models/fishaudio_s2_pro/fish_speech/models/dac/
+modded_dac.py:541-835 fed by the RVQ gather-sum (rvq.py:374-388). Every op runs in a HIP kernel,
+on channels-last activations, one launch per conv:
+
+    rvq_gather_sum                       codes -> z (bf16)
+    conv k7 (512 -> C0)                  epilogue: bias, Snake(block 0) -> bf16
+    per block:
+      polyphase ConvTranspose (k = 2s)   epilogue: bias -> x (float32 residual stream),
+                                                   Snake(unit 0, act1) -> bf16
+      per residual unit (d = 1, 3, 9):
+        conv k7 dilation d               epilogue: bias, Snake(act2) -> bf16
+        conv k1                          epilogue: bias + x -> x (float32),
+                                                   Snake(next act) -> bf16
+    conv to one channel k7               tanh -> float32 waveform
+
+Streaming keeps each causal conv's left context (its last (k-1)*d input samples) per slot in HBM;
+the conv kernels read it in place of zeros and write the new context themselves, double-buffered
+by a per-slot parity that ``omni_advance_slots`` flips at the end of the step. A transposed conv
+with k = 2s needs one input sample of context, which is exactly the reference's overlap-add.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+
+from .. import _native as N
+from ..kernels.conv import PackedConv, fused_conv, pack_conv1d, pack_conv_transpose1d
+from ..kernels.rvq import rvq_gather_sum
+from ..kernels.single_output_conv import single_output_conv
+from ..quantization import reference_weights
+from .configs import DacDecoderConfig
+
+
+@dataclass
+class _Layer:
+    name: str
+    conv: PackedConv
+    act_a: torch.Tensor | None = None  # Snake a (alpha) of the activation applied in the epilogue
+    act_b: torch.Tensor | None = None  # Snake b (1 / (alpha + 1e-9))
+
+
+@dataclass
+class _Unit:
+    conv1: _Layer  # k = 7, dilation d; epilogue Snake(act2)
+    conv2: _Layer  # k = 1; epilogue + residual, Snake(next act)
+
+
+@dataclass
+class _Block:
+    up: _Layer
+    units: list[_Unit]
+    stride: int
+    c_out: int
+
+
+def _snake_coefficients(alpha: torch.Tensor, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    a = alpha.detach().float().reshape(-1)
+    return a.to(device).contiguous(), (a + 1e-9).reciprocal().to(device).contiguous()
+
+
+class CodecStatePool:
+    """Per-slot decoder state resident in HBM: for every causal conv with left context, a
+    [slots, 2, context, C_in] bf16 pool (two copies, selected by the slot's parity), then
+    ``capture_slots`` scratch slots past the streams' slots (for graph capture), mirroring
+    ``CodecStatePool`` (sglang_omni/models/qwen3_omni/components/codec_state_pool.py:63-145)."""
+
+    def __init__(self, layout: list[tuple[str, int, int]], *, num_slots: int, capture_slots: int = 0,
+                 device: torch.device):
+        total = num_slots + capture_slots
+        self.device = device
+        self.num_slots = num_slots
+        self.free_slots = list(reversed(range(num_slots)))
+        self.scratch_slots = tuple(range(num_slots, total))
+        self.histories = {
+            name: torch.zeros(total, 2, length, channels, dtype=torch.bfloat16, device=device)
+            for name, channels, length in layout
+            if length
+        }
+        self.parity = torch.zeros(total, dtype=torch.int64, device=device)
+        self.bytes_per_slot = sum(2 * 2 * length * channels for _, channels, length in layout)
+
+    def available_size(self) -> int:
+        return len(self.free_slots)
+
+    def acquire(self) -> int | None:
+        """A free slot, or None when every slot is taken."""
+        if not self.free_slots:
+            return None
+        return self.free_slots.pop()
+
+    def release(self, slot: int) -> None:
+        self.free_slots.append(slot)
+
+    def stage_index(self, slots: list[int]) -> torch.Tensor:
+        """The slots' ids on the device, copied from pinned memory so the host never waits."""
+        return torch.tensor(slots, dtype=torch.long, pin_memory=True).to(self.device,
+                                                                          non_blocking=True)
+
+    def zero_slots(self, slots: torch.Tensor) -> None:
+        """Clear the slots' state (both copies) and parity."""
+        for pool in self.histories.values():
+            pool.index_fill_(0, slots, 0)
+        self.parity.index_fill_(0, slots, 0)
+
+
+@dataclass
+class _Workspace:
+    z: torch.Tensor
+    act: list[torch.Tensor]
+    h: torch.Tensor
+    xres: torch.Tensor
+
+
+class DacCodecDecoder:
+    """RVQ dequant + causal DAC decoder, every op on gfx950 HIP kernels.
+
+    ``weights`` is the float32 master weight tree of ``configs.make_dac_weights``;
+    ``weight_format`` "bf16" rounds every conv weight to bf16, "fp8" stores E4M3 weights with a
+    float32 scale per output channel. Activations between convs are bf16, the residual stream
+    float32, accumulation float32.
+    """
+
+    def __init__(self, weights: dict[str, Any], config: DacDecoderConfig, *,
+                 device: torch.device | str = "cuda", weight_format: str = "bf16"):
+        self.config = config
+        self.device = torch.device(device)
+        self.weight_format = weight_format
+        fp8 = weight_format == "fp8"
+        ref = reference_weights(weights, weight_format)
+        self.sample_rate = config.sample_rate
+        self.frame_length = config.hop_length
+        self.delay = 0
+        dev = self.device
+        self.codebooks = ref["codebooks"].to(torch.bfloat16).to(dev).contiguous()
+
+        def conv1d(src: dict, rsrc: dict, dilation: int = 1) -> PackedConv:
+            w = src["weight"] if fp8 else rsrc["weight"]
+            return pack_conv1d(w, rsrc["bias"], dilation=dilation, fp8=fp8).to(dev)
+
+        def convt(src: dict, rsrc: dict, stride: int) -> PackedConv:
+            w = src["weight"] if fp8 else rsrc["weight"]
+            return pack_conv_transpose1d(w, rsrc["bias"], stride=stride, fp8=fp8).to(dev)
+
+        blocks_w, blocks_r = weights["blocks"], ref["blocks"]
+        a, b = _snake_coefficients(blocks_r[0]["alpha"], dev)
+        self.in_conv = _Layer("in_conv", conv1d(weights["in_conv"], ref["in_conv"]), a, b)
+        self.blocks: list[_Block] = []
+        for i, (bw, br) in enumerate(zip(blocks_w, blocks_r)):
+            units_r = br["units"]
+            a, b = _snake_coefficients(units_r[0]["alpha1"], dev)
+            up = _Layer(f"blocks.{i}.up", convt(bw["up"], br["up"], br["stride"]), a, b)
+            units = []
+            for u, (uw, ur) in enumerate(zip(bw["units"], units_r)):
+                a2, b2 = _snake_coefficients(ur["alpha2"], dev)
+                c1 = _Layer(f"blocks.{i}.units.{u}.conv1",
+                            conv1d(uw["conv1"], ur["conv1"], ur["dilation"]), a2, b2)
+                if u + 1 < len(units_r):
+                    nxt = units_r[u + 1]["alpha1"]
+                elif i + 1 < len(blocks_r):
+                    nxt = blocks_r[i + 1]["alpha"]
+                else:
+                    nxt = ref["final"]["alpha"]
+                an, bn = _snake_coefficients(nxt, dev)
+                c2 = _Layer(f"blocks.{i}.units.{u}.conv2", conv1d(uw["conv2"], ur["conv2"]), an, bn)
+                units.append(_Unit(c1, c2))
+            self.blocks.append(_Block(up, units, br["stride"], up.conv.c_out))
+        fw = ref["final"]["conv"]["weight"]  # [1, C, k]
+        self.final_weight = fw[0].t().contiguous().float().to(dev)  # [k, C]
+        self.final_bias = ref["final"]["conv"]["bias"].float().to(dev).contiguous()
+        self.final_taps = fw.shape[-1]
+        self.final_channels = fw.shape[1]
+        self._workspaces: dict[tuple[int, int], _Workspace] = {}
+
+    # ---------------------------------------------------------------- state layout / pool
+
+    def state_layout(self) -> list[tuple[str, int, int]]:
+        """(name, channels, context samples) of every causal conv's per-slot left context, in
+        decode order (k = 1 convs have none)."""
+        layout = [("in_conv", self.in_conv.conv.c_in, self.in_conv.conv.left_pad)]
+        for blk in self.blocks:
+            layout.append((blk.up.name, blk.up.conv.c_in, blk.up.conv.left_pad))
+            for unit in blk.units:
+                layout.append((unit.conv1.name, unit.conv1.conv.c_in, unit.conv1.conv.left_pad))
+                layout.append((unit.conv2.name, unit.conv2.conv.c_in, unit.conv2.conv.left_pad))
+        layout.append(("final", self.final_channels, self.final_taps - 1))
+        return layout
+
+    def new_state_pool(self, num_slots: int, capture_slots: int = 0) -> CodecStatePool:
+        return CodecStatePool(self.state_layout(), num_slots=num_slots,
+                              capture_slots=capture_slots, device=self.device)
+
+    # ---------------------------------------------------------------- decode
+
+    def _workspace(self, batch: int, frames: int) -> _Workspace:
+        key = (batch, frames)
+        ws = self._workspaces.get(key)
+        if ws is None:
+            dev = self.device
+            length = frames
+            max_act = frames * self.in_conv.conv.n_cols
+            max_res = 0
+            for blk in self.blocks:
+                length *= blk.stride
+                max_act = max(max_act, length * blk.c_out)
+                max_res = max(max_res, length * blk.c_out)
+            ws = _Workspace(
+                z=torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16, device=dev),
+                act=[torch.empty(batch * max_act, dtype=torch.bfloat16, device=dev) for _ in range(2)],
+                h=torch.empty(batch * max_res, dtype=torch.bfloat16, device=dev),
+                xres=torch.empty(batch * max_res, dtype=torch.float32, device=dev),
+            )
+            self._workspaces[key] = ws
+        return ws
+
+    @staticmethod
+    def _view(flat: torch.Tensor, batch: int, length: int, channels: int) -> torch.Tensor:
+        return flat[: batch * length * channels].view(batch, length, channels)
+
+    def _decode(self, codes: torch.Tensor, state: dict | None) -> torch.Tensor:
+        if codes.dim() != 3:
+            raise ValueError(f"codes must be [B, Q, T], got {tuple(codes.shape)}")
+        batch, _, frames = codes.shape
+        if batch == 0 or frames == 0:
+            raise ValueError("codes must hold at least one row and one frame")
+        if codes.device != self.device:
+            raise ValueError(f"codes are on {codes.device}, the decoder on {self.device}")
+        ws = self._workspace(batch, frames)
+
+        def hist(name: str) -> dict:
+            if state is None:
+                return {}
+            return {
+                "history": state["pool"].histories.get(name),
+                "slot_index": state["slot_index"],
+                "slot_parity": state["pool"].parity,
+                "history_cold": state["cold"],
+            }
+
+        rvq_gather_sum(codes, self.codebooks, out=ws.z, clamp=True)
+        cur = 0
+        length = frames
+        c0 = self.in_conv.conv.n_cols
+        x_act = self._view(ws.act[cur], batch, length, c0)
+        fused_conv(ws.z, self.in_conv.conv, x_act, activation=N.ACT_SNAKE,
+                   act_a=self.in_conv.act_a, act_b=self.in_conv.act_b, **hist("in_conv"))
+        for blk in self.blocks:
+            nxt = 1 - cur
+            up = blk.up.conv
+            out_len = length * blk.stride
+            # the polyphase output [B, L, s*C] is the transposed conv's [B, L*s, C]
+            y = self._view(ws.act[nxt], batch, out_len, blk.c_out)
+            xres = self._view(ws.xres, batch, out_len, blk.c_out)
+            fused_conv(x_act, up, y.view(batch, length, up.n_cols), activation=N.ACT_SNAKE,
+                       act_a=blk.up.act_a, act_b=blk.up.act_b,
+                       sum_out=xres.view(batch, length, up.n_cols), **hist(blk.up.name))
+            length = out_len
+            h = self._view(ws.h, batch, length, blk.c_out)
+            for u, unit in enumerate(blk.units):
+                fused_conv(y, unit.conv1.conv, h, activation=N.ACT_SNAKE, act_a=unit.conv1.act_a,
+                           act_b=unit.conv1.act_b, **hist(unit.conv1.name))
+                last = u + 1 == len(blk.units)
+                fused_conv(h, unit.conv2.conv, y, activation=N.ACT_SNAKE, act_a=unit.conv2.act_a,
+                           act_b=unit.conv2.act_b, residual=xres,
+                           sum_out=None if last else xres, **hist(unit.conv2.name))
+            x_act = y
+            cur = nxt
+        wave = torch.empty(batch, 1, length, dtype=torch.float32, device=self.device)
+        single_output_conv(x_act, self.final_weight, self.final_bias, wave,
+                           activation=N.ACT_TANH, left_pad=self.final_taps - 1, **hist("final"))
+        if state is not None:
+            lib = N.load_library()
+            parity = state["pool"].parity
+            N.check(lib.omni_advance_slots(parity.data_ptr(), parity.shape[0],
+                                           state["slot_index"].data_ptr(), batch,
+                                           N.stream_handle(self.device)), "omni_advance_slots")
+        return wave
+
+    @torch.no_grad()
+    def from_indices(self, indices: torch.Tensor) -> torch.Tensor:
+        """[B, Q, T] codes -> [B, 1, T * frame_length] float32 waveform (``DAC.from_indices``,
+        modded_dac.py:990-992). Codes above the codebook size read its last entry."""
+        return self._decode(indices, None)
+
+    __call__ = from_indices
+
+    @torch.no_grad()
+    def decode_slots(self, codes: torch.Tensor, pool: CodecStatePool, slot_index: torch.Tensor,
+                     *, first_decode: bool) -> torch.Tensor:
+        """The (B, 1, T * frame_length) waveform of the (B, Q, T) codes after the frames the rows'
+        slots hold, their state advanced in place; decoding a stream in any split of chunks gives
+        the waveform ``from_indices`` gives on all of it. A first decode starts every row's
+        stream and reads no slot. Rows must name distinct slots. Capturable in a graph with a
+        static ``slot_index``."""
+        if slot_index.dtype != torch.int64 or slot_index.shape != (codes.shape[0],):
+            raise ValueError("slot_index must be int64 [B]")
+        return self._decode(codes, {"pool": pool, "slot_index": slot_index, "cold": first_decode})
