@@ -1,0 +1,236 @@
+"""Benchmark of the codec decode stage on one MI355X.
+
+Default workload (the streaming serving pattern): the 24 kHz codec decoder (16 x 2048 x 512 RVQ
+tables, 1536 channels, strides 8/8/5/6 = x1920) decoding 64 independent streams; one step decodes
+a 12-frame chunk of every stream (768 frames = 61.44 audio-seconds) with the per-layer causal-conv
+state held in the HBM slot pool, 20 chunks per stream (the streams restart every 20 steps). Codes
+are uniform random per stream (seed 1 + s), weights seeded random (kaiming, bf16). Inputs are
+staged in HBM before the timed region.
+
+Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
+  roofline      the conv kernel (omni_conv1d_fused, bf16 MFMA): algorithmic FLOPs per launch over
+                its mean launch time, timed with HIP events on the launch stream;
+  rvq_gather    the RVQ gather-sum's achieved bytes/s, in the step and on a large batch;
+  cpu_baseline  the float32 CPU restatement of the reference path (oracle/codec_oracle.py) timed
+                on this host's cores on a bounded sample of the same workload.
+
+--workload selects another configuration (single24k, hifigan, fp8long) for manual runs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO / "sglang-omni_amd", REPO):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import torch  # noqa: E402
+
+METRIC = "audio-sec decoded per wall-sec (xRT) at batch 64; HBM GB/s & MFMA % of peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBPS = 8000.0
+CHUNK_FRAMES = 12
+CHUNKS_PER_STREAM = 20
+STREAMS = 64
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def sync() -> None:
+    torch.cuda.synchronize()
+
+
+def timed_steps(step, steps: int, warmup: int) -> float:
+    for i in range(warmup):
+        step(i)
+    sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(warmup + i)
+    sync()
+    return time.perf_counter() - t0
+
+
+def measure_rvq_large(device: torch.device) -> dict:
+    """The gather-sum alone at the long-form quantizer's shape: 8 x 1500 frames, 32 codebooks of
+    1024 x 512 bf16, int32 codes, bf16 output (33 920 B per frame)."""
+    from sglang_omni_amd.kernels.rvq import rvq_gather_sum
+
+    gen = torch.Generator().manual_seed(0)
+    tables = (torch.randn(32, 1024, 512, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    codes = torch.randint(0, 1024, (8, 32, 1500), generator=gen, dtype=torch.int32).to(device)
+    out = torch.empty(8, 1500, 512, dtype=torch.bfloat16, device=device)
+    frames = 8 * 1500
+    per_frame = 32 * 512 * 2 + 512 * 2 + 32 * 4
+    for _ in range(3):
+        rvq_gather_sum(codes, tables, out=out)
+    reps = 20
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        rvq_gather_sum(codes, tables, out=out)
+    end.record()
+    sync()
+    ms = start.elapsed_time(end) / reps
+    gbps = frames * per_frame / (ms * 1e-3) / 1e9
+    return {"frames": frames, "bytes_per_frame": per_frame, "ms": round(ms, 4),
+            "achieved_GBps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4)}
+
+
+def cpu_baseline(config, weights, frames: int, streams: int) -> dict:
+    """The float32 CPU restatement of the reference decode path on `streams` x `frames` frames."""
+    from oracle import codec_oracle as O
+    from sglang_omni_amd.quantization import reference_weights
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    ref = reference_weights(weights, "bf16")
+    gen = torch.Generator().manual_seed(1)
+    codes = torch.randint(0, config.codebook_size, (streams, config.n_codebooks, frames),
+                          generator=gen)
+    O.dac_from_indices(codes[:1, :, :2], ref)  # warm the CPU kernels
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        O.dac_from_indices(codes, ref)
+    dt = time.perf_counter() - t0
+    audio = streams * frames / config.frame_rate
+    return {"value": round(audio / dt, 3), "unit": "audio-s/s", "cores": threads, "kind": "port",
+            "sample": f"{streams} streams x {frames} frames ({audio:.2f} audio-s) whole-stream "
+                      f"decode, float32, torch CPU, {dt:.1f} s"}
+
+
+def bench_streaming(args, device) -> dict:
+    from sglang_omni_amd.models import DacCodecDecoder, make_dac_weights
+    from sglang_omni_amd.models.configs import CODEC_24K, dac_macs_per_frame
+    from sglang_omni_amd.utils.timing import NO_TIMER, LaunchTimer
+
+    config = CODEC_24K
+    weights = make_dac_weights(config, seed=0)
+    decoder = DacCodecDecoder(weights, config, device=device)
+    total = CHUNK_FRAMES * CHUNKS_PER_STREAM
+    codes = torch.stack([
+        torch.randint(0, config.codebook_size, (config.n_codebooks, total),
+                      generator=torch.Generator().manual_seed(1 + s))
+        for s in range(STREAMS)
+    ])
+    chunks = [codes[..., c * CHUNK_FRAMES:(c + 1) * CHUNK_FRAMES].contiguous().to(device)
+              for c in range(CHUNKS_PER_STREAM)]
+    pool = decoder.new_state_pool(num_slots=STREAMS)
+    slot_index = torch.arange(STREAMS, device=device)
+
+    def step(i: int) -> None:
+        c = i % CHUNKS_PER_STREAM
+        decoder.decode_slots(chunks[c], pool, slot_index, first_decode=c == 0)
+
+    log(f"streaming: {STREAMS} streams x {CHUNK_FRAMES}-frame chunks, warmup {args.warmup}, "
+        f"steps {args.steps}")
+    elapsed = timed_steps(step, args.steps, args.warmup)
+    audio_per_step = STREAMS * CHUNK_FRAMES / config.frame_rate
+    value = args.steps * audio_per_step / elapsed
+    log(f"streaming: {elapsed * 1e3 / args.steps:.3f} ms/step, {value:.1f} xRT")
+
+    # instrumented pass: every launch between HIP events on the launch stream
+    timer = LaunchTimer()
+    decoder.timer = timer
+    inst_steps = min(args.steps, CHUNKS_PER_STREAM)
+    for i in range(inst_steps):
+        step(args.warmup + args.steps + i)
+    sync()
+    decoder.timer = NO_TIMER
+    summ = timer.summary()
+    conv = summ["conv"]
+    conv_flops_launch = conv["work"] / conv["launches"]
+    conv_ms_launch = conv["ms"] / conv["launches"]
+    achieved = conv_flops_launch / (conv_ms_launch * 1e-3) / 1e12
+    rvq = summ["rvq"]
+    rvq_gbps = rvq["work"] / (rvq["ms"] * 1e-3) / 1e9
+    # the decoder's MFMA convs: everything but the final one-channel conv
+    final_macs = config.stage_channels()[-1] * config.kernel_size * config.hop_length
+    expected = 2.0 * (dac_macs_per_frame(config) - final_macs) * STREAMS * CHUNK_FRAMES
+    log(f"conv: {conv['launches'] / inst_steps:.0f} launches/step, "
+        f"{conv['ms'] / inst_steps:.3f} ms/step, {achieved:.1f} TFLOP/s; work/step "
+        f"{conv['work'] / inst_steps / 1e12:.4f} TFLOP (layer list: {expected / 1e12:.4f})")
+    kernel_ms = sum(v["ms"] for v in summ.values()) / inst_steps
+    result = {
+        "value": value,
+        "ms_per_step": elapsed * 1e3 / args.steps,
+        "config": {"workload": "streaming 24 kHz codec decode, 64 streams x 12-frame chunks, "
+                               "36-frame context in per-layer slot state, 20 chunks per stream",
+                   "streams": STREAMS, "chunk_frames": CHUNK_FRAMES,
+                   "audio_s_per_step": audio_per_step, "codebooks": "16 x 2048 x 512",
+                   "channels": 1536, "strides": [8, 8, 5, 6], "weights": "bf16"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None,
+                     "kernel": "omni_conv1d_fused (conv_mfma_kernel, all launches of a step)",
+                     "launches_per_step": conv["launches"] / inst_steps,
+                     "flops_per_launch": conv_flops_launch, "mean_launch_ms": conv_ms_launch},
+        "rvq_gather": {"in_step_GBps": round(rvq_gbps, 1),
+                       "in_step_us": round(rvq["ms"] * 1e3 / rvq["launches"], 2)},
+        "kernel_ms_per_step": round(kernel_ms, 4),
+    }
+    if not args.no_rvq_large:
+        result["rvq_gather"]["large_batch"] = measure_rvq_large(device)
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(config, weights, frames=24, streams=2)
+    return result
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=40)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", default="streaming64")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-rvq-large", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); streams shard across GPUs by process, see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda", 0)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    if args.workload != "streaming64":
+        raise SystemExit(f"unknown workload {args.workload}")
+    r = bench_streaming(args, device)
+    line = {
+        "metric": METRIC,
+        "value": round(r["value"], 2),
+        "unit": "audio-s/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random codes, seeded random-init weights)",
+        "config": r["config"],
+        "roofline": r["roofline"],
+        "rvq_gather": r["rvq_gather"],
+        "kernel_ms_per_step": r["kernel_ms_per_step"],
+    }
+    if "cpu_baseline" in r:
+        line["cpu_baseline"] = r["cpu_baseline"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -115,24 +115,27 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 
   // blockIdx -> (b, position tile, column tile), column tile fastest so the workgroups that share
   // an input tile run back to back.
-  int64_t bid = blockIdx.x;
-  const int64_t n_tile = bid % p.n_tiles;
-  bid /= p.n_tiles;
-  const int64_t p_tile = bid % p.p_tiles;
-  const int64_t b = bid / p.p_tiles;
-  const int64_t n0 = n_tile * BCO;
-  const int64_t i0 = p_tile * BP;
+  const int n_tiles = (int)p.n_tiles;
+  const int p_tiles = (int)p.p_tiles;
+  const int bid = blockIdx.x;
+  const int n_tile = bid % n_tiles;
+  const int p_tile = (bid / n_tiles) % p_tiles;
+  const int64_t b = bid / (n_tiles * p_tiles);
+  const int n0 = n_tile * BCO;
+  const int i0 = p_tile * BP;
 
-  const int64_t taps = p.taps;
-  const int64_t dil = p.dil;
-  const int64_t halo = (taps - 1) * dil;
-  const int64_t rows = BP + halo;
-  const int64_t L = p.length;     // output positions
-  const int64_t XL = p.x_length;  // input positions (history ends at XL)
-  const int64_t H = p.lpad;       // history samples when streaming
+  const int taps = (int)p.taps;
+  const int dil = (int)p.dil;
+  const int lpad = (int)p.lpad;
+  const int rows = BP + (taps - 1) * dil;
+  const int L = (int)p.length;     // output positions
+  const int XL = (int)p.x_length;  // input positions (the history ends at XL)
+  const int H = lpad;              // history samples when streaming
+  const int c_in = (int)p.c_in;
+  const int n_cols = (int)p.n_cols;
 
-  u16* xs = lds;                      // [rows][40]
-  u16* ws = lds + rows * kRowElems;   // [taps][BCO][40]
+  u16* xs = lds;                     // [rows][40]
+  u16* ws = lds + rows * kRowElems;  // [taps][BCO][40]
 
   const u16* hist_read = nullptr;
   u16* hist_write = nullptr;
@@ -140,91 +143,114 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   if (slot >= 0 && slot < p.hist_slots) {
     const int64_t parity = p.slot_parity[slot] & 1;
     const u16* base = p.hist + slot * p.hist_slot_stride;
-    hist_read = p.hist_cold ? nullptr : base + parity * H * p.c_in;
-    hist_write = const_cast<u16*>(base) + (1 - parity) * H * p.c_in;
+    hist_read = p.hist_cold ? nullptr : base + parity * H * c_in;
+    hist_write = const_cast<u16*>(base) + (1 - parity) * H * c_in;
   }
   const bool writes_history = hist_write != nullptr && n_tile == 0 && H > 0;
 
-  const int64_t chunks = (p.c_in + kChunk - 1) / kChunk;
-  const int64_t x_pieces = rows * 4;
-  const int64_t w_pieces = (int64_t)BCO * taps * 4;
+  const int chunks = (c_in + kChunk - 1) / kChunk;
+  const int x_pieces = rows * 4;
+  const int w_pieces = BCO * taps * 4;
+  // NT is a multiple of 4, so a thread stages the same 8-channel quarter q of every row it loads.
+  const int q8 = (tid & 3) * 8;
+
+  // Per-thread staging descriptors, computed once: each input piece's element offset at channel
+  // q8 of chunk 0 (from the x row or from the slot history, 2 bits of xmode per piece: 0 zeros,
+  // 1 x, 2 history), and each weight piece's LDS slot (-1 = none) and whether it is a real column.
+  const u16* xrow = p.x + b * p.x_sb;
+  int xoff[Tile::X_PIECES];
+  unsigned xmode = 0;
+#pragma unroll
+  for (int u = 0; u < Tile::X_PIECES; ++u) {
+    const int piece = tid + u * NT;
+    const int pos = i0 - lpad + (piece >> 2);
+    int off = 0;
+    if (piece < x_pieces) {
+      if (pos >= 0 && pos < XL) {
+        off = pos * (int)p.x_st + q8;
+        xmode |= 1u << (2 * u);
+      } else if (pos < 0 && hist_read != nullptr) {
+        off = (H + pos) * c_in + q8;
+        xmode |= 2u << (2 * u);
+      }
+    }
+    xoff[u] = off;
+  }
+  int wlds[Tile::W_PIECES];
+  unsigned wreal = 0;
+#pragma unroll
+  for (int u = 0; u < Tile::W_PIECES; ++u) {
+    const int piece = tid + u * NT;
+    int off = -1;
+    if (piece < w_pieces) {
+      // packed order within a chunk is [n][tap][32]
+      const int nl = piece / (taps * 4);
+      const int rem = piece - nl * taps * 4;
+      off = ((rem >> 2) * BCO + nl) * kRowElems + (rem & 3) * 8;
+      if (n0 + nl < n_cols) wreal |= 1u << u;
+    }
+    wlds[u] = off;
+  }
 
   uint4 xr[Tile::X_PIECES];
-  uint4 wr[Tile::W_PIECES];
+  uint4 wr[W_FP8 ? 1 : Tile::W_PIECES];
   uint2 wr8[W_FP8 ? Tile::W_PIECES : 1];
 
-  auto load_chunk = [&](int64_t kc) {
-    const int64_t ci_base = kc * kChunk;
+  auto load_chunk = [&](int kc) {
+    const bool in_range = kc * kChunk + q8 < c_in;
 #pragma unroll
     for (int u = 0; u < Tile::X_PIECES; ++u) {
-      const int64_t piece = tid + (int64_t)u * NT;
+      const unsigned mode = (xmode >> (2 * u)) & 3u;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (piece < x_pieces) {
-        const int64_t r = piece >> 2;
-        const int64_t ci = ci_base + (piece & 3) * 8;
-        const int64_t pos = i0 - p.lpad + r;
-        if (ci < p.c_in) {
-          if (pos >= 0 && pos < XL) {
-            v = *reinterpret_cast<const uint4*>(p.x + b * p.x_sb + pos * p.x_st + ci);
-          } else if (pos < 0 && hist_read != nullptr) {
-            v = *reinterpret_cast<const uint4*>(hist_read + (H + pos) * p.c_in + ci);
-          }
-        }
+      if (mode != 0 && in_range) {
+        const u16* base = mode == 1 ? xrow : hist_read;
+        v = *reinterpret_cast<const uint4*>(base + xoff[u] + kc * kChunk);
       }
       xr[u] = v;
     }
-    const int64_t wbase = (kc * p.n_cols + n0) * taps * kChunk;
+    const int64_t wbase = ((int64_t)kc * n_cols + n0) * taps * kChunk;
 #pragma unroll
     for (int u = 0; u < Tile::W_PIECES; ++u) {
-      const int64_t piece = tid + (int64_t)u * NT;
-      const int64_t n = n0 + piece / (taps * 4);
+      const int64_t off = wbase + (int64_t)(tid + u * NT) * 8;
       if constexpr (W_FP8) {
         uint2 v = make_uint2(0, 0);
-        if (piece < w_pieces && n < p.n_cols)
-          v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(p.weight) +
-                                              wbase + piece * 8);
+        if (wreal & (1u << u))
+          v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(p.weight) + off);
         wr8[u] = v;
       } else {
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (piece < w_pieces && n < p.n_cols)
-          v = *reinterpret_cast<const uint4*>(reinterpret_cast<const u16*>(p.weight) + wbase +
-                                              piece * 8);
+        if (wreal & (1u << u))
+          v = *reinterpret_cast<const uint4*>(reinterpret_cast<const u16*>(p.weight) + off);
         wr[u] = v;
       }
     }
   };
 
-  auto store_chunk = [&](int64_t kc) {
-    const int64_t ci_base = kc * kChunk;
+  auto store_chunk = [&](int kc) {
+    const bool in_range = kc * kChunk + q8 < c_in;
 #pragma unroll
     for (int u = 0; u < Tile::X_PIECES; ++u) {
-      const int64_t piece = tid + (int64_t)u * NT;
+      const int piece = tid + u * NT;
       if (piece < x_pieces) {
-        const int64_t r = piece >> 2;
-        const int q = (int)(piece & 3);
-        *reinterpret_cast<uint4*>(xs + r * kRowElems + q * 8) = xr[u];
-        if (writes_history) {
-          const int64_t pos = i0 - p.lpad + r;
-          const int64_t ci = ci_base + q * 8;
+        *reinterpret_cast<uint4*>(xs + (piece >> 2) * kRowElems + q8) = xr[u];
+        if (writes_history && in_range) {
+          // the new history is the last H samples of (history ++ x); each sample is written by
+          // the workgroup whose own positions hold it (negative ones by the first tile)
+          const int pos = i0 - lpad + (piece >> 2);
           const bool owned = (pos >= i0 && pos < i0 + BP) || (i0 == 0 && pos < 0);
-          if (owned && pos >= XL - H && pos < XL && ci < p.c_in)
-            *reinterpret_cast<uint4*>(hist_write + (pos - (XL - H)) * p.c_in + ci) = xr[u];
+          if (owned && pos >= XL - H && pos < XL)
+            *reinterpret_cast<uint4*>(hist_write + (int64_t)(pos - (XL - H)) * c_in + q8 +
+                                      kc * kChunk) = xr[u];
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < Tile::W_PIECES; ++u) {
-      const int64_t piece = tid + (int64_t)u * NT;
-      if (piece < w_pieces) {
-        // piece -> (n_local, tap, q): packed order is [n][tap][32]
-        const int64_t nl = piece / (taps * 4);
-        const int64_t rem = piece - nl * taps * 4;
-        const int64_t j = rem >> 2;
-        const int q = (int)(rem & 3);
+      if (wlds[u] >= 0) {
         uint4 v;
         if constexpr (W_FP8) v = fp8x8_to_bf16x8(wr8[u]);
         else v = wr[u];
-        *reinterpret_cast<uint4*>(ws + (j * BCO + nl) * kRowElems + q * 8) = v;
+        *reinterpret_cast<uint4*>(ws + wlds[u]) = v;
       }
     }
   };
@@ -241,56 +267,66 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   const int wp0 = wave_p * TP * 16;
 
   load_chunk(0);
-  for (int64_t kc = 0; kc < chunks; ++kc) {
+  for (int kc = 0; kc < chunks; ++kc) {
     __syncthreads();
     store_chunk(kc);
     __syncthreads();
     if (kc + 1 < chunks) load_chunk(kc + 1);
-    for (int64_t j = 0; j < taps; ++j) {
+    const u16* wtap = ws + (wco0 + lrow) * kRowElems + lk;
+    const u16* xtap = xs + (wp0 + lrow) * kRowElems + lk;
+    for (int j = 0; j < taps; ++j) {
       bf16x8 a[TCO];
 #pragma unroll
       for (int c = 0; c < TCO; ++c)
-        a[c] = *reinterpret_cast<const bf16x8*>(ws + (j * BCO + wco0 + c * 16 + lrow) * kRowElems +
-                                                lk);
-      const int64_t xrow0 = wp0 + lrow + j * dil;
+        a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * kRowElems);
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
-        const bf16x8 bv =
-            *reinterpret_cast<const bf16x8*>(xs + (xrow0 + t * 16) * kRowElems + lk);
+        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(xtap + t * 16 * kRowElems);
 #pragma unroll
         for (int c = 0; c < TCO; ++c)
           acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
       }
+      wtap += BCO * kRowElems;
+      xtap += dil * kRowElems;
     }
   }
 
-  // Epilogue: lane holds D[co = 4*(lane/16) + e][pos = lane % 16] of each 16x16 tile.
+  // Epilogue: lane holds D[co = 4*(lane/16) + e][pos = lane % 16] of each 16x16 tile. Column by
+  // column, every position's residual / mix operands are loaded before the first store (they
+  // may alias sum_out), so the loads of a column overlap.
   const int ch_in_tile = (lane >> 4) * 4;
 #pragma unroll
   for (int c = 0; c < TCO; ++c) {
-    const int64_t n = n0 + wco0 + c * 16 + ch_in_tile;
-    if (n >= p.n_cols) continue;
+    const int n = n0 + wco0 + c * 16 + ch_in_tile;
+    if (n >= n_cols) continue;
     float scale[4], bias[4], aa[4], bb[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int64_t co = (n + e) % p.c_out;
+      const int co = (n + e) % (int)p.c_out;
       scale[e] = p.wscale ? p.wscale[n + e] : 1.f;
       bias[e] = p.bias ? p.bias[co] : 0.f;
       aa[e] = p.act_a ? p.act_a[co] : 0.f;
       bb[e] = p.act_b ? p.act_b[co] : 0.f;
     }
+    float4 res[TP];
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
-      const int64_t pos = i0 + wp0 + t * 16 + lrow;
+      const int pos = i0 + wp0 + t * 16 + lrow;
+      res[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (pos < L && p.residual)
+        res[t] = *reinterpret_cast<const float4*>(p.residual + b * p.r_sb +
+                                                  (int64_t)pos * p.r_st + n);
+    }
+#pragma unroll
+    for (int t = 0; t < TP; ++t) {
+      const int pos = i0 + wp0 + t * 16 + lrow;
       if (pos >= L) continue;
       float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[c][t][e] * scale[e] + bias[e];
-      const int64_t roff = b * p.r_sb + pos * p.r_st + n;
-      if (p.residual) {
-        const float4 r = *reinterpret_cast<const float4*>(p.residual + roff);
-        v[0] += r.x; v[1] += r.y; v[2] += r.z; v[3] += r.w;
-      }
+      v[0] = acc[c][t][0] * scale[0] + bias[0] + res[t].x;
+      v[1] = acc[c][t][1] * scale[1] + bias[1] + res[t].y;
+      v[2] = acc[c][t][2] * scale[2] + bias[2] + res[t].z;
+      v[3] = acc[c][t][3] * scale[3] + bias[3] + res[t].w;
+      const int64_t roff = b * p.r_sb + (int64_t)pos * p.r_st + n;
       if (p.mix_a) {
         const float4 ma = *reinterpret_cast<const float4*>(p.mix_a + roff);
         const float4 mb = *reinterpret_cast<const float4*>(p.mix_b + roff);
@@ -305,15 +341,15 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       float y[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[e] = apply_act(p.act, v[e], aa[e], bb[e], p.slope);
+      const int64_t ooff = b * p.o_sb + (int64_t)pos * p.o_st + n;
       if (p.out_bf16) {
         uint2 o;
         o.x = pack_bf16x2(y[0], y[1]);
         o.y = pack_bf16x2(y[2], y[3]);
-        *reinterpret_cast<uint2*>(reinterpret_cast<u16*>(p.out) + b * p.o_sb + pos * p.o_st + n) =
-            o;
+        *reinterpret_cast<uint2*>(reinterpret_cast<u16*>(p.out) + ooff) = o;
       } else {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + b * p.o_sb + pos * p.o_st +
-                                   n) = make_float4(y[0], y[1], y[2], y[3]);
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + ooff) =
+            make_float4(y[0], y[1], y[2], y[3]);
       }
     }
   }
@@ -337,7 +373,11 @@ int launch_tile(ConvParams p, bool fp8, hipStream_t stream) {
   p.n_tiles = (p.n_cols + Tile::BCO - 1) / Tile::BCO;
   const int64_t blocks = p.batch * p.p_tiles * p.n_tiles;
   if (blocks == 0) return OMNI_OK;
-  if (blocks > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
+  // in-block offsets are 32-bit: a row of x, a slot's history and a chunk of weights
+  if (blocks > 0x7fffffffLL || p.n_cols * p.taps * kChunk > 0x7fffffffLL ||
+      p.length > 0x3fffffffLL || (p.x_length + p.lpad) * p.x_st > 0x7fffffffLL ||
+      p.lpad * p.c_in > 0x7fffffffLL)
+    return OMNI_ERR_UNSUPPORTED;
   const size_t lds = Tile::lds_bytes(halo, p.taps);
   if (lds > 160 * 1024) return OMNI_ERR_UNSUPPORTED;
   // The dynamic-LDS limit is raised once per kernel instantiation (to the 160 KiB maximum), on

@@ -42,6 +42,7 @@ class PackedConv:
     dilation: int
     left_pad: int
     phases: int
+    macs_per_position: int = 0  # algorithmic multiply-adds per output (conv) / input (transposed) position
 
     @property
     def history(self) -> int:
@@ -55,6 +56,7 @@ class PackedConv:
             bias=None if self.bias is None else self.bias.to(device),
             c_in=self.c_in, c_out=self.c_out, n_cols=self.n_cols, taps=self.taps,
             dilation=self.dilation, left_pad=self.left_pad, phases=self.phases,
+            macs_per_position=self.macs_per_position,
         )
 
 
@@ -113,8 +115,10 @@ def pack_conv1d(weight: torch.Tensor, bias: torch.Tensor | None, *, dilation: in
     modded_dac.py:541-572) or 'same' (pad (k*d-d)//2, hift_layers.py:67-92)."""
     c_out, c_in, k = weight.shape
     left = (k - 1) * dilation if causal else (k * dilation - dilation) // 2
-    return _finish(weight.permute(0, 2, 1), bias, c_in=c_in, c_out=c_out, taps=k,
-                   dilation=dilation, left_pad=left, phases=1, fp8=fp8)
+    packed = _finish(weight.permute(0, 2, 1), bias, c_in=c_in, c_out=c_out, taps=k,
+                     dilation=dilation, left_pad=left, phases=1, fp8=fp8)
+    packed.macs_per_position = c_out * c_in * k
+    return packed
 
 
 def pack_conv_transpose1d(weight: torch.Tensor, bias: torch.Tensor | None, *, stride: int,
@@ -124,8 +128,10 @@ def pack_conv_transpose1d(weight: torch.Tensor, bias: torch.Tensor | None, *, st
     is the HiFT upsampler (hift.py:143-156). Either way L inputs give L*s outputs."""
     c_in, c_out, k = weight.shape
     w, left = polyphase_taps(weight, stride, padding)
-    return _finish(w, bias, c_in=c_in, c_out=c_out, taps=w.shape[1], dilation=1,
-                   left_pad=left, phases=stride, fp8=fp8)
+    packed = _finish(w, bias, c_in=c_in, c_out=c_out, taps=w.shape[1], dilation=1,
+                     left_pad=left, phases=stride, fp8=fp8)
+    packed.macs_per_position = c_out * c_in * k  # every input sample meets all k taps
+    return packed
 
 
 def fused_conv(

@@ -41,6 +41,7 @@ from ..kernels.conv import PackedConv, fused_conv, pack_conv1d, pack_conv_transp
 from ..kernels.rvq import rvq_gather_sum
 from ..kernels.single_output_conv import single_output_conv
 from ..quantization import reference_weights
+from ..utils.timing import NO_TIMER
 from .configs import DacDecoderConfig
 
 
@@ -183,6 +184,8 @@ class DacCodecDecoder:
         self.final_taps = fw.shape[-1]
         self.final_channels = fw.shape[1]
         self._workspaces: dict[tuple[int, int], _Workspace] = {}
+        # a utils.timing.LaunchTimer installed here records every launch with its work
+        self.timer = NO_TIMER
 
     # ---------------------------------------------------------------- state layout / pool
 
@@ -249,13 +252,24 @@ class DacCodecDecoder:
                 "history_cold": state["cold"],
             }
 
-        rvq_gather_sum(codes, self.codebooks, out=ws.z, clamp=True)
+        timer = self.timer
+
+        def conv(x, layer: _Layer, out, **kw):
+            length = x.shape[1]
+            flops = 2.0 * batch * length * layer.conv.macs_per_position
+            with timer.launch("conv", flops, layer.name):
+                fused_conv(x, layer.conv, out, activation=N.ACT_SNAKE, act_a=layer.act_a,
+                           act_b=layer.act_b, **kw, **hist(layer.name))
+
+        k_books, _, dim = self.codebooks.shape
+        rvq_bytes = batch * frames * (k_books * dim * 2 + dim * 2 + k_books * codes.element_size())
+        with timer.launch("rvq", rvq_bytes):
+            rvq_gather_sum(codes, self.codebooks, out=ws.z, clamp=True)
         cur = 0
         length = frames
         c0 = self.in_conv.conv.n_cols
         x_act = self._view(ws.act[cur], batch, length, c0)
-        fused_conv(ws.z, self.in_conv.conv, x_act, activation=N.ACT_SNAKE,
-                   act_a=self.in_conv.act_a, act_b=self.in_conv.act_b, **hist("in_conv"))
+        conv(ws.z, self.in_conv, x_act)
         for blk in self.blocks:
             nxt = 1 - cur
             up = blk.up.conv
@@ -263,23 +277,21 @@ class DacCodecDecoder:
             # the polyphase output [B, L, s*C] is the transposed conv's [B, L*s, C]
             y = self._view(ws.act[nxt], batch, out_len, blk.c_out)
             xres = self._view(ws.xres, batch, out_len, blk.c_out)
-            fused_conv(x_act, up, y.view(batch, length, up.n_cols), activation=N.ACT_SNAKE,
-                       act_a=blk.up.act_a, act_b=blk.up.act_b,
-                       sum_out=xres.view(batch, length, up.n_cols), **hist(blk.up.name))
+            conv(x_act, blk.up, y.view(batch, length, up.n_cols),
+                 sum_out=xres.view(batch, length, up.n_cols))
             length = out_len
             h = self._view(ws.h, batch, length, blk.c_out)
             for u, unit in enumerate(blk.units):
-                fused_conv(y, unit.conv1.conv, h, activation=N.ACT_SNAKE, act_a=unit.conv1.act_a,
-                           act_b=unit.conv1.act_b, **hist(unit.conv1.name))
+                conv(y, unit.conv1, h)
                 last = u + 1 == len(blk.units)
-                fused_conv(h, unit.conv2.conv, y, activation=N.ACT_SNAKE, act_a=unit.conv2.act_a,
-                           act_b=unit.conv2.act_b, residual=xres,
-                           sum_out=None if last else xres, **hist(unit.conv2.name))
+                conv(h, unit.conv2, y, residual=xres, sum_out=None if last else xres)
             x_act = y
             cur = nxt
         wave = torch.empty(batch, 1, length, dtype=torch.float32, device=self.device)
-        single_output_conv(x_act, self.final_weight, self.final_bias, wave,
-                           activation=N.ACT_TANH, left_pad=self.final_taps - 1, **hist("final"))
+        with timer.launch("final", 2.0 * batch * length * self.final_taps * self.final_channels):
+            single_output_conv(x_act, self.final_weight, self.final_bias, wave,
+                               activation=N.ACT_TANH, left_pad=self.final_taps - 1,
+                               **hist("final"))
         if state is not None:
             lib = N.load_library()
             parity = state["pool"].parity
