@@ -1,0 +1,477 @@
+"""CPU pins of the oracle (oracle/codec_oracle.py): each oracle function is checked against
+something that fixes it independently of its own formula — a brute-force loop, the C direct-sum
+restatement (oracle/codec_oracle.c), an installed ``transformers`` module with the same
+arithmetic, a closed form or a whole-stream invariant — chosen so that a dropped term, a wrong
+sign, index or trim, or a transposed operand fails."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import codec_oracle as O
+
+REPO = Path(__file__).resolve().parents[1]
+ORACLE_LIB = REPO / "oracle" / "_build" / "libcodec_oracle.so"
+
+
+@pytest.fixture(scope="module")
+def clib() -> ctypes.CDLL:
+    if not ORACLE_LIB.exists():
+        import subprocess
+
+        subprocess.run(["make", "-s", "-C", str(REPO / "oracle")], check=True)
+    lib = ctypes.CDLL(str(ORACLE_LIB))
+    i64, p = ctypes.c_int64, ctypes.c_void_p
+    lib.oracle_rvq_gather_sum.argtypes = [p, i64, i64, i64, p, i64, i64, p, ctypes.c_int]
+    lib.oracle_conv1d_f64.argtypes = [p, i64, i64, i64, p, p, i64, i64, i64, i64, p]
+    lib.oracle_conv_transpose1d_f64.argtypes = [p, i64, i64, i64, p, p, i64, i64, i64, i64, i64, p]
+    return lib
+
+
+def _np_ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def c_conv1d(lib, x, w, b, dilation, left_pad) -> torch.Tensor:
+    x64 = np.ascontiguousarray(x.double().numpy())
+    w64 = np.ascontiguousarray(w.double().numpy())
+    b64 = None if b is None else np.ascontiguousarray(b.double().numpy())
+    batch, c_in, length = x64.shape
+    c_out, _, taps = w64.shape
+    y = np.zeros((batch, c_out, length))
+    lib.oracle_conv1d_f64(_np_ptr(x64), batch, c_in, length, _np_ptr(w64),
+                          None if b64 is None else _np_ptr(b64), c_out, taps, dilation, left_pad,
+                          _np_ptr(y))
+    return torch.from_numpy(y)
+
+
+def c_conv_transpose1d(lib, x, w, b, stride, padding, out_length) -> torch.Tensor:
+    x64 = np.ascontiguousarray(x.double().numpy())
+    w64 = np.ascontiguousarray(w.double().numpy())
+    b64 = None if b is None else np.ascontiguousarray(b.double().numpy())
+    batch, c_in, length = x64.shape
+    _, c_out, taps = w64.shape
+    y = np.zeros((batch, c_out, out_length))
+    lib.oracle_conv_transpose1d_f64(_np_ptr(x64), batch, c_in, length, _np_ptr(w64),
+                                    None if b64 is None else _np_ptr(b64), c_out, taps, stride,
+                                    padding, out_length, _np_ptr(y))
+    return torch.from_numpy(y)
+
+
+# ------------------------------------------------------------------------------------ a1 RVQ
+
+
+def test_rvq_matches_a_brute_force_loop():
+    gen = torch.Generator().manual_seed(0)
+    tables = torch.randn(3, 7, 5, generator=gen)
+    codes = torch.randint(0, 7, (2, 3, 4), generator=gen)
+    got = O.rvq_gather_sum(codes, tables)
+    for b in range(2):
+        for t in range(4):
+            for d in range(5):
+                acc = 0.0
+                for k in range(3):
+                    acc = float(np.float32(acc) + np.float32(tables[k, codes[b, k, t], d].item()))
+                assert got[b, d, t].item() == np.float32(acc)
+
+
+@pytest.mark.parametrize("clamp", [False, True])
+def test_rvq_is_bit_identical_to_the_c_restatement(clib, clamp):
+    gen = torch.Generator().manual_seed(1)
+    k, v, d, t = 8, 1024, 256, 50
+    tables = (torch.randn(k, v, d, generator=gen) * 0.02).contiguous()
+    codes = torch.randint(0, v + (40 if clamp else 0), (2, k, t), generator=gen)
+    out = np.zeros((2, d, t), dtype=np.float32)
+    codes_np = np.ascontiguousarray(codes.numpy().astype(np.int64))
+    tables_np = np.ascontiguousarray(tables.numpy())
+    clib.oracle_rvq_gather_sum(_np_ptr(codes_np), 2, k, t, _np_ptr(tables_np), v, d, _np_ptr(out),
+                               int(clamp))
+    src = O.clamp_codes(codes, v) if clamp else codes
+    assert torch.equal(O.rvq_gather_sum(src, tables), torch.from_numpy(out))
+
+
+def test_rvq_with_one_codebook_is_an_embedding_lookup():
+    gen = torch.Generator().manual_seed(2)
+    tables = torch.randn(1, 33, 12, generator=gen)
+    codes = torch.randint(0, 33, (3, 1, 9), generator=gen)
+    expected = F.embedding(codes[:, 0], tables[0]).transpose(1, 2)
+    assert torch.equal(O.rvq_gather_sum(codes, tables), expected)
+
+
+def test_rvq_mean_is_the_sum_divided_by_k_and_permutation_changes_only_rounding():
+    gen = torch.Generator().manual_seed(3)
+    tables = torch.randn(6, 20, 8, generator=gen)
+    codes = torch.randint(0, 20, (2, 6, 5), generator=gen)
+    total = O.rvq_gather_sum(codes, tables)
+    assert torch.equal(O.rvq_gather_sum(codes, tables, mean=True), total / 6)
+    perm = torch.tensor([5, 3, 1, 0, 2, 4])
+    permuted = O.rvq_gather_sum(codes[:, perm], tables[perm])
+    torch.testing.assert_close(permuted, total, rtol=1e-6, atol=1e-6)
+    # an exact float64 reference of the unordered sum
+    f64 = sum(tables[k].double()[codes[:, k]] for k in range(6)).transpose(1, 2)
+    torch.testing.assert_close(total.double(), f64, rtol=1e-6, atol=1e-6)
+
+
+def test_rvq_code_clamp_reads_the_last_entry():
+    tables = torch.arange(2 * 4 * 3, dtype=torch.float32).view(2, 4, 3)
+    codes = torch.tensor([[[0, 9], [3, 4]]])
+    got = O.rvq_gather_sum(O.clamp_codes(codes, 4), tables)
+    assert got[0, :, 1].tolist() == (tables[0, 3] + tables[1, 3]).tolist()
+
+
+# ---------------------------------------------------------------------------------- a4 Snake
+
+
+def test_snake_matches_transformers_snake1d_and_the_float64_formula():
+    from transformers.models.dac.modeling_dac import Snake1d
+
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 6, 40, generator=gen) * 3
+    alpha = torch.rand(6, generator=gen) * 2 + 0.1
+    module = Snake1d(6)
+    with torch.no_grad():
+        module.alpha.copy_(alpha.view(1, 6, 1))
+        expected = module(x)
+    got = O.snake(x, alpha)
+    assert torch.equal(got, expected)
+    a = alpha.double().view(1, 6, 1)
+    f64 = x.double() + torch.sin(a * x.double()) ** 2 / (a + 1e-9)
+    torch.testing.assert_close(got.double(), f64, rtol=1e-5, atol=1e-5)
+
+
+def test_snake_limits():
+    x = torch.linspace(-2, 2, 41).view(1, 1, -1)
+    # x = 0 is a fixed point
+    assert O.snake(torch.zeros(1, 3, 5), torch.ones(3)).abs().max().item() == 0.0
+    # alpha -> 0: sin(a x)^2 / a -> a x^2 -> 0, so y -> x (and y - x ~ a x^2)
+    a = torch.tensor([1e-4])
+    y = O.snake(x, a)
+    torch.testing.assert_close(y - x, a * x * x, rtol=1e-2, atol=1e-7)
+    # the periodic term is non-negative and at most 1/alpha
+    alpha = torch.tensor([0.5])
+    d = O.snake(x * 10, alpha) - x * 10
+    assert d.min().item() >= 0.0 and d.max().item() <= 2.0 + 1e-6
+
+
+def test_snake_beta_matches_transformers():
+    from transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe import Qwen3OmniMoeSnakeBeta
+
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 8, 30, generator=gen) * 2
+    alpha_log = torch.randn(8, generator=gen) * 0.3
+    beta_log = torch.randn(8, generator=gen) * 0.3
+    module = Qwen3OmniMoeSnakeBeta(8)
+    with torch.no_grad():
+        module.alpha.copy_(alpha_log)
+        module.beta.copy_(beta_log)
+        expected = module(x)
+    torch.testing.assert_close(O.snake_beta(x, alpha_log, beta_log), expected, rtol=1e-6,
+                               atol=1e-6)
+
+
+# ------------------------------------------------------------------------------ a2 / a3 convs
+
+
+@pytest.mark.parametrize("k,d", [(7, 1), (7, 3), (7, 9), (1, 1), (3, 2)])
+def test_causal_conv_matches_c_direct_summation(clib, k, d):
+    gen = torch.Generator().manual_seed(10 + k * d)
+    x = torch.randn(2, 5, 40, generator=gen)
+    w = torch.randn(4, 5, k, generator=gen)
+    b = torch.randn(4, generator=gen)
+    got = O.causal_conv1d(x, w, b, d)
+    expected = c_conv1d(clib, x, w, b, d, (k - 1) * d)
+    torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("k,d", [(3, 1), (7, 3), (11, 5)])
+def test_same_conv_matches_c_direct_summation(clib, k, d):
+    gen = torch.Generator().manual_seed(20 + k)
+    x = torch.randn(1, 4, 50, generator=gen)
+    w = torch.randn(3, 4, k, generator=gen)
+    got = O.same_conv1d(x, w, None, d)
+    expected = c_conv1d(clib, x, w, None, d, (k * d - d) // 2)
+    torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("stride", [2, 5, 6, 8])
+def test_causal_transposed_conv_matches_c_scatter_and_keeps_t_times_s(clib, stride):
+    gen = torch.Generator().manual_seed(30 + stride)
+    x = torch.randn(2, 6, 9, generator=gen)
+    w = torch.randn(6, 3, 2 * stride, generator=gen)
+    b = torch.randn(3, generator=gen)
+    got = O.causal_conv_transpose1d(x, w, b, stride)
+    assert got.shape[-1] == 9 * stride
+    expected = c_conv_transpose1d(clib, x, w, b, stride, 0, 9 * stride)
+    torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("rate,k", [(8, 16), (5, 11), (3, 7), (4, 8)])
+def test_padded_transposed_conv_matches_c_scatter(clib, rate, k):
+    gen = torch.Generator().manual_seed(40 + k)
+    x = torch.randn(1, 4, 7, generator=gen)
+    w = torch.randn(4, 2, k, generator=gen)
+    got = O.padded_conv_transpose1d(x, w, None, rate)
+    assert got.shape[-1] == 7 * rate
+    expected = c_conv_transpose1d(clib, x, w, None, rate, (k - rate) // 2, 7 * rate)
+    torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-5)
+
+
+def test_causal_transposed_conv_is_the_qwen3_both_sides_trim_shifted_by_s():
+    from transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe import (
+        Qwen3OmniMoeCausalTransConvNet,
+    )
+
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(1, 4, 10, generator=gen)
+    module = Qwen3OmniMoeCausalTransConvNet(4, 3, 10, 5)
+    with torch.no_grad():
+        q = module(x)
+        ours = O.causal_conv_transpose1d(x, module.conv.weight, module.conv.bias, 5)
+    torch.testing.assert_close(ours[..., 5:], q)
+
+
+# -------------------------------------------------------------------------- a5 composition
+
+
+def _unit(gen, c, dilation) -> dict:
+    return {
+        "dilation": dilation,
+        "alpha1": torch.rand(c, generator=gen) + 0.5,
+        "conv1": {"weight": torch.randn(c, c, 7, generator=gen) * 0.2,
+                  "bias": torch.randn(c, generator=gen) * 0.1},
+        "alpha2": torch.rand(c, generator=gen) + 0.5,
+        "conv2": {"weight": torch.randn(c, c, 1, generator=gen) * 0.2,
+                  "bias": torch.randn(c, generator=gen) * 0.1},
+    }
+
+
+def _load_qwen3_unit(module, unit):
+    # SnakeBeta with alpha = beta = log(a) is Snake1d(a): exp(log a) = a up to rounding
+    with torch.no_grad():
+        module.act1.alpha.copy_(unit["alpha1"].log())
+        module.act1.beta.copy_(unit["alpha1"].log())
+        module.act2.alpha.copy_(unit["alpha2"].log())
+        module.act2.beta.copy_(unit["alpha2"].log())
+        module.conv1.conv.weight.copy_(unit["conv1"]["weight"])
+        module.conv1.conv.bias.copy_(unit["conv1"]["bias"])
+        module.conv2.conv.weight.copy_(unit["conv2"]["weight"])
+        module.conv2.conv.bias.copy_(unit["conv2"]["bias"])
+
+
+@pytest.mark.parametrize("dilation", [1, 3, 9])
+def test_residual_unit_matches_the_causal_qwen3_residual_unit(dilation):
+    from transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe import (
+        Qwen3OmniMoeCode2WavDecoderResidualUnit,
+    )
+
+    gen = torch.Generator().manual_seed(50 + dilation)
+    unit = _unit(gen, 6, dilation)
+    module = Qwen3OmniMoeCode2WavDecoderResidualUnit(6, dilation)
+    _load_qwen3_unit(module, unit)
+    x = torch.randn(2, 6, 37, generator=gen)
+    with torch.no_grad():
+        expected = module(x)
+    torch.testing.assert_close(O.residual_unit(x, unit), expected, rtol=1e-5, atol=1e-5)
+
+
+def test_the_residual_unit_pin_rejects_the_conv_before_snake_order():
+    # a plausible transposition (conv -> Snake instead of Snake -> conv) fails the pin above
+    from transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe import (
+        Qwen3OmniMoeCode2WavDecoderResidualUnit,
+    )
+
+    gen = torch.Generator().manual_seed(60)
+    unit = _unit(gen, 4, 1)
+    module = Qwen3OmniMoeCode2WavDecoderResidualUnit(4, 1)
+    _load_qwen3_unit(module, unit)
+    x = torch.randn(1, 4, 20, generator=gen)
+    with torch.no_grad():
+        expected = module(x)
+    swapped = x + O.snake(O.causal_conv1d(O.snake(O.causal_conv1d(
+        x, unit["conv1"]["weight"], unit["conv1"]["bias"]), unit["alpha1"]),
+        unit["conv2"]["weight"], unit["conv2"]["bias"]), unit["alpha2"])
+    assert not torch.allclose(swapped, expected, atol=1e-3)
+
+
+def test_decoder_block_matches_the_qwen3_block_up_to_the_trim():
+    from transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe import (
+        Qwen3OmniMoeCode2WavConfig,
+        Qwen3OmniMoeCode2WavDecoderBlock,
+    )
+
+    gen = torch.Generator().manual_seed(70)
+    cfg = Qwen3OmniMoeCode2WavConfig(decoder_dim=16, upsample_rates=[4], hidden_size=16,
+                                     codebook_size=8, num_quantizers=2)
+    module = Qwen3OmniMoeCode2WavDecoderBlock(cfg, 0).eval()
+    c_in, c_out, s = 16, 8, 4
+    block = {
+        "stride": s,
+        "alpha": torch.rand(c_in, generator=gen) + 0.5,
+        "up": {"weight": torch.randn(c_in, c_out, 2 * s, generator=gen) * 0.2,
+               "bias": torch.randn(c_out, generator=gen) * 0.1},
+        "units": [_unit(gen, c_out, d) for d in (1, 3, 9)],
+    }
+    with torch.no_grad():
+        module.block[0].alpha.copy_(block["alpha"].log())
+        module.block[0].beta.copy_(block["alpha"].log())
+        module.block[1].conv.weight.copy_(block["up"]["weight"])
+        module.block[1].conv.bias.copy_(block["up"]["bias"])
+        for i, unit in enumerate(block["units"]):
+            _load_qwen3_unit(module.block[2 + i], unit)
+    x = torch.randn(1, c_in, 12, generator=gen)
+    with torch.no_grad():
+        q = module(x)
+    ours = O.decoder_block(x, block)
+    assert ours.shape[-1] == 12 * s and q.shape[-1] == 11 * s
+    # Qwen3 trims k - s samples on both sides of the transposed conv, the causal DAC block only on
+    # the right, so the Qwen3 block is the same residual units run on the DAC upsampler's output
+    # from sample s on.
+    up = O.causal_conv_transpose1d(O.snake(x, block["alpha"]), block["up"]["weight"],
+                                   block["up"]["bias"], s)
+
+    def units(y):
+        for unit in block["units"]:
+            y = O.residual_unit(y, unit)
+        return y
+
+    torch.testing.assert_close(units(up[..., s:]), q, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(ours, units(up))
+
+
+def test_hifigan_generator_matches_transformers_speecht5_hifigan():
+    from transformers import SpeechT5HifiGan, SpeechT5HifiGanConfig
+
+    cfg = SpeechT5HifiGanConfig(model_in_dim=10, upsample_initial_channel=16,
+                                upsample_rates=[2, 3], upsample_kernel_sizes=[4, 7],
+                                resblock_kernel_sizes=[3, 7, 11],
+                                resblock_dilation_sizes=[[1, 3, 5]] * 3, leaky_relu_slope=0.1,
+                                normalize_before=False)
+    torch.manual_seed(0)
+    module = SpeechT5HifiGan(cfg).eval()
+    with torch.no_grad():
+        for p in module.parameters():
+            p.normal_(0, 0.2)
+    weights = {
+        "slope": 0.1,
+        "final_slope": 0.01,
+        "conv_pre": {"weight": module.conv_pre.weight, "bias": module.conv_pre.bias},
+        "stages": [],
+        "conv_post": {"weight": module.conv_post.weight, "bias": module.conv_post.bias},
+    }
+    for i, (rate, up) in enumerate(zip(cfg.upsample_rates, module.upsampler)):
+        stage = {"rate": rate, "up": {"weight": up.weight, "bias": up.bias}, "resblocks": []}
+        for j in range(3):
+            rb = module.resblocks[i * 3 + j]
+            stage["resblocks"].append({
+                "dilations": (1, 3, 5),
+                "convs1": [{"weight": c.weight, "bias": c.bias} for c in rb.convs1],
+                "convs2": [{"weight": c.weight, "bias": c.bias} for c in rb.convs2],
+            })
+        weights["stages"].append(stage)
+    mel = torch.randn(2, 13, 10)
+    with torch.no_grad():
+        expected = module(mel)  # [B, T * 6]
+        got = O.hifigan_generator(mel.transpose(1, 2), weights)
+    torch.testing.assert_close(got[:, 0], expected, rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------------------- a6 final conv
+
+
+def test_clamped_single_output_conv_is_the_float64_conv_clamped(clib):
+    gen = torch.Generator().manual_seed(80)
+    padded = torch.randn(2, 30 + 6, 8, generator=gen)
+    w = torch.randn(1, 8, 7, generator=gen)
+    b = torch.randn(1, generator=gen)
+    got = O.clamped_single_output_conv(padded, w, b, 30)
+    direct = c_conv1d(clib, padded.transpose(1, 2), w, b, 1, 0)[..., :30]
+    assert torch.equal(got, direct.clamp(-1, 1))
+    assert got.abs().max().item() <= 1.0
+
+
+# ------------------------------------------------------------------------- a7 streaming
+
+
+@pytest.mark.parametrize("splits", [(5, 7, 9), (1,) * 12 + (9,), (21,)])
+@pytest.mark.parametrize("history", [6, 18, 54])
+def test_history_exchange_reference_builds_the_whole_stream_causal_window(splits, history):
+    gen = torch.Generator().manual_seed(90 + history)
+    stream = torch.randn(2, sum(splits), 3, generator=gen)
+    pool = torch.zeros(4, history, 3)
+    slot = torch.tensor([2, 0])
+    whole = F.pad(stream, (0, 0, history, 0))
+    pos = 0
+    for i, n in enumerate(splits):
+        padded = torch.full((2, history + n + 2, 3), float("nan"))
+        padded[:, history:history + n] = stream[:, pos:pos + n]
+        O.history_exchange_reference(padded, pool, slot, n, i == 0)
+        assert torch.equal(padded[:, :history + n], whole[:, pos:pos + history + n])
+        assert torch.equal(padded[:, history + n:], torch.zeros(2, 2, 3))
+        pos += n
+
+
+@pytest.mark.parametrize("stride", [2, 5, 8])
+def test_streamed_transposed_conv_with_overlap_reference_equals_whole(stride):
+    gen = torch.Generator().manual_seed(100 + stride)
+    k = 2 * stride
+    x = torch.randn(1, 4, 17, generator=gen)
+    w = torch.randn(4, 3, k, generator=gen)
+    whole = F.conv_transpose1d(x, w, stride=stride)  # (T-1)s + k samples
+    pool = torch.zeros(2, k - stride, 3)
+    slot = torch.tensor([1])
+    outs = []
+    pos = 0
+    for i, n in enumerate((4, 1, 7, 5)):
+        full = F.conv_transpose1d(x[..., pos:pos + n], w, stride=stride)  # [1, 3, (n+1)s]
+        chunk = full.transpose(1, 2).contiguous()
+        O.overlap_exchange_reference(chunk, pool, slot, n * stride, i == 0)
+        outs.append(chunk[:, :n * stride])
+        pos += n
+    streamed = torch.cat(outs, dim=1).transpose(1, 2)
+    torch.testing.assert_close(streamed, whole[..., :17 * stride], rtol=1e-5, atol=1e-5)
+
+
+def test_decoder_split_decodes_equal_the_whole_decode():
+    """Causality of the oracle decoder: output sample i depends only on frames <= i / hop."""
+    from sglang_omni_amd.models.configs import DacDecoderConfig, make_dac_weights
+
+    cfg = DacDecoderConfig(n_codebooks=2, codebook_size=16, latent_dim=16, channels=32,
+                           rates=(2, 3))
+    weights = make_dac_weights(cfg, seed=1)
+    codes = torch.randint(0, 16, (1, 2, 10), generator=torch.Generator().manual_seed(3))
+    whole = O.dac_from_indices(codes, weights)
+    prefix = O.dac_from_indices(codes[..., :6], weights)
+    torch.testing.assert_close(whole[..., :6 * cfg.hop_length], prefix, rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------------------------- a8 fp8
+
+
+def test_fp8_per_channel_quantization():
+    gen = torch.Generator().manual_seed(110)
+    w = torch.randn(6, 5, 7, generator=gen) * torch.logspace(-3, 0, 6).view(6, 1, 1)
+    q, s = O.quantize_fp8_per_channel(w)
+    assert q.dtype == torch.float8_e4m3fn and s.shape == (6,)
+    # each channel's largest magnitude maps to 448 exactly
+    assert torch.equal(q.float().reshape(6, -1).abs().amax(1), torch.full((6,), 448.0))
+    deq = O.dequantize_fp8_per_channel(q, s)
+    # e4m3 keeps 3 mantissa bits: relative error <= 2^-4 for normal values
+    rel = ((deq - w).abs() / w.abs().clamp_min(1e-30))
+    normal = w.abs() >= s.view(6, 1, 1) * 2.0 ** -6
+    assert rel[normal].max().item() <= 2.0 ** -4 + 1e-7
+    assert torch.equal(O.dequantize_fp8_per_channel(*O.quantize_fp8_per_channel(deq)), deq)
+
+
+def test_snr_db():
+    ref = torch.ones(100)
+    assert O.snr_db(ref, ref) == math.inf
+    # noise at 1 % of the signal amplitude is 40 dB (1.01 is inexact in float32)
+    assert abs(O.snr_db(ref, ref * 1.01) - 40.0) < 1e-4
+    assert abs(O.snr_db(ref, ref * 1.1) - 20.0) < 1e-4
