@@ -85,7 +85,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void);
+int omni_codec_abi_version(void); /* 2: omni_conv_args with input activation and fused k=1 conv */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -106,40 +106,63 @@ int omni_rvq_gather_sum(const void* codes, int codes_dtype, int64_t batch, int64
                         int flags, omni_stream_t stream);
 
 /*
- * One fused convolution over channels-last bf16 activations, on bf16 MFMA:
+ * One fused convolution over channels-last activations, on bf16 MFMA:
  *
- *   acc[b, i, n] = sum_{j < taps} sum_{ci < c_in} W[n, j, ci] * x[b, i + j * dilation - left_pad, ci]
- *   v = acc * weight_scale[n] (fp8 weights only) + bias[n % c_out] (+ residual[b, i, n])
+ *   u[b, p, ci] = in_act(x[b, p, ci])   rounded to bf16 (x bf16 or float32; in_act is applied
+ *                                       to x only, never to history or padding, which are zero
+ *                                       or already activated)
+ *   acc[b, i, n] = sum_{j < taps} sum_{ci < c_in} W[n, j, ci] * u[b, i + j * dilation - left_pad, ci]
+ *   v = acc * weight_scale[n] (fp8 weights only) + bias[n % c_out]
+ *   with weight2 (a second, k = 1 conv fused behind the first; needs n_cols == c_out, and the
+ *   second conv maps c_out -> c_out channels):
+ *     h[b, i, n] = mid_act(v) rounded to bf16
+ *     v = (sum_{n'} W2[n, n'] * h[b, i, n']) * weight2_scale[n] (fp8 only) + bias2[n]
+ *   v = v (+ residual[b, i, n])
  *   v = ((mix_a[b, i, n] + mix_b[b, i, n]) + v) * mix_scale      (optional, mix_a != NULL)
  *   sum_out[b, i, n] = v            (float32, optional)
  *   out[b, i, n] = act(v)           (bf16 or float32; optional when sum_out is given)
  *
- * for i < length and n < n_cols. x holds x_length positions (x_length = 0 means length); the
- * residual, mix and sum_out tensors share the residual strides. A causal Conv1d is taps = k, left_pad = (k-1)*d; a
- * ConvTranspose1d of stride s is its polyphase form (n = phase * c_out + co, so out viewed as
- * [B, length * s, c_out] is the transposed conv's output), see the packing helpers of the host
- * layer. Inputs left of position 0 come from the slot history (below) or are zero; inputs at or
- * past x_length are zero.
+ * for i < length and n < n_cols. x holds x_length positions per row (x_length = 0 means length);
+ * the residual, mix and sum_out tensors share the residual strides; sum_out may alias residual
+ * (each element is read before it is written by the same thread) but no output may alias x. A
+ * causal Conv1d is taps = k, left_pad = (k-1)*d; a ConvTranspose1d of stride s is its polyphase
+ * form (n = phase * c_out + co, so out viewed as [B, length * s, c_out] is the transposed conv's
+ * output), see the packing helpers of the host layer. Inputs left of position 0 come from the
+ * slot history (below) or are zero; inputs at or past x_length are zero. The batch rows are one
+ * position space for tiling, so short rows (streaming chunks) share weight tiles.
  *
  * weight: packed [ceil(c_in/32)][n_cols][taps][32] (ci = 32 * chunk + lane, zero past c_in),
- * bf16, or fp8-e4m3 with weight_scale[n_cols] float32.
+ * bf16, or fp8-e4m3 with weight_scale[n_cols] float32; weight2 the same layout with taps = 1 and
+ * c_in = n_cols = c_out, in the same dtype (weight2_scale for fp8).
  *
  * Streaming history (hist_pool != NULL; requires left_pad == (taps-1)*dilation): the pool is
- * bf16 [slots][2][left_pad][c_in]; row b reads the copy (slot_parity[s] & 1) of slot
- * s = slot_index[b] (zeros instead when history_cold) as positions -left_pad .. -1, and writes the
- * last left_pad samples of (history ++ x) to the other copy. omni_advance_slots flips the parity
- * once every conv of a decode step has run.
+ * bf16 [slots][2][left_pad][c_in] of activated inputs u; row b reads the copy
+ * (slot_parity[s] & 1) of slot s = slot_index[b] (zeros instead when history_cold) as positions
+ * -left_pad .. -1, and writes the last left_pad samples of (history ++ u) to the other copy.
+ * omni_advance_slots flips the parity once every conv of a decode step has run.
  */
 typedef struct omni_conv_args {
   const void* x;
+  int x_dtype; /* OMNI_DTYPE_BF16 or OMNI_DTYPE_F32 */
   int64_t x_stride_b, x_stride_t;
   int64_t batch, length, c_in;
   int64_t x_length;
+  int in_activation; /* OMNI_ACTIVATION_NONE, _SNAKE or _LEAKY_RELU, per input channel */
+  const float* in_act_a;
+  const float* in_act_b;
+  float in_act_slope;
   const void* weight;
   int weight_dtype;
   const float* weight_scale;
   int64_t n_cols, c_out, taps, dilation, left_pad;
   const float* bias;
+  const void* weight2; /* optional fused k = 1 conv */
+  const float* weight2_scale;
+  const float* bias2;
+  int mid_activation;
+  const float* mid_act_a;
+  const float* mid_act_b;
+  float mid_act_slope;
   const void* hist_pool;
   const int64_t* slot_index;
   const int64_t* slot_parity;
@@ -166,17 +189,22 @@ int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
 
 /*
  * Conv from channels-last activations to one output channel, stride 1, undilated:
- *   out[b, i] = act(bias + sum_{j < taps} sum_c weight[j * channels + c] * x[b, i + j - left_pad, c])
+ *   u = in_act(x) (OMNI_ACTIVATION_NONE or _SNAKE with per-channel in_act_a / in_act_b)
+ *   out[b, i] = act(bias + sum_{j < taps} sum_c weight[j * channels + c] * u[b, i + j - left_pad, c])
  * accumulated in float32 in one fixed order per position (so any split of positions or rows gives
  * identical bits) and rounded once. x points at position 0 and holds `length` positions (later
  * ones read as zero); when context_in_buffer is set, the left_pad positions before it are valid
  * memory (the reference's padded input); otherwise they come from the slot history (bf16 pool
- * [slots][2][taps-1][channels], same parity rule as omni_conv1d_fused; needs left_pad = taps-1)
- * or are zero. activation is OMNI_ACTIVATION_TANH or _CLAMP or _NONE.
- * x dtype bf16, f16 or f32; out [B, 1, length] at b * out_stride_b + i, dtype of out_dtype.
+ * [slots][2][taps-1][channels] of activated inputs, same parity rule as omni_conv1d_fused; needs
+ * left_pad = taps-1) or are zero. With an input activation or a history the activated inputs are
+ * rounded to bf16 (the decoder's operands and its history); otherwise they are used exactly.
+ * activation is OMNI_ACTIVATION_TANH or _CLAMP or _NONE. x dtype bf16, f16 or f32, channels a
+ * multiple of 4 (of 8 with an activation or history); out [B, 1, length] at b * out_stride_b + i,
+ * dtype of out_dtype.
  */
 int omni_single_output_conv(const void* x, int x_dtype, int64_t x_stride_b, int64_t x_stride_t,
                             int64_t batch, int64_t length, int64_t channels, int context_in_buffer,
+                            int in_activation, const float* in_act_a, const float* in_act_b,
                             const float* weight, const float* bias, int64_t taps, int64_t left_pad,
                             const void* hist_pool, const int64_t* slot_index,
                             const int64_t* slot_parity, int64_t hist_num_slots,

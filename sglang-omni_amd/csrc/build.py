@@ -23,8 +23,9 @@ OBJ_DIR = PKG_ROOT / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["capi.hip", "rvq.hip", "conv.hip", "single_output_conv.hip", "codec_state.hip",
-           "snake.hip"]
+SOURCES = ["capi.hip", "rvq.hip", "conv.hip", "conv_k7_raw_wbf16.hip", "conv_k7_raw_wfp8.hip",
+           "conv_k7_act_wbf16.hip", "conv_k7_act_wfp8.hip", "conv_k11.hip", "conv_ru_wbf16.hip",
+           "conv_ru_wfp8.hip", "single_output_conv.hip", "codec_state.hip", "snake.hip"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -52,7 +53,7 @@ def _compile(src: str) -> Path:
 def build(verbose: bool = False) -> Path:
     """Compile every source for gfx950 and link the shared library; returns its path."""
     OBJ_DIR.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as pool:
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4, 16)) as pool:
         objs = list(pool.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]

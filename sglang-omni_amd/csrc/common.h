@@ -9,9 +9,21 @@
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16;
 
 #define OMNI_DEVICE __device__ __forceinline__
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer access (CDNA buffer resources): a load at an offset outside [0, bytes) returns zeros
+// and a store there is dropped, so padding, masked rows and tails need no branches around memory
+// instructions (a branch per access would also serialize their completion waits).
+constexpr uint32_t kOutOfRange = 0x80000000u;  // every buffer here is smaller than 2 GiB
+OMNI_DEVICE __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
 
 // Round-to-nearest-even float -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
 OMNI_DEVICE __bf16 to_bf16(float x) { return (__bf16)x; }
@@ -54,6 +66,20 @@ enum {
   OMNI_ACT_CLAMP = 4,       // clamp(x, -1, 1), NaN propagated
 };
 
+// tanh is out of line: inlined at every activation site of an unrolled tile it would multiply
+// the kernel's code size, and only the decoder's last layer uses it.
+__device__ __noinline__ float act_tanh(float v) { return tanhf(v); }
+
+// The activations applied to conv operands (staging, between fused convs): cheap and inline.
+OMNI_DEVICE float operand_act(int act, float v, float a, float b, float slope) {
+  if (act == OMNI_ACT_SNAKE) {
+    const float s = snake_sin(a * v);
+    return v + b * (s * s);
+  }
+  if (act == OMNI_ACT_LEAKY_RELU) return v >= 0.f ? v : v * slope;
+  return v;
+}
+
 OMNI_DEVICE float apply_act(int act, float v, float a, float b, float slope) {
   switch (act) {
     case OMNI_ACT_SNAKE: {
@@ -63,7 +89,7 @@ OMNI_DEVICE float apply_act(int act, float v, float a, float b, float slope) {
     case OMNI_ACT_LEAKY_RELU:
       return v >= 0.f ? v : v * slope;
     case OMNI_ACT_TANH:
-      return tanhf(v);
+      return act_tanh(v);
     case OMNI_ACT_CLAMP:
       return v != v ? v : fminf(fmaxf(v, -1.f), 1.f);
     default:

@@ -30,7 +30,15 @@ TORCH_TO_OMNI = {
 
 
 class OmniCodecError(RuntimeError):
-    """A nonzero status from the native library."""
+    """A nonzero status from the native library (``status``; 0 when the error is raised on the
+    host before any call)."""
+
+    def __init__(self, message: str, status: int = 0):
+        super().__init__(message)
+        self.status = status
+
+
+UNSUPPORTED = 2
 
 
 class ConvArgs(ctypes.Structure):
@@ -38,12 +46,17 @@ class ConvArgs(ctypes.Structure):
 
     _fields_ = [
         ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int),
         ("x_stride_b", ctypes.c_int64),
         ("x_stride_t", ctypes.c_int64),
         ("batch", ctypes.c_int64),
         ("length", ctypes.c_int64),
         ("c_in", ctypes.c_int64),
         ("x_length", ctypes.c_int64),
+        ("in_activation", ctypes.c_int),
+        ("in_act_a", ctypes.c_void_p),
+        ("in_act_b", ctypes.c_void_p),
+        ("in_act_slope", ctypes.c_float),
         ("weight", ctypes.c_void_p),
         ("weight_dtype", ctypes.c_int),
         ("weight_scale", ctypes.c_void_p),
@@ -53,6 +66,13 @@ class ConvArgs(ctypes.Structure):
         ("dilation", ctypes.c_int64),
         ("left_pad", ctypes.c_int64),
         ("bias", ctypes.c_void_p),
+        ("weight2", ctypes.c_void_p),
+        ("weight2_scale", ctypes.c_void_p),
+        ("bias2", ctypes.c_void_p),
+        ("mid_activation", ctypes.c_int),
+        ("mid_act_a", ctypes.c_void_p),
+        ("mid_act_b", ctypes.c_void_p),
+        ("mid_act_slope", ctypes.c_float),
         ("hist_pool", ctypes.c_void_p),
         ("slot_index", ctypes.c_void_p),
         ("slot_parity", ctypes.c_void_p),
@@ -90,9 +110,9 @@ SIGNATURES: dict[str, list] = {
     "omni_rvq_gather_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _INT, _I64, _I64,
                             _PTR, _INT, _I64, _I64, _I64, _INT, _PTR],
     "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
-    "omni_single_output_conv": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _PTR, _PTR, _I64,
-                                _I64, _PTR, _PTR, _PTR, _I64, _I64, _INT, _INT, _PTR, _INT, _I64,
-                                _PTR],
+    "omni_single_output_conv": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _PTR, _PTR,
+                                _PTR, _PTR, _I64, _I64, _PTR, _PTR, _PTR, _I64, _I64, _INT, _INT,
+                                _PTR, _INT, _I64, _PTR],
     "omni_history_exchange": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _I64, _I64,
                               _I64, _I64, _I64, _PTR, _I64, _INT, _PTR],
     "omni_overlap_exchange": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _PTR, _I64, _I64, _I64,
@@ -129,7 +149,7 @@ def load_library(path: Path | str = LIB_PATH) -> ctypes.CDLL:
 def check(status: int, what: str) -> None:
     if status != OK:
         msg = load_library().omni_codec_error_string(status).decode()
-        raise OmniCodecError(f"{what}: status {status} ({msg})")
+        raise OmniCodecError(f"{what}: status {status} ({msg})", status)
 
 
 def require_device(*tensors: torch.Tensor) -> None:

@@ -141,6 +141,15 @@ def fused_conv(
     *,
     length: int | None = None,
     x_length: int | None = None,
+    in_activation: int = N.ACT_NONE,
+    in_a: torch.Tensor | None = None,
+    in_b: torch.Tensor | None = None,
+    in_slope: float = 0.0,
+    second: PackedConv | None = None,
+    mid_activation: int = N.ACT_NONE,
+    mid_a: torch.Tensor | None = None,
+    mid_b: torch.Tensor | None = None,
+    mid_slope: float = 0.0,
     activation: int = N.ACT_NONE,
     act_a: torch.Tensor | None = None,
     act_b: torch.Tensor | None = None,
@@ -155,7 +164,9 @@ def fused_conv(
 ) -> torch.Tensor:
     """Launch ``omni_conv1d_fused`` on the current stream.
 
-    x [B, >=x_length, C_in] bf16 (rows may sit in longer buffers; channel stride 1);
+    x [B, >=x_length, C_in] bf16 or float32 (rows may sit in longer buffers; channel stride 1),
+    activated per input channel by ``in_activation`` while it is staged; ``second`` is a k = 1
+    conv (C_out -> C_out) fused behind this one with ``mid_activation`` between them;
     out [B, length, n_cols] bf16 or float32; residual / sum_out / mix tensors float32 with out's
     logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16.
     """
@@ -167,17 +178,23 @@ def fused_conv(
         length = x.shape[1]
     if x_length is None:
         x_length = x.shape[1] if history is None else length
-    if x.dtype != torch.bfloat16 or x.stride(2) != 1:
-        raise ValueError("x must be bf16 with channel stride 1")
+    if x.dtype not in (torch.bfloat16, torch.float32) or x.stride(2) != 1:
+        raise ValueError("x must be bf16 or float32 with channel stride 1")
     if x.shape[2] != conv.c_in:
         raise ValueError(f"x has {x.shape[2]} channels, the conv takes {conv.c_in}")
+    if second is not None and (second.c_in != conv.c_out or second.taps != 1
+                               or conv.n_cols != conv.c_out or second.weight.dtype != conv.weight.dtype):
+        raise ValueError("the fused second conv is a k = 1 conv over the first one's channels")
+    n_cols = conv.n_cols if second is None else second.n_cols
     for t in (out, sum_out):
         if t is None:
             continue
-        if t.dim() != 3 or t.shape[0] != batch or t.shape[2] != conv.n_cols or t.stride(2) != 1:
-            raise ValueError(f"outputs must be [B, {length}, {conv.n_cols}] with channel stride 1")
+        if t.dim() != 3 or t.shape[0] != batch or t.shape[2] != n_cols or t.stride(2) != 1:
+            raise ValueError(f"outputs must be [B, {length}, {n_cols}] with channel stride 1")
         if t.shape[1] < length:
             raise ValueError("an output holds fewer positions than length")
+        if t.data_ptr() == x.data_ptr():
+            raise ValueError("an output may not alias x")
     aux = [t for t in (residual, sum_out) if t is not None]
     if mix is not None:
         aux += [mix[0], mix[1]]
@@ -187,12 +204,17 @@ def fused_conv(
     r_strides = aux[0].stride() if aux else (0, 0, 1)
     args = N.ConvArgs()
     args.x = x.data_ptr()
+    args.x_dtype = N.omni_dtype(x.dtype)
     args.x_stride_b = x.stride(0)
     args.x_stride_t = x.stride(1)
     args.batch = batch
     args.length = length
     args.c_in = conv.c_in
     args.x_length = x_length
+    args.in_activation = in_activation
+    args.in_act_a = N.ptr(in_a)
+    args.in_act_b = N.ptr(in_b)
+    args.in_act_slope = in_slope
     args.weight = conv.weight.data_ptr()
     args.weight_dtype = N.omni_dtype(conv.weight.dtype)
     args.weight_scale = N.ptr(conv.scale)
@@ -202,6 +224,14 @@ def fused_conv(
     args.dilation = conv.dilation
     args.left_pad = conv.left_pad
     args.bias = N.ptr(conv.bias)
+    if second is not None:
+        args.weight2 = second.weight.data_ptr()
+        args.weight2_scale = N.ptr(second.scale)
+        args.bias2 = N.ptr(second.bias)
+        args.mid_activation = mid_activation
+        args.mid_act_a = N.ptr(mid_a)
+        args.mid_act_b = N.ptr(mid_b)
+        args.mid_act_slope = mid_slope
     if history is not None:
         if slot_index is None or slot_parity is None:
             raise ValueError("a history pool needs slot_index and slot_parity")

@@ -34,7 +34,8 @@ def clamped_single_output_conv(
     N.check(
         lib.omni_single_output_conv(
             context.data_ptr(), N.omni_dtype(padded.dtype), padded.stride(0), padded.stride(1),
-            batch_size, length, channels, 1, weight.data_ptr(), N.ptr(bias), taps, taps - 1,
+            batch_size, length, channels, 1, N.ACT_NONE, None, None, weight.data_ptr(),
+            N.ptr(bias), taps, taps - 1,
             None, None, None, 0, 0, 0, act, output.data_ptr(), N.omni_dtype(output.dtype),
             output.stride(0), N.stream_handle(padded.device),
         ),
@@ -51,13 +52,17 @@ def single_output_conv(
     *,
     activation: int,
     left_pad: int,
+    in_activation: int = N.ACT_NONE,
+    in_a: torch.Tensor | None = None,
+    in_b: torch.Tensor | None = None,
     history: torch.Tensor | None = None,
     slot_index: torch.Tensor | None = None,
     slot_parity: torch.Tensor | None = None,
     history_cold: bool = False,
 ) -> torch.Tensor:
     """Decoder form: x [B, L, C] (no context in the buffer; zeros or slot history left of 0,
-    zeros right of L), weight [taps, C] float32, out [B, 1, L]."""
+    zeros right of L), activated per channel by ``in_activation`` (Snake with in_a / in_b),
+    weight [taps, C] float32, out [B, 1, L]."""
     N.require_device(x, out)
     batch, length, channels = x.shape
     taps = weight.shape[0]
@@ -65,7 +70,8 @@ def single_output_conv(
     N.check(
         lib.omni_single_output_conv(
             x.data_ptr(), N.omni_dtype(x.dtype), x.stride(0), x.stride(1), batch, length,
-            channels, 0, weight.data_ptr(), N.ptr(bias), taps, left_pad, N.ptr(history),
+            channels, 0, in_activation, N.ptr(in_a), N.ptr(in_b), weight.data_ptr(), N.ptr(bias),
+            taps, left_pad, N.ptr(history),
             N.ptr(slot_index), N.ptr(slot_parity), 0 if history is None else history.shape[0],
             0 if history is None else history.stride(0),
             int(history_cold), activation, out.data_ptr(), N.omni_dtype(out.dtype),

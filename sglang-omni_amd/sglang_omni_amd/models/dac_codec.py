@@ -10,23 +10,27 @@ slot_index, first_decode=...)``) with a ``CodecStatePool``-shaped state pool
 The decoder follows ``Decoder`` / ``DecoderBlock`` / ``ResidualUnit`` / ``CausalConvNet`` /
 ``CausalTransConvNet`` of sglang_omni/models/fishaudio_s2_pro/fish_speech/models/dac/
 modded_dac.py:541-835 fed by the RVQ gather-sum (rvq.py:374-388). Every op runs in a HIP kernel,
-on channels-last activations, one launch per conv:
+on channels-last activations. The residual stream x stays float32 in HBM; every producer also
+writes the next conv's operand u = Snake(x) as bf16 in its epilogue, so each conv reads a ready
+bf16 operand:
 
     rvq_gather_sum                       codes -> z (bf16)
-    conv k7 (512 -> C0)                  epilogue: bias, Snake(block 0) -> bf16
+    conv k7 (512 -> C0)                  z -> u = Snake(block 0)(x) (bf16)
     per block:
-      polyphase ConvTranspose (k = 2s)   epilogue: bias -> x (float32 residual stream),
-                                                   Snake(unit 0, act1) -> bf16
+      polyphase ConvTranspose (k = 2s)   u -> x (float32), u = Snake(unit 0 act1)(x)
       per residual unit (d = 1, 3, 9):
-        conv k7 dilation d               epilogue: bias, Snake(act2) -> bf16
-        conv k1                          epilogue: bias + x -> x (float32),
-                                                   Snake(next act) -> bf16
-    conv to one channel k7               tanh -> float32 waveform
+        96 / 192 channels: one launch    conv k7 dilation d; bias + Snake(act2) -> bf16 tile in
+                                         LDS; conv k1; bias + x -> x (float32, in place),
+                                         u' = Snake(next)(x) (bf16)
+        wider:             two launches  conv k7; bias + Snake(act2) -> h (bf16)
+                                         conv k1 of h; bias + x -> x (in place), u' = Snake(next)(x)
+    conv to one channel k7               u = Snake(final)(x); tanh -> float32 waveform
 
-Streaming keeps each causal conv's left context (its last (k-1)*d input samples) per slot in HBM;
-the conv kernels read it in place of zeros and write the new context themselves, double-buffered
-by a per-slot parity that ``omni_advance_slots`` flips at the end of the step. A transposed conv
-with k = 2s needs one input sample of context, which is exactly the reference's overlap-add.
+Streaming keeps each causal conv's left context (its last (k-1)*d activated input samples) per
+slot in HBM; the conv kernels read it in place of zeros and write the new context themselves,
+double-buffered by a per-slot parity that ``omni_advance_slots`` flips at the end of the step. A
+transposed conv with k = 2s needs one input sample of context, which is exactly the reference's
+overlap-add.
 """
 
 from __future__ import annotations
@@ -49,22 +53,31 @@ from .configs import DacDecoderConfig
 class _Layer:
     name: str
     conv: PackedConv
-    act_a: torch.Tensor | None = None  # Snake a (alpha) of the activation applied in the epilogue
-    act_b: torch.Tensor | None = None  # Snake b (1 / (alpha + 1e-9))
+    out_a: torch.Tensor | None = None  # Snake a (alpha) of the operand the epilogue writes
+    out_b: torch.Tensor | None = None  # Snake b (1 / (alpha + 1e-9))
 
 
 @dataclass
 class _Unit:
-    conv1: _Layer  # k = 7, dilation d; epilogue Snake(act2)
-    conv2: _Layer  # k = 1; epilogue + residual, Snake(next act)
+    conv1: _Layer  # k = 7, dilation d; its output gets Snake(act2)
+    conv2: PackedConv  # k = 1; its output (the new x) gets Snake(next)
+    mid_a: torch.Tensor  # Snake(act2) between the two convs
+    mid_b: torch.Tensor
+    next_a: torch.Tensor  # Snake of the next conv's input
+    next_b: torch.Tensor
+    fused: bool  # both convs in one launch
 
 
 @dataclass
 class _Block:
-    up: _Layer
+    up: _Layer  # out_a / out_b: Snake(act1) of the first unit
     units: list[_Unit]
     stride: int
     c_out: int
+
+
+# channel counts the fused residual-unit kernel handles (one column tile holds every channel)
+FUSED_UNIT_CHANNELS = (96, 192)
 
 
 def _snake_coefficients(alpha: torch.Tensor, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -120,9 +133,12 @@ class CodecStatePool:
 @dataclass
 class _Workspace:
     z: torch.Tensor
-    act: list[torch.Tensor]
-    h: torch.Tensor
-    xres: torch.Tensor
+    x: torch.Tensor  # the float32 residual stream (updated in place by each residual unit)
+    u: list[torch.Tensor]  # the bf16 operand of the next conv, two buffers (read while written)
+    h: torch.Tensor  # bf16 activation between the two convs of an unfused residual unit
+    # blocks whose residual units the fused kernel has no tile for at this shape (short rows with a
+    # wide halo): they run as two launches
+    unfused_blocks: set[int] = field(default_factory=set)
 
 
 class DacCodecDecoder:
@@ -156,8 +172,8 @@ class DacCodecDecoder:
             return pack_conv_transpose1d(w, rsrc["bias"], stride=stride, fp8=fp8).to(dev)
 
         blocks_w, blocks_r = weights["blocks"], ref["blocks"]
-        a, b = _snake_coefficients(blocks_r[0]["alpha"], dev)
-        self.in_conv = _Layer("in_conv", conv1d(weights["in_conv"], ref["in_conv"]), a, b)
+        a0, b0 = _snake_coefficients(blocks_r[0]["alpha"], dev)
+        self.in_conv = _Layer("in_conv", conv1d(weights["in_conv"], ref["in_conv"]), a0, b0)
         self.blocks: list[_Block] = []
         for i, (bw, br) in enumerate(zip(blocks_w, blocks_r)):
             units_r = br["units"]
@@ -166,8 +182,6 @@ class DacCodecDecoder:
             units = []
             for u, (uw, ur) in enumerate(zip(bw["units"], units_r)):
                 a2, b2 = _snake_coefficients(ur["alpha2"], dev)
-                c1 = _Layer(f"blocks.{i}.units.{u}.conv1",
-                            conv1d(uw["conv1"], ur["conv1"], ur["dilation"]), a2, b2)
                 if u + 1 < len(units_r):
                     nxt = units_r[u + 1]["alpha1"]
                 elif i + 1 < len(blocks_r):
@@ -175,8 +189,11 @@ class DacCodecDecoder:
                 else:
                     nxt = ref["final"]["alpha"]
                 an, bn = _snake_coefficients(nxt, dev)
-                c2 = _Layer(f"blocks.{i}.units.{u}.conv2", conv1d(uw["conv2"], ur["conv2"]), an, bn)
-                units.append(_Unit(c1, c2))
+                c1 = _Layer(f"blocks.{i}.units.{u}.conv1",
+                            conv1d(uw["conv1"], ur["conv1"], ur["dilation"]), a2, b2)
+                c2 = conv1d(uw["conv2"], ur["conv2"])
+                units.append(_Unit(c1, c2, a2, b2, an, bn,
+                                   c1.conv.c_out in FUSED_UNIT_CHANNELS))
             self.blocks.append(_Block(up, units, br["stride"], up.conv.c_out))
         fw = ref["final"]["conv"]["weight"]  # [1, C, k]
         self.final_weight = fw[0].t().contiguous().float().to(dev)  # [k, C]
@@ -197,7 +214,6 @@ class DacCodecDecoder:
             layout.append((blk.up.name, blk.up.conv.c_in, blk.up.conv.left_pad))
             for unit in blk.units:
                 layout.append((unit.conv1.name, unit.conv1.conv.c_in, unit.conv1.conv.left_pad))
-                layout.append((unit.conv2.name, unit.conv2.conv.c_in, unit.conv2.conv.left_pad))
         layout.append(("final", self.final_channels, self.final_taps - 1))
         return layout
 
@@ -213,17 +229,16 @@ class DacCodecDecoder:
         if ws is None:
             dev = self.device
             length = frames
-            max_act = frames * self.in_conv.conv.n_cols
-            max_res = 0
+            largest = frames * self.in_conv.conv.n_cols
             for blk in self.blocks:
                 length *= blk.stride
-                max_act = max(max_act, length * blk.c_out)
-                max_res = max(max_res, length * blk.c_out)
+                largest = max(largest, length * blk.c_out)
             ws = _Workspace(
-                z=torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16, device=dev),
-                act=[torch.empty(batch * max_act, dtype=torch.bfloat16, device=dev) for _ in range(2)],
-                h=torch.empty(batch * max_res, dtype=torch.bfloat16, device=dev),
-                xres=torch.empty(batch * max_res, dtype=torch.float32, device=dev),
+                z=torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16,
+                              device=dev),
+                x=torch.empty(batch * largest, dtype=torch.float32, device=dev),
+                u=[torch.empty(batch * largest, dtype=torch.bfloat16, device=dev) for _ in range(2)],
+                h=torch.empty(batch * largest, dtype=torch.bfloat16, device=dev),
             )
             self._workspaces[key] = ws
         return ws
@@ -253,43 +268,66 @@ class DacCodecDecoder:
             }
 
         timer = self.timer
-
-        def conv(x, layer: _Layer, out, **kw):
-            length = x.shape[1]
-            flops = 2.0 * batch * length * layer.conv.macs_per_position
-            with timer.launch("conv", flops, layer.name):
-                fused_conv(x, layer.conv, out, activation=N.ACT_SNAKE, act_a=layer.act_a,
-                           act_b=layer.act_b, **kw, **hist(layer.name))
+        snake = N.ACT_SNAKE
 
         k_books, _, dim = self.codebooks.shape
         rvq_bytes = batch * frames * (k_books * dim * 2 + dim * 2 + k_books * codes.element_size())
         with timer.launch("rvq", rvq_bytes):
             rvq_gather_sum(codes, self.codebooks, out=ws.z, clamp=True)
-        cur = 0
         length = frames
-        c0 = self.in_conv.conv.n_cols
-        x_act = self._view(ws.act[cur], batch, length, c0)
-        conv(ws.z, self.in_conv, x_act)
-        for blk in self.blocks:
-            nxt = 1 - cur
-            up = blk.up.conv
+        cur = 0
+        u = self._view(ws.u[cur], batch, length, self.in_conv.conv.n_cols)
+        ic = self.in_conv
+        with timer.launch("conv", 2.0 * batch * length * ic.conv.macs_per_position, ic.name):
+            fused_conv(ws.z, ic.conv, u, activation=snake, act_a=ic.out_a, act_b=ic.out_b,
+                       **hist(ic.name))
+        for bi, blk in enumerate(self.blocks):
+            up = blk.up
             out_len = length * blk.stride
+            c = blk.c_out
             # the polyphase output [B, L, s*C] is the transposed conv's [B, L*s, C]
-            y = self._view(ws.act[nxt], batch, out_len, blk.c_out)
-            xres = self._view(ws.xres, batch, out_len, blk.c_out)
-            conv(x_act, blk.up, y.view(batch, length, up.n_cols),
-                 sum_out=xres.view(batch, length, up.n_cols))
+            x = self._view(ws.x, batch, out_len, c)
+            u_next = self._view(ws.u[1 - cur], batch, out_len, c)
+            with timer.launch("conv", 2.0 * batch * length * up.conv.macs_per_position, up.name):
+                fused_conv(u, up.conv, u_next.view(batch, length, up.conv.n_cols),
+                           sum_out=x.view(batch, length, up.conv.n_cols), activation=snake,
+                           act_a=up.out_a, act_b=up.out_b, **hist(up.name))
+            cur = 1 - cur
+            u = u_next
             length = out_len
-            h = self._view(ws.h, batch, length, blk.c_out)
-            for u, unit in enumerate(blk.units):
-                conv(y, unit.conv1, h)
-                last = u + 1 == len(blk.units)
-                conv(h, unit.conv2, y, residual=xres, sum_out=None if last else xres)
-            x_act = y
-            cur = nxt
+            for unit in blk.units:
+                c1 = unit.conv1
+                flops = 2.0 * batch * length * (c1.conv.macs_per_position +
+                                                unit.conv2.macs_per_position)
+                u_next = self._view(ws.u[1 - cur], batch, length, c)
+                fused = False
+                if unit.fused and bi not in ws.unfused_blocks:
+                    try:
+                        with timer.launch(f"unit{c}", flops, c1.name):
+                            fused_conv(u, c1.conv, u_next, second=unit.conv2,
+                                       mid_activation=snake, mid_a=unit.mid_a, mid_b=unit.mid_b,
+                                       residual=x, sum_out=x, activation=snake,
+                                       act_a=unit.next_a, act_b=unit.next_b, **hist(c1.name))
+                        fused = True
+                    except N.OmniCodecError as err:
+                        if err.status != N.UNSUPPORTED:
+                            raise
+                        ws.unfused_blocks.add(bi)
+                if not fused:
+                    h = self._view(ws.h, batch, length, c)
+                    with timer.launch("conv", 2.0 * batch * length * c1.conv.macs_per_position,
+                                      c1.name):
+                        fused_conv(u, c1.conv, h, activation=snake, act_a=unit.mid_a,
+                                   act_b=unit.mid_b, **hist(c1.name))
+                    with timer.launch("conv", 2.0 * batch * length * unit.conv2.macs_per_position,
+                                      c1.name.replace("conv1", "conv2")):
+                        fused_conv(h, unit.conv2, u_next, residual=x, sum_out=x, activation=snake,
+                                   act_a=unit.next_a, act_b=unit.next_b)
+                cur = 1 - cur
+                u = u_next
         wave = torch.empty(batch, 1, length, dtype=torch.float32, device=self.device)
         with timer.launch("final", 2.0 * batch * length * self.final_taps * self.final_channels):
-            single_output_conv(x_act, self.final_weight, self.final_bias, wave,
+            single_output_conv(u, self.final_weight, self.final_bias, wave,
                                activation=N.ACT_TANH, left_pad=self.final_taps - 1,
                                **hist("final"))
         if state is not None:

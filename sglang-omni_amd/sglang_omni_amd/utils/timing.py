@@ -32,17 +32,15 @@ class LaunchTimer:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
-        try:
-            yield
-        finally:
-            end.record()
-            keys = [kind]
-            if self.per_layer and detail is not None:
-                keys.append(f"{kind}:{detail}")
-            for key in keys:
-                entry = self.kinds.setdefault(key, _Kind())
-                entry.events.append((start, end))
-                entry.work += work
+        yield  # a launch that raises (nothing enqueued) is not recorded
+        end.record()
+        keys = [kind]
+        if self.per_layer and detail is not None:
+            keys.append(f"{kind}:{detail}")
+        for key in keys:
+            entry = self.kinds.setdefault(key, _Kind())
+            entry.events.append((start, end))
+            entry.work += work
 
     def reset(self) -> None:
         self.kinds.clear()

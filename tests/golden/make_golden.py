@@ -35,7 +35,8 @@ from sglang_omni_amd.quantization import reference_weights  # noqa: E402
 
 TINY_DAC = DacDecoderConfig(n_codebooks=4, codebook_size=64, latent_dim=64, channels=128,
                             rates=(2, 4), conv_gain=0.85)
-TINY_HIFIGAN = HifiGanConfig(n_mels=16, channels=64, rates=(2, 3), up_kernels=(4, 7))
+# gain 0.4: output RMS ~0.04, the level of the full-size vocoder (tanh's linear range)
+TINY_HIFIGAN = HifiGanConfig(n_mels=16, channels=64, rates=(2, 3), up_kernels=(4, 7), conv_gain=0.4)
 
 
 def digest(*tensors: torch.Tensor) -> str:

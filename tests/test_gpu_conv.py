@@ -278,8 +278,72 @@ def test_invalid_arguments_raise_before_launch(gpu):
     with pytest.raises(ValueError):
         fused_conv(x, packed, torch.empty(1, 10, 64, device=gpu))
     with pytest.raises(ValueError):
-        fused_conv(x.float(), packed, torch.empty(1, 10, 96, device=gpu))
+        fused_conv(x.half(), packed, torch.empty(1, 10, 96, device=gpu))
+    with pytest.raises(ValueError):  # an output may not alias the input
+        xf = torch.zeros(1, 10, 96, device=gpu)
+        fused_conv(xf, packed, xf)
     # a dilation whose halo exceeds the kernel's staging budget is refused by the library
     big = pack_conv1d(bf(rand(96, 96, 7, gen=gen)), None, dilation=27).to(gpu)
     with pytest.raises(N.OmniCodecError, match="status 2"):
         fused_conv(x, big, torch.empty(1, 10, 96, device=gpu))
+
+
+def snake64(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
+    a = alpha.double().view(1, 1, -1)
+    return x.double() + torch.sin(a * x.double()) ** 2 / (a + 1e-9)
+
+
+@pytest.mark.parametrize("batch,length,c_in,c_out,k,d", [(3, 12, 192, 96, 7, 3), (2, 700, 96, 96, 7, 9),
+                                                      (64, 12, 512, 256, 7, 1)])
+def test_float32_input_with_the_snake_staged(gpu, batch, length, c_in, c_out, k, d):
+    """x float32 -> Snake per input channel -> bf16 operand, as the decoder feeds every conv."""
+    gen = torch.Generator().manual_seed(length + c_in)
+    x = rand(batch, length, c_in, gen=gen)
+    alpha = torch.rand(c_in, generator=gen) + 0.5
+    w = bf(rand(c_out, c_in, k, gen=gen, scale=1 / math.sqrt(c_in * k)))
+    b = rand(c_out, gen=gen, scale=0.1)
+    packed = pack_conv1d(w, b, dilation=d).to(gpu)
+    out = torch.empty(batch, length, c_out, dtype=torch.float32, device=gpu)
+    a_d = alpha.to(gpu)
+    fused_conv(x.to(gpu), packed, None, sum_out=out, in_activation=N.ACT_SNAKE, in_a=a_d,
+               in_b=(a_d + 1e-9).reciprocal())
+    u = bf(snake64(x, alpha).float())  # the staged operand: Snake in float32, rounded to bf16
+    # the GPU's float32 Snake and this float64 one round to different bf16 neighbours for a few
+    # operands (one bf16 ulp of the operand times a weight): a loose bound on every output, and a
+    # float32-summation bound on almost all of them
+    expected = conv_ref64(u, w, b, dilation=d)
+    close(out, expected, rtol=0, atol=2e-3)
+    err = (out.cpu().double() - expected).abs()
+    assert (err > 1e-4).double().mean().item() < 0.01
+
+
+@pytest.mark.parametrize("channels", [96, 192])
+@pytest.mark.parametrize("batch,length,d", [(1, 500, 1), (3, 37, 9), (64, 12, 3)])
+def test_fused_residual_unit_matches_float64(gpu, channels, batch, length, d):
+    """x + conv1x1(Snake2(conv7_d(Snake1(x)))) in one launch: the k = 1 conv runs on the bf16
+    tile the first conv leaves in LDS."""
+    gen = torch.Generator().manual_seed(channels + length + d)
+    c = channels
+    x = rand(batch, length, c, gen=gen)
+    a1 = torch.rand(c, generator=gen) + 0.5
+    a2 = torch.rand(c, generator=gen) + 0.5
+    w1 = bf(rand(c, c, 7, gen=gen, scale=1 / math.sqrt(c * 7)))
+    b1 = rand(c, gen=gen, scale=0.1)
+    w2 = bf(rand(c, c, 1, gen=gen, scale=1 / math.sqrt(c)))
+    b2 = rand(c, gen=gen, scale=0.1)
+    p1 = pack_conv1d(w1, b1, dilation=d).to(gpu)
+    p2 = pack_conv1d(w2, b2).to(gpu)
+    xd = x.to(gpu)
+    out = torch.empty(batch, length, c, dtype=torch.float32, device=gpu)
+    a1d, a2d = a1.to(gpu), a2.to(gpu)
+    fused_conv(xd, p1, None, sum_out=out, residual=xd, second=p2, in_activation=N.ACT_SNAKE,
+               in_a=a1d, in_b=(a1d + 1e-9).reciprocal(), mid_activation=N.ACT_SNAKE, mid_a=a2d,
+               mid_b=(a2d + 1e-9).reciprocal())
+    u = bf(snake64(x, a1).float())
+    h = bf(snake64(conv_ref64(u, w1, b1, dilation=d).float(), a2).float())
+    expected = x.double() + conv_ref64(h, w2, b2)
+    # h is rounded to bf16 from a float32 sum on the GPU and a float64 one here: one bf16 ulp of h
+    # may differ, which the k = 1 conv spreads over its channels
+    close(out, expected, rtol=0, atol=3e-2)
+    err = (out.cpu().double() - expected).abs()
+    assert err.mean().item() < 2e-3

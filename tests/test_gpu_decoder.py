@@ -31,6 +31,9 @@ pytestmark = pytest.mark.gpu
 
 TINY = DacDecoderConfig(n_codebooks=4, codebook_size=64, latent_dim=64, channels=128,
                         rates=(2, 4), conv_gain=0.85)
+# 384 -> 192 -> 96 channels: both residual-unit stages run the fused (one-launch) unit kernel
+TINY_FUSED = DacDecoderConfig(n_codebooks=4, codebook_size=64, latent_dim=64, channels=384,
+                              rates=(2, 3), conv_gain=0.85)
 
 
 def check_waveform(actual: torch.Tensor, expected: torch.Tensor, max_abs: float,
@@ -46,10 +49,10 @@ def check_waveform(actual: torch.Tensor, expected: torch.Tensor, max_abs: float,
     assert snr >= min_snr, snr
 
 
-@pytest.fixture(scope="module")
-def tiny(gpu):
-    weights = make_dac_weights(TINY, seed=0)
-    return weights, DacCodecDecoder(weights, TINY, device=gpu)
+@pytest.fixture(scope="module", params=[TINY, TINY_FUSED], ids=["unfused", "fused"])
+def tiny(gpu, request):
+    weights = make_dac_weights(request.param, seed=0)
+    return weights, DacCodecDecoder(weights, request.param, device=gpu)
 
 
 def test_single_conv_block_workload(gpu):
@@ -140,7 +143,7 @@ def test_rows_at_different_positions_keep_their_streams(gpu, tiny):
                                 torch.tensor([0, 2], device=gpu), first_decode=False)
     a_whole = decoder.from_indices(a[..., :7])
     b_whole = decoder.from_indices(b)
-    hop = TINY.hop_length
+    hop = decoder.frame_length
     assert torch.equal(torch.cat([a0, both[:1]], -1), a_whole)
     assert torch.equal(torch.cat([b0, both[1:]], -1), b_whole)
     assert pool.parity.tolist() == [2, 0, 2]
