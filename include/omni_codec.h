@@ -25,6 +25,10 @@
  *                                (sglang_omni/kernels/bias_snake_beta.py:102-151) and the slot
  *                                history of history_exchange (sglang_omni/kernels/
  *                                codec_state.py:150-181) folded in
+ *   omni_residual_stack          the ResidualUnit modules of a DAC DecoderBlock (sglang_omni/
+ *                                models/fishaudio_s2_pro/fish_speech/models/dac/
+ *                                modded_dac.py:619-643,742-790) as channels_last_decoder.py:
+ *                                114-122 runs them
  *   omni_single_output_conv      clamped_single_output_conv (sglang_omni/kernels/
  *                                single_output_conv.py:62-102); tanh form modded_dac.py:829
  *   omni_history_exchange        history_exchange (sglang_omni/kernels/codec_state.py:150-181)
@@ -85,7 +89,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 2: omni_conv_args with input activation and fused k=1 conv */
+int omni_codec_abi_version(void); /* 3: omni_residual_stack */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -186,6 +190,70 @@ typedef struct omni_conv_args {
 } omni_conv_args;
 
 int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
+
+/*
+ * The residual units of a DAC decoder block in one launch (Snake -> conv k = 7, dilation d ->
+ * Snake -> conv k = 1 -> + x, for each unit in turn), the residual stream kept in float32:
+ *
+ *   x_0 = x
+ *   for each unit k:
+ *     u_k = in_act_k(x_k) rounded to bf16               (Snake with unit.in_act_a / in_act_b)
+ *     v   = sum_{j < 7} sum_ci W1_k[n, j, ci] * u_k[b, i + (j - 6) * d_k, ci] * w1_scale + bias1
+ *     h   = Snake(mid_act_a, mid_act_b)(v) rounded to bf16
+ *     x_{k+1} = (sum_n' W2_k[n, n'] * h[n']) * w2_scale + bias2 + x_k
+ *   out   = Snake(out_act_a, out_act_b)(x_last) rounded to bf16   (the next layer's operand)
+ *   x_out = x_last                                                   (float32, optional)
+ *
+ * with the arithmetic of one omni_conv1d_fused residual-unit call per unit, so the results are
+ * the same bits. Weights use omni_conv1d_fused's packing ([C/32][C][7][32] and [C/32][C][32],
+ * bf16, or fp8-e4m3 with per-column scales). Each unit's dilated conv keeps its own streaming
+ * history (unit.hist_pool, bf16 [slots][2][6 * d_k][C], the omni_conv1d_fused contract with
+ * the shared slot_index / slot_parity / history_cold). channels = 96; x, out and x_out are
+ * [B, L, C] with channel stride 1 and must not alias.
+ *
+ * Replaces the three ResidualUnit modules of a DecoderBlock
+ * (sglang_omni/models/fishaudio_s2_pro/fish_speech/models/dac/modded_dac.py:619-643,742-790) as
+ * the channels-last decoder runs them (sglang_omni/models/fishaudio_drama3/
+ * channels_last_decoder.py:114-122).
+ */
+typedef struct omni_residual_unit {
+  const void* weight1;
+  const float* weight1_scale;
+  const float* bias1;
+  int64_t dilation;
+  const float* in_act_a;
+  const float* in_act_b;
+  const float* mid_act_a;
+  const float* mid_act_b;
+  const void* weight2;
+  const float* weight2_scale;
+  const float* bias2;
+  void* hist_pool;
+  int64_t hist_slot_stride;
+} omni_residual_unit;
+
+#define OMNI_MAX_RESIDUAL_UNITS 4
+
+typedef struct omni_residual_stack_args {
+  const float* x;
+  int64_t x_stride_b, x_stride_t;
+  int64_t batch, length, channels;
+  int weight_dtype;
+  int num_units;
+  omni_residual_unit units[OMNI_MAX_RESIDUAL_UNITS];
+  const int64_t* slot_index;
+  const int64_t* slot_parity;
+  int64_t hist_num_slots;
+  int history_cold;
+  const float* out_act_a;
+  const float* out_act_b;
+  void* out; /* bf16 */
+  int64_t out_stride_b, out_stride_t;
+  float* x_out; /* optional */
+  int64_t x_out_stride_b, x_out_stride_t;
+} omni_residual_stack_args;
+
+int omni_residual_stack(const omni_residual_stack_args* args, omni_stream_t stream);
 
 /*
  * Conv from channels-last activations to one output channel, stride 1, undilated:

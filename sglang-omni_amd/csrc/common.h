@@ -57,6 +57,12 @@ OMNI_DEVICE float snake_sin(float x) {
   return __builtin_amdgcn_sinf(r);
 }
 
+// Snake: v + b * sin(a * v)^2 (one expression for every kernel, so they round alike).
+OMNI_DEVICE float snake_value(float v, float a, float b) {
+  const float s = snake_sin(a * v);
+  return v + b * (s * s);
+}
+
 // Activations applied in the conv epilogues.
 enum {
   OMNI_ACT_NONE = 0,
@@ -72,20 +78,15 @@ __device__ __noinline__ float act_tanh(float v) { return tanhf(v); }
 
 // The activations applied to conv operands (staging, between fused convs): cheap and inline.
 OMNI_DEVICE float operand_act(int act, float v, float a, float b, float slope) {
-  if (act == OMNI_ACT_SNAKE) {
-    const float s = snake_sin(a * v);
-    return v + b * (s * s);
-  }
+  if (act == OMNI_ACT_SNAKE) return snake_value(v, a, b);
   if (act == OMNI_ACT_LEAKY_RELU) return v >= 0.f ? v : v * slope;
   return v;
 }
 
 OMNI_DEVICE float apply_act(int act, float v, float a, float b, float slope) {
   switch (act) {
-    case OMNI_ACT_SNAKE: {
-      float s = snake_sin(a * v);
-      return v + b * (s * s);
-    }
+    case OMNI_ACT_SNAKE:
+      return snake_value(v, a, b);
     case OMNI_ACT_LEAKY_RELU:
       return v >= 0.f ? v : v * slope;
     case OMNI_ACT_TANH:

@@ -624,10 +624,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
           f32x4 y = v[u];
           if (act == OMNI_ACT_SNAKE) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float sn = snake_sin(act_a[e] * y[e]);
-              y[e] = y[e] + act_b[e] * (sn * sn);
-            }
+            for (int e = 0; e < 4; ++e) y[e] = snake_value(y[e], act_a[e], act_b[e]);
           } else if (act == OMNI_ACT_LEAKY_RELU) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;

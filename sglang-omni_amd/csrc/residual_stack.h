@@ -1,0 +1,471 @@
+// The residual units of a decoder block in one kernel (gfx950 bf16 MFMA).
+//
+// A DAC decoder block ends in residual units u -> conv k7 (dilation 1, 3, 9) -> Snake -> conv k1
+// -> + x. Run one launch per unit, the float32 residual stream x and the bf16 operand travel
+// through HBM between every unit (12 bytes per element per unit at the 96-channel stage). Here a
+// workgroup owns a tile of positions and runs every unit over it with x held in registers:
+//
+//   * staged rows: each row segment of the tile is preceded by H = sum of the unit halos rows
+//     (the causal receptive field of the whole stack), so the last unit's outputs for the tile's
+//     positions depend only on staged data. Unit k computes every staged row; a row whose window
+//     reaches before the segment's first staged row gives a value no later unit's valid row
+//     reads (row q of a segment is exact for unit k once q >= halo_1 + ... + halo_k).
+//   * x: float32 in the MFMA accumulator layout (lane = row, 4 consecutive channels per lane),
+//     loaded once from HBM, updated in place by each unit's k = 1 conv.
+//   * the operand u_k = Snake(x_k) and the h tile between the two convs: bf16 in one LDS tile
+//     [C/32][guard + rows][32] (64-byte rows, the 16-byte slots rotated by (row / 4) % 4 so the
+//     accumulator-layout writes and the operand reads both spread over all banks); guard rows
+//     ahead of row 0 keep the taps of the first rows inside the tile.
+//   * weights: the dilated conv's chunk [C][7 * 32 + 8] or the k = 1 conv's [C/32][C][32] in one
+//     LDS region, each prefetched into registers while the previous one is in use.
+//   * streaming: rows left of position 0 of a stream row take each unit's own history copy (or
+//     zeros), and the workgroup that owns the last 6 * d positions of a row writes them as the
+//     unit's new history, as the one-unit kernel does.
+//
+// Only the last unit's operand-to-be, Snake(x_last), leaves as bf16 (and x_last as float32 on
+// request). The arithmetic of every element repeats the one-unit kernel's expression for
+// expression, so the two paths give the same bits.
+#pragma once
+
+#include "conv_kernel.h"
+
+namespace omni_stack {
+
+using omni_conv::fp8x8_to_bf16x8;
+using omni_conv::kChunk;
+using omni_conv::pack_bf16x2;
+
+constexpr int kMaxUnits = OMNI_MAX_RESIDUAL_UNITS;
+constexpr int kTaps = 7;    // the residual unit's dilated conv
+constexpr int kGuard = 64;  // LDS rows ahead of row 0: the largest unit halo taken (6 * 10 = 60)
+constexpr int kCoefRows = 8;
+
+struct StackUnit {
+  const void* w1;  // [C/32][C][7][32]
+  const float* w1_scale;
+  const float* b1;
+  const float* in_a;  // Snake of the unit's input
+  const float* in_b;
+  const float* mid_a;  // Snake between the two convs
+  const float* mid_b;
+  const void* w2;  // [C/32][C][32]
+  const float* w2_scale;
+  const float* b2;
+  u16* hist;  // history pool of the dilated conv's operand, or NULL
+  int hist_stride;
+  int dil, halo;
+  uint32_t w1_bytes, w2_bytes, hist_bytes;
+};
+
+struct StackParams {
+  const float* x;
+  int x_sb, x_st;
+  int batch, length;
+  int nunits;
+  StackUnit unit[kMaxUnits];
+  const int64_t* slot_index;
+  const int64_t* slot_parity;
+  int64_t hist_slots;
+  int hist_cold;
+  const float* out_a;
+  const float* out_b;
+  u16* out;
+  int o_sb, o_st;
+  float* x_out;
+  int xo_sb, xo_st;
+  uint32_t x_bytes, o_bytes, xo_bytes;
+  int H;              // staged rows ahead of each segment (sum of the unit halos)
+  int seg_len;        // long rows: output positions per tile; short rows: the row length
+  int tiles_per_row;  // long rows: tiles per stream row; 0: short rows, whole rows per tile
+  int rows_per_tile;  // short rows: stream rows per tile
+};
+
+// LDS element offset of 16-byte slot `slot` of staged row `row` (guard included) in chunk kc.
+template <int UROWS>
+__device__ __forceinline__ int uaddr(int kc, int row, int slot) {
+  return (kc * UROWS + row) * kChunk + ((slot ^ ((row >> 2) & 3)) << 3);
+}
+
+template <int C, int WCO, int WP, int TP>
+struct StackTile {
+  static constexpr int NT = 64 * WCO * WP;
+  static constexpr int TCO = C / (16 * WCO);
+  static constexpr int R = WP * TP * 16;  // staged rows per tile
+  static constexpr int CH = C / kChunk;
+  static constexpr int UROWS = kGuard + R;
+  static constexpr int WROW = kTaps * kChunk + 8;
+  static constexpr int W1_PIECES = (C * kTaps * 4 + NT - 1) / NT;
+  static constexpr int W2_PIECES = (C * C / 8 + NT - 1) / NT;
+  static constexpr int WPR = W1_PIECES > W2_PIECES ? W1_PIECES : W2_PIECES;
+  static constexpr int W_ELEMS = C * WROW > CH * C * kChunk ? C * WROW : CH * C * kChunk;
+  static constexpr int COEF = (kMaxUnits * kCoefRows + 2) * C;  // floats
+  static constexpr size_t lds_bytes() {
+    return (size_t)CH * UROWS * kChunk * 2 + (size_t)W_ELEMS * 2 + (size_t)COEF * 4;
+  }
+  static_assert(C % (16 * WCO) == 0 && C % kChunk == 0, "tile shape");
+};
+
+template <int C, int WCO, int WP, int TP, bool W_FP8>
+__global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const StackParams p) {
+  using Tile = StackTile<C, WCO, WP, TP>;
+  constexpr int NT = Tile::NT;
+  constexpr int TCO = Tile::TCO;
+  constexpr int CH = Tile::CH;
+  constexpr int UROWS = Tile::UROWS;
+  constexpr int WROW = Tile::WROW;
+  constexpr int PIECES_PER_ROW = C / 8;  // 16-byte pieces of a staged row
+  constexpr uint32_t WE = W_FP8 ? 1 : 2;
+  extern __shared__ __attribute__((aligned(16))) u16 lds[];
+  u16* us = lds;                        // operand / h tile
+  u16* ws = lds + CH * UROWS * kChunk;  // weights
+  float* coef = reinterpret_cast<float*>(ws + Tile::W_ELEMS);
+  enum { kS1, kB1, kMA, kMB, kS2, kB2, kNA, kNB };
+  float* in0 = coef + kMaxUnits * kCoefRows * C;  // unit 0's input Snake a, b
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_co = wave % WCO;
+  const int wave_p = wave / WCO;
+  const int lrow = lane & 15;
+  const int lk = (lane >> 4) * 8;
+  const int wco0 = wave_co * TCO * 16;
+
+  // The tile: nseg row segments of len output positions starting at position i0 of rows b0..
+  int b0, i0, nseg, len;
+  if (p.tiles_per_row > 0) {
+    b0 = blockIdx.x / p.tiles_per_row;
+    i0 = (blockIdx.x - b0 * p.tiles_per_row) * p.seg_len;
+    nseg = 1;
+    len = min(p.seg_len, p.length - i0);
+  } else {
+    b0 = blockIdx.x * p.rows_per_tile;
+    i0 = 0;
+    nseg = min(p.rows_per_tile, p.batch - b0);
+    len = p.length;
+  }
+  const int H = p.H;
+  const int L = p.length;
+  const int span = len + H;  // staged rows per segment
+  const int rows = nseg * span;
+
+  // This lane's staged rows in the accumulator layout and their stream positions.
+  int rrow[TP], rb[TP], rpos[TP];
+#pragma unroll
+  for (int t = 0; t < TP; ++t) {
+    const int r = wave_p * TP * 16 + t * 16 + lrow;
+    const int s = r / span;
+    rrow[t] = r;
+    rb[t] = b0 + s;
+    rpos[t] = r < rows ? i0 - H + (r - s * span) : -(1 << 30);
+  }
+
+  // ---- set-up: x into registers, coefficients and guard rows into LDS, the first weights
+  f32x4 xv[TCO][TP];
+  {
+    const auto xr = buffer_rsrc(p.x, p.x_bytes);
+#pragma unroll
+    for (int c = 0; c < TCO; ++c) {
+      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const bool ok = rpos[t] >= 0 && rpos[t] < L;
+        const uint32_t off = ok ? (uint32_t)(rb[t] * p.x_sb + rpos[t] * p.x_st + n) * 4 : kOutOfRange;
+        xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+      }
+    }
+  }
+  for (int e = tid; e < (p.nunits * kCoefRows + 2) * C; e += NT) {
+    const int k = e / C;
+    const int n = e - k * C;
+    float v;
+    if (k >= p.nunits * kCoefRows) {
+      v = k == p.nunits * kCoefRows ? p.unit[0].in_a[n] : p.unit[0].in_b[n];
+      in0[(k - p.nunits * kCoefRows) * C + n] = v;
+      continue;
+    }
+    const int unit = k / kCoefRows;
+    const int row = k - unit * kCoefRows;
+    const StackUnit& U = p.unit[unit];
+    const bool last = unit + 1 == p.nunits;
+    switch (row) {
+      case kS1: v = U.w1_scale ? U.w1_scale[n] : 1.f; break;
+      case kB1: v = U.b1 ? U.b1[n] : 0.f; break;
+      case kMA: v = U.mid_a[n]; break;
+      case kMB: v = U.mid_b[n]; break;
+      case kS2: v = U.w2_scale ? U.w2_scale[n] : 1.f; break;
+      case kB2: v = U.b2 ? U.b2[n] : 0.f; break;
+      case kNA: v = last ? p.out_a[n] : p.unit[unit + 1].in_a[n]; break;
+      default: v = last ? p.out_b[n] : p.unit[unit + 1].in_b[n]; break;
+    }
+    coef[unit * kCoefRows * C + row * C + n] = v;
+  }
+  for (int e = tid; e < CH * kGuard * 4; e += NT) {
+    const int kc = e / (kGuard * 4);
+    const int rem = e - kc * kGuard * 4;
+    *reinterpret_cast<u32x4*>(us + (kc * UROWS + (rem >> 2)) * kChunk + (rem & 3) * 8) =
+        u32x4{0u, 0u, 0u, 0u};
+  }
+
+  u32x4 wr[W_FP8 ? 1 : Tile::WPR];
+  u32x2 wr8[W_FP8 ? Tile::WPR : 1];
+  auto load_w1 = [&](int k, int kc) __attribute__((always_inline)) {
+    const auto rs = buffer_rsrc(p.unit[k].w1, p.unit[k].w1_bytes);
+    const uint32_t base = (uint32_t)(kc * C * kTaps * kChunk);
+#pragma unroll
+    for (int u = 0; u < Tile::W1_PIECES; ++u) {
+      const int piece = tid + u * NT;
+      const uint32_t off = piece < C * kTaps * 4 ? (base + (uint32_t)piece * 8) * WE : kOutOfRange;
+      if constexpr (W_FP8) wr8[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      else wr[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    }
+  };
+  auto load_w2 = [&](int k) __attribute__((always_inline)) {
+    const auto rs = buffer_rsrc(p.unit[k].w2, p.unit[k].w2_bytes);
+#pragma unroll
+    for (int u = 0; u < Tile::W2_PIECES; ++u) {
+      const int piece = tid + u * NT;
+      const uint32_t off = piece < C * C / 8 ? (uint32_t)piece * 8 * WE : kOutOfRange;
+      if constexpr (W_FP8) wr8[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      else wr[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    }
+  };
+  auto wpiece = [&](int u) __attribute__((always_inline)) -> u32x4 {
+    if constexpr (W_FP8) return fp8x8_to_bf16x8(wr8[u]);
+    else return wr[u];
+  };
+  auto store_w1 = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < Tile::W1_PIECES; ++u) {
+      const int piece = tid + u * NT;
+      if (piece < C * kTaps * 4) {
+        const int nl = piece / (kTaps * 4);
+        const int rem = piece - nl * kTaps * 4;
+        *reinterpret_cast<u32x4*>(ws + nl * WROW + (rem >> 2) * kChunk + (rem & 3) * 8) = wpiece(u);
+      }
+    }
+  };
+  auto store_w2 = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < Tile::W2_PIECES; ++u) {
+      const int piece = tid + u * NT;
+      if (piece < C * C / 8) *reinterpret_cast<u32x4*>(ws + piece * 8) = wpiece(u);
+    }
+  };
+  // LDS addressing of the operand tile from the accumulator layout. Staged rows of this lane are
+  // kGuard + wave_p * TP * 16 + t * 16 + lrow, so the slot rotation (row / 4) % 4 is the lane's
+  // (lrow / 4) % 4 for every t: each access is a per-lane base plus a compile-time offset.
+  const int row0 = kGuard + wave_p * TP * 16 + lrow;  // staged row of t = 0 (guard included)
+  const int sw = (lrow >> 2) & 3;
+  // columns n = c * 16 + (lane / 16) * 4 .. + 3 of the lane: chunk c / 2, 16-byte slot
+  // 2 * (c % 2) + lane / 32, element (lane / 16 % 2) * 4 within the slot
+  const int put_base0 = row0 * kChunk + ((((lane >> 5)) ^ sw) << 3) + ((lane >> 4) & 1) * 4;
+  const int put_base1 = row0 * kChunk + (((2 | (lane >> 5)) ^ sw) << 3) + ((lane >> 4) & 1) * 4;
+  const int rd_base = row0 * kChunk + (((lane >> 4) ^ sw) << 3);  // operand reads at row0 + 16t
+  static_assert(WCO == 1, "the column layout below assumes one wave holds every column");
+  auto put = [&](int c, int t, float y0, float y1, float y2, float y3) __attribute__((always_inline)) {
+    uint2 o;
+    o.x = pack_bf16x2(y0, y1);
+    o.y = pack_bf16x2(y2, y3);
+    const int base = (c & 1) ? put_base1 : put_base0;
+    *reinterpret_cast<uint2*>(us + base + (c >> 1) * UROWS * kChunk + t * 16 * kChunk) = o;
+  };
+
+  load_w1(0, 0);
+  __syncthreads();  // coefficients and guard rows
+  // unit 0's operand
+#pragma unroll
+  for (int c = 0; c < TCO; ++c) {
+    const int n = wco0 + c * 16 + (lane >> 4) * 4;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(in0 + n);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(in0 + C + n);
+#pragma unroll
+    for (int t = 0; t < TP; ++t) {
+      const f32x4 v = xv[c][t];
+      put(c, t, snake_value(v[0], a[0], b[0]), snake_value(v[1], a[1], b[1]),
+          snake_value(v[2], a[2], b[2]), snake_value(v[3], a[3], b[3]));
+    }
+  }
+
+  f32x4 acc[TCO][TP];
+  for (int k = 0; k < p.nunits; ++k) {
+    const int h = p.unit[k].halo;
+    const int d = p.unit[k].dil;
+    u16* hist = p.unit[k].hist;
+    const auto hr = buffer_rsrc(hist, p.unit[k].hist_bytes);
+    const int hstride = p.unit[k].hist_stride;
+    __syncthreads();  // the operand tile is complete
+    // (a) operand rows left of position 0 (segments that start a stream row): the history copy
+    // of the row's slot, or zeros
+    if (i0 == 0 && h > 0) {
+      for (int e = tid; e < nseg * h * PIECES_PER_ROW; e += NT) {
+        const int s = e / (h * PIECES_PER_ROW);
+        const int rem = e - s * h * PIECES_PER_ROW;
+        const int j = rem / PIECES_PER_ROW;  // sample j of the history: position j - h
+        const int piece = rem - j * PIECES_PER_ROW;
+        uint32_t off = kOutOfRange;
+        if (hist != nullptr && !p.hist_cold) {
+          const int64_t slot = p.slot_index[b0 + s];
+          if (slot >= 0 && slot < p.hist_slots) {
+            const int parity = (int)(p.slot_parity[slot] & 1);
+            off = (uint32_t)((int)slot * hstride + (parity * h + j) * C + piece * 8) * 2;
+          }
+        }
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0);
+        const int row = kGuard + s * span + H - h + j;
+        *reinterpret_cast<u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3)) = v;
+      }
+      __syncthreads();
+    }
+    // (b) the new history: the last h operand samples of each stream row, written by the
+    // workgroup holding them (those left of 0 by the one holding position 0)
+    if (hist != nullptr) {
+      for (int e = tid; e < nseg * h * PIECES_PER_ROW; e += NT) {
+        const int s = e / (h * PIECES_PER_ROW);
+        const int rem = e - s * h * PIECES_PER_ROW;
+        const int j = rem / PIECES_PER_ROW;
+        const int piece = rem - j * PIECES_PER_ROW;
+        const int pos = L - h + j;
+        const bool own = pos >= 0 ? (pos >= i0 && pos < i0 + len) : i0 == 0;
+        const int64_t slot = p.slot_index[b0 + s];
+        if (own && slot >= 0 && slot < p.hist_slots) {
+          const int parity = (int)(p.slot_parity[slot] & 1);
+          const int row = kGuard + s * span + (pos - i0) + H;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
+          const uint32_t off = (uint32_t)((int)slot * hstride + ((1 - parity) * h + j) * C + piece * 8) * 2;
+          __builtin_amdgcn_raw_buffer_store_b128(v, hr, off, 0, 0);
+        }
+      }
+    }
+    // (c) the dilated conv
+#pragma unroll
+    for (int c = 0; c < TCO; ++c)
+#pragma unroll
+      for (int t = 0; t < TP; ++t) acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kc = 0; kc < CH; ++kc) {
+      if (kc > 0) __syncthreads();  // the previous chunk's weights are no longer read
+      store_w1();
+      __syncthreads();
+      if (kc + 1 < CH) load_w1(k, kc + 1);
+      else load_w2(k);
+      const u16* wtap = ws + (wco0 + lrow) * WROW + lk;
+      const u16* ukc = us + kc * UROWS * kChunk;
+#pragma unroll 1
+      for (int j = 0; j < kTaps; ++j) {
+        bf16x8 a[TCO];
+#pragma unroll
+        for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * WROW);
+        // rows row0 + j * d - h + 16 t: one rotation for every t
+        const int rj = row0 + j * d - h;
+        const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+          const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
+#pragma unroll
+          for (int c = 0; c < TCO; ++c)
+            acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
+        }
+        wtap += kChunk;
+      }
+    }
+    __syncthreads();  // the operand and the weights are no longer read
+    // (d) h = Snake(acc * scale + bias) over the operand tile; the k = 1 weights
+    const float* cf = coef + k * kCoefRows * C;
+#pragma unroll
+    for (int c = 0; c < TCO; ++c) {
+      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(cf + kS1 * C + n);
+      const f32x4 bi = *reinterpret_cast<const f32x4*>(cf + kB1 * C + n);
+      const f32x4 ma = *reinterpret_cast<const f32x4*>(cf + kMA * C + n);
+      const f32x4 mb = *reinterpret_cast<const f32x4*>(cf + kMB * C + n);
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = operand_act(OMNI_ACT_SNAKE, acc[c][t][e] * sc[e] + bi[e], ma[e], mb[e], 0.f);
+        put(c, t, y[0], y[1], y[2], y[3]);
+        acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    store_w2();
+    __syncthreads();
+    if (k + 1 < p.nunits) load_w1(k + 1, 0);
+    // (e) the k = 1 conv
+#pragma unroll
+    for (int kc = 0; kc < CH; ++kc) {
+      bf16x8 a[TCO];
+#pragma unroll
+      for (int c = 0; c < TCO; ++c)
+        a[c] = *reinterpret_cast<const bf16x8*>(ws + (kc * C + wco0 + c * 16 + lrow) * kChunk + lk);
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(
+            us + rd_base + kc * UROWS * kChunk + t * 16 * kChunk);
+#pragma unroll
+        for (int c = 0; c < TCO; ++c)
+          acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // h and the k = 1 weights are no longer read
+    // (f) x += acc * scale + bias; the next operand Snake(x) (the next unit's input Snake, or
+    // the output Snake)
+#pragma unroll
+    for (int c = 0; c < TCO; ++c) {
+      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(cf + kS2 * C + n);
+      const f32x4 bi = *reinterpret_cast<const f32x4*>(cf + kB2 * C + n);
+      const f32x4 na = *reinterpret_cast<const f32x4*>(cf + kNA * C + n);
+      const f32x4 nb = *reinterpret_cast<const f32x4*>(cf + kNB * C + n);
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        f32x4 v = acc[c][t] * sc + bi;
+        v += xv[c][t];
+        xv[c][t] = v;
+        put(c, t, snake_value(v[0], na[0], nb[0]), snake_value(v[1], na[1], nb[1]),
+            snake_value(v[2], na[2], nb[2]), snake_value(v[3], na[3], nb[3]));
+      }
+    }
+  }
+  __syncthreads();
+  // ---- the output operand rows of the tile's positions, 16 contiguous bytes per thread
+  {
+    const auto orsrc = buffer_rsrc(p.out, p.o_bytes);
+    for (int e = tid; e < nseg * len * PIECES_PER_ROW; e += NT) {
+      const int s = e / (len * PIECES_PER_ROW);
+      const int rem = e - s * len * PIECES_PER_ROW;
+      const int q = rem / PIECES_PER_ROW;
+      const int piece = rem - q * PIECES_PER_ROW;
+      const int row = kGuard + s * span + H + q;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
+      const uint32_t off = (uint32_t)((b0 + s) * p.o_sb + (i0 + q) * p.o_st + piece * 8) * 2;
+      __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, off, 0, 0);
+    }
+  }
+  if (p.x_out != nullptr) {
+    const auto xo = buffer_rsrc(p.x_out, p.xo_bytes);
+#pragma unroll
+    for (int c = 0; c < TCO; ++c) {
+      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const int q = rrow[t] - (rrow[t] / span) * span;
+        const bool ok = rrow[t] < rows && q >= H;
+        const uint32_t off =
+            ok ? (uint32_t)(rb[t] * p.xo_sb + rpos[t] * p.xo_st + n) * 4 : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xv[c][t]), xo, off, 0, 0);
+      }
+    }
+  }
+}
+
+// 96 channels: 8 waves, each with all 96 columns and 32 of the 256 staged rows (the register
+// budget of two waves per SIMD: x and the accumulators take 96 of them).
+using Stack96 = StackTile<96, 1, 8, 2>;
+
+template <bool W_FP8>
+int launch_stack96(const StackParams& p, int grid, hipStream_t stream);
+template <> int launch_stack96<false>(const StackParams& p, int grid, hipStream_t stream);
+template <> int launch_stack96<true>(const StackParams& p, int grid, hipStream_t stream);
+
+}  // namespace omni_stack

@@ -1,0 +1,128 @@
+// C ABI of the residual-stack kernel: argument validation and the tiling of the position space.
+#include "residual_stack.h"
+
+namespace {
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_stream_t stream) {
+  using namespace omni_stack;
+  if (!a || !a->x || !a->out || !a->out_act_a || !a->out_act_b) return OMNI_ERR_INVALID_ARG;
+  if (a->batch < 0 || a->length < 0 || a->num_units < 1 || a->num_units > kMaxUnits)
+    return OMNI_ERR_INVALID_ARG;
+  if (a->weight_dtype != OMNI_DTYPE_BF16 && a->weight_dtype != OMNI_DTYPE_FP8_E4M3)
+    return OMNI_ERR_INVALID_ARG;
+  const bool fp8 = a->weight_dtype == OMNI_DTYPE_FP8_E4M3;
+  const int64_t C = a->channels;
+  if (C != 96) return C > 0 && C % 32 == 0 ? OMNI_ERR_UNSUPPORTED : OMNI_ERR_INVALID_ARG;
+  // 16-byte accesses of x, out and x_out rows
+  if (!aligned16(a->x) || a->x_stride_t < C || a->x_stride_t % 4 || a->x_stride_b % 4)
+    return OMNI_ERR_INVALID_ARG;
+  if (!aligned16(a->out) || a->out_stride_t < C || a->out_stride_t % 8 || a->out_stride_b % 8)
+    return OMNI_ERR_INVALID_ARG;
+  if (a->x_out && (!aligned16(a->x_out) || a->x_out_stride_t < C || a->x_out_stride_t % 4 ||
+                   a->x_out_stride_b % 4))
+    return OMNI_ERR_INVALID_ARG;
+  bool any_hist = false;
+  int64_t H = 0;
+  for (int k = 0; k < a->num_units; ++k) {
+    const omni_residual_unit& u = a->units[k];
+    if (!u.weight1 || !u.weight2 || !u.in_act_a || !u.in_act_b || !u.mid_act_a || !u.mid_act_b)
+      return OMNI_ERR_INVALID_ARG;
+    if (!aligned16(u.weight1) || !aligned16(u.weight2)) return OMNI_ERR_INVALID_ARG;
+    if (fp8 && (!u.weight1_scale || !u.weight2_scale)) return OMNI_ERR_INVALID_ARG;
+    if (u.dilation < 1) return OMNI_ERR_INVALID_ARG;
+    if (6 * u.dilation > 60) return OMNI_ERR_UNSUPPORTED;
+    if (u.hist_pool) {
+      if (!aligned16(u.hist_pool) || u.hist_slot_stride < 2 * 6 * u.dilation * C ||
+          u.hist_slot_stride % 8)
+        return OMNI_ERR_INVALID_ARG;
+      any_hist = true;
+    }
+    H += 6 * u.dilation;
+  }
+  if (any_hist && (!a->slot_index || !a->slot_parity || a->hist_num_slots < 1))
+    return OMNI_ERR_INVALID_ARG;
+  if (a->batch == 0 || a->length == 0) return OMNI_OK;
+  if (H + 16 > Stack96::R) return OMNI_ERR_UNSUPPORTED;
+
+  // byte extents (buffer offsets are 32-bit)
+  const int64_t B = a->batch, L = a->length;
+  const int64_t limit = 0x7fffffffLL;
+  const int64_t x_bytes = ((B - 1) * a->x_stride_b + (L - 1) * a->x_stride_t + C) * 4;
+  const int64_t o_bytes = ((B - 1) * a->out_stride_b + (L - 1) * a->out_stride_t + C) * 2;
+  const int64_t xo_bytes =
+      a->x_out ? ((B - 1) * a->x_out_stride_b + (L - 1) * a->x_out_stride_t + C) * 4 : 0;
+  if (x_bytes > limit || o_bytes > limit || xo_bytes > limit) return OMNI_ERR_UNSUPPORTED;
+
+  StackParams p{};
+  p.x = a->x;
+  p.x_sb = (int)a->x_stride_b;
+  p.x_st = (int)a->x_stride_t;
+  p.batch = (int)B;
+  p.length = (int)L;
+  p.nunits = a->num_units;
+  const int64_t w_elem = fp8 ? 1 : 2;
+  for (int k = 0; k < a->num_units; ++k) {
+    const omni_residual_unit& u = a->units[k];
+    StackUnit& s = p.unit[k];
+    s.w1 = u.weight1;
+    s.w1_scale = fp8 ? u.weight1_scale : nullptr;
+    s.b1 = u.bias1;
+    s.in_a = u.in_act_a;
+    s.in_b = u.in_act_b;
+    s.mid_a = u.mid_act_a;
+    s.mid_b = u.mid_act_b;
+    s.w2 = u.weight2;
+    s.w2_scale = fp8 ? u.weight2_scale : nullptr;
+    s.b2 = u.bias2;
+    s.dil = (int)u.dilation;
+    s.halo = (int)(6 * u.dilation);
+    s.w1_bytes = (uint32_t)(C * C * kTaps * w_elem);
+    s.w2_bytes = (uint32_t)(C * C * w_elem);
+    if (u.hist_pool) {
+      const int64_t hb = a->hist_num_slots * u.hist_slot_stride * 2;
+      if (hb > limit) return OMNI_ERR_UNSUPPORTED;
+      s.hist = reinterpret_cast<u16*>(u.hist_pool);
+      s.hist_stride = (int)u.hist_slot_stride;
+      s.hist_bytes = (uint32_t)hb;
+    }
+  }
+  p.slot_index = a->slot_index;
+  p.slot_parity = a->slot_parity;
+  p.hist_slots = a->hist_num_slots;
+  p.hist_cold = a->history_cold;
+  p.out_a = a->out_act_a;
+  p.out_b = a->out_act_b;
+  p.out = reinterpret_cast<u16*>(a->out);
+  p.o_sb = (int)a->out_stride_b;
+  p.o_st = (int)a->out_stride_t;
+  p.x_out = a->x_out;
+  p.xo_sb = (int)a->x_out_stride_b;
+  p.xo_st = (int)a->x_out_stride_t;
+  p.x_bytes = (uint32_t)x_bytes;
+  p.o_bytes = (uint32_t)o_bytes;
+  p.xo_bytes = (uint32_t)xo_bytes;
+  p.H = (int)H;
+
+  // Long rows: tiles inside one row, as many as the staged rows need, evened out; short rows:
+  // as many whole rows (each with its halo) as the staged rows hold.
+  constexpr int64_t R = Stack96::R;
+  int64_t grid;
+  if (L + H > R) {
+    const int64_t tiles = (L + (R - H) - 1) / (R - H);
+    p.seg_len = (int)((L + tiles - 1) / tiles);
+    p.tiles_per_row = (int)((L + p.seg_len - 1) / p.seg_len);
+    grid = B * p.tiles_per_row;
+  } else {
+    p.seg_len = (int)L;
+    p.tiles_per_row = 0;
+    p.rows_per_tile = (int)(R / (L + H));
+    grid = (B + p.rows_per_tile - 1) / p.rows_per_tile;
+  }
+  if (grid > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return fp8 ? launch_stack96<true>(p, (int)grid, s) : launch_stack96<false>(p, (int)grid, s);
+}

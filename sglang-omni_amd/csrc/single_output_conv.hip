@@ -165,6 +165,137 @@ __global__ void __launch_bounds__(kPositions) single_output_conv_kernel(const So
   }
 }
 
+// The decoder's form, bf16 input used as is with G * 8 <= 128 channels and at most 8 taps: the
+// same tile, order and history handling as above, but every thread issues all of its 16-byte
+// staging loads (buffer loads: pieces past an edge read zeros) before the first LDS store, so a
+// workgroup waits for HBM once rather than once per piece.
+constexpr int kFastMaxTaps = 8;
+
+struct SocFastParams {
+  const u16* x;
+  int x_sb, x_st, length, tiles;
+  const float* weight;  // [taps][channels]
+  const float* bias;
+  int taps, lpad;
+  const u16* hist;
+  const int64_t* slot_index;
+  const int64_t* slot_parity;
+  int64_t hist_slots;
+  int hist_slot_stride;
+  int hist_cold;
+  int act;
+  void* out;
+  int64_t o_sb;
+  uint32_t x_bytes, hist_bytes;
+};
+
+template <int G, int ODT>
+__global__ void __launch_bounds__(kPositions) single_output_conv_bf16_kernel(const SocFastParams p) {
+  constexpr int C = G * 8;
+  constexpr int PITCH = C + 8;  // elements per LDS row (16 bytes of padding)
+  constexpr int PIECES = ((kPositions + kFastMaxTaps - 1) * G + kPositions - 1) / kPositions;
+  extern __shared__ __attribute__((aligned(16))) u16 xs[];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x / p.tiles;
+  const int i0 = (blockIdx.x - b * p.tiles) * kPositions;
+  const int ctx = p.lpad;
+  const int rows = kPositions + p.taps - 1;
+  const int L = p.length;
+
+  int hread = -1, hwrite = -1;  // element offsets of this row's two history copies in the pool
+  if (p.hist != nullptr) {
+    const int64_t slot = p.slot_index[b];
+    if (slot >= 0 && slot < p.hist_slots) {
+      const int parity = (int)(p.slot_parity[slot] & 1);
+      const int base = (int)slot * p.hist_slot_stride;
+      hread = p.hist_cold ? -1 : base + parity * ctx * C;
+      hwrite = base + (1 - parity) * ctx * C;
+    }
+  }
+  const auto x_rsrc = buffer_rsrc(p.x, p.x_bytes);
+  const auto h_rsrc = buffer_rsrc(p.hist, p.hist_bytes);
+  u32x4 v[PIECES];
+#pragma unroll
+  for (int u = 0; u < PIECES; ++u) {
+    const int piece = tid + u * kPositions;
+    const int r = piece / G;
+    const int c = (piece - r * G) * 8;
+    const int pos = i0 - ctx + r;
+    uint32_t xo = kOutOfRange, ho = kOutOfRange;
+    if (r < rows) {
+      if (pos >= 0 && pos < L) xo = (uint32_t)(b * p.x_sb + pos * p.x_st + c) * 2;
+      else if (pos < 0 && hread >= 0) ho = (uint32_t)(hread + (ctx + pos) * C + c) * 2;
+    }
+    v[u] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, xo, 0, 0) |
+           __builtin_amdgcn_raw_buffer_load_b128(h_rsrc, ho, 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < PIECES; ++u) {
+    const int piece = tid + u * kPositions;
+    const int r = piece / G;
+    const int c = (piece - r * G) * 8;
+    if (r < rows) *reinterpret_cast<u32x4*>(xs + r * PITCH + c) = v[u];
+  }
+  if (hwrite >= 0) {
+    // the last ctx samples of history ++ input, each written by the workgroup whose positions
+    // hold it (those left of 0 by the first)
+#pragma unroll
+    for (int u = 0; u < PIECES; ++u) {
+      const int piece = tid + u * kPositions;
+      const int r = piece / G;
+      const int c = (piece - r * G) * 8;
+      const int pos = i0 - ctx + r;
+      const bool own = r < rows && pos >= L - ctx && pos < L &&
+                       ((pos >= i0 && pos < i0 + kPositions) || (i0 == 0 && pos < 0));
+      const uint32_t wo = own ? (uint32_t)(hwrite + (pos - (L - ctx)) * C + c) * 2 : kOutOfRange;
+      __builtin_amdgcn_raw_buffer_store_b128(v[u], h_rsrc, wo, 0, 0);
+    }
+  }
+  __syncthreads();
+  float acc = 0.f;
+  const u16* xrow = xs + tid * PITCH;
+  for (int j = 0; j < p.taps; ++j) {
+    const float* wrow = p.weight + j * C;
+#pragma unroll
+    for (int c = 0; c < C; c += 8) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(xrow + j * PITCH + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc = __builtin_fmaf(wrow[c + 2 * e], __uint_as_float(w[e] << 16), acc);
+        acc = __builtin_fmaf(wrow[c + 2 * e + 1], __uint_as_float(w[e] & 0xffff0000u), acc);
+      }
+    }
+  }
+  const int i = i0 + tid;
+  if (i < L) {
+    const float y = acc + (p.bias ? p.bias[0] : 0.f);
+    store_val<ODT>(p.out, b * p.o_sb + i, apply_act(p.act, y, 0.f, 0.f, 0.f));
+  }
+}
+
+template <int G, int ODT>
+int launch_soc_fast(const SocFastParams& p, hipStream_t s, dim3 grid) {
+  auto k = single_output_conv_bf16_kernel<G, ODT>;
+  static const bool raised = [&] {
+    const hipError_t e = hipFuncSetAttribute((const void*)k,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipGetLastError();
+    return e == hipSuccess;
+  }();
+  (void)raised;
+  const size_t lds = (size_t)(kPositions + p.taps - 1) * (G * 8 + 8) * 2;
+  hipLaunchKernelGGL(k, grid, dim3(kPositions), lds, s, p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+template <int G>
+int launch_soc_fast_o(const SocFastParams& p, int out_dtype, hipStream_t s, dim3 grid) {
+  if (out_dtype == OMNI_DTYPE_F32) return launch_soc_fast<G, OMNI_DTYPE_F32>(p, s, grid);
+  if (out_dtype == OMNI_DTYPE_BF16) return launch_soc_fast<G, OMNI_DTYPE_BF16>(p, s, grid);
+  return launch_soc_fast<G, OMNI_DTYPE_F16>(p, s, grid);
+}
+
 size_t lds_bytes(int64_t channels, int taps, bool stage_bf16) {
   const int64_t cn = channels < kMaxChunk ? channels : kMaxChunk;
   const int64_t elem = stage_bf16 ? 2 : 4;
@@ -271,6 +402,44 @@ extern "C" int omni_single_output_conv(const void* x, int x_dtype, int64_t x_str
   // the decoder's form (an input activation or a slot history): bf16 operands, like the history
   const bool stage_bf16 = in_activation != OMNI_ACTIVATION_NONE || hist_pool != nullptr;
   if (stage_bf16 && channels % 8) return OMNI_ERR_UNSUPPORTED;
+  if (x_dtype == OMNI_DTYPE_BF16 && in_activation == OMNI_ACTIVATION_NONE && !context_in_buffer &&
+      (channels == 32 || channels == 64 || channels == 96 || channels == 128) &&
+      taps <= kFastMaxTaps && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && x_stride_t % 8 == 0 &&
+      x_stride_b % 8 == 0 && (!hist_pool || (reinterpret_cast<uintptr_t>(hist_pool) & 15) == 0)) {
+    // 32-bit element offsets and buffer extents
+    const int64_t x_bytes = ((batch - 1) * x_stride_b + (length - 1) * x_stride_t + channels) * 2;
+    const int64_t hist_bytes = hist_pool ? hist_num_slots * hist_slot_stride * 2 : 0;
+    if (x_bytes <= 0x7fffffffLL && hist_bytes <= 0x7fffffffLL && x_stride_b <= 0x7fffffffLL &&
+        hist_slot_stride % 8 == 0) {
+      SocFastParams f{};
+      f.x = reinterpret_cast<const u16*>(x);
+      f.x_sb = (int)x_stride_b;
+      f.x_st = (int)x_stride_t;
+      f.length = (int)length;
+      f.tiles = (int)tiles;
+      f.weight = weight;
+      f.bias = bias;
+      f.taps = (int)taps;
+      f.lpad = (int)left_pad;
+      f.hist = p.hist;
+      f.slot_index = slot_index;
+      f.slot_parity = slot_parity;
+      f.hist_slots = hist_num_slots;
+      f.hist_slot_stride = (int)hist_slot_stride;
+      f.hist_cold = history_cold;
+      f.act = activation;
+      f.out = out;
+      f.o_sb = out_stride_b;
+      f.x_bytes = (uint32_t)x_bytes;
+      f.hist_bytes = (uint32_t)hist_bytes;
+      switch (channels) {
+        case 32: return launch_soc_fast_o<4>(f, out_dtype, s, grid);
+        case 64: return launch_soc_fast_o<8>(f, out_dtype, s, grid);
+        case 96: return launch_soc_fast_o<12>(f, out_dtype, s, grid);
+        default: return launch_soc_fast_o<16>(f, out_dtype, s, grid);
+      }
+    }
+  }
   if (stage_bf16) {
     if (x_dtype == OMNI_DTYPE_F32) return launch_soc_x<OMNI_DTYPE_F32, true>(p, out_dtype, s, grid);
     if (x_dtype == OMNI_DTYPE_BF16) return launch_soc_x<OMNI_DTYPE_BF16, true>(p, out_dtype, s, grid);

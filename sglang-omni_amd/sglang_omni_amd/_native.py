@@ -97,6 +97,57 @@ class ConvArgs(ctypes.Structure):
     ]
 
 
+class ResidualUnitArgs(ctypes.Structure):
+    """Mirror of ``omni_residual_unit`` in include/omni_codec.h."""
+
+    _fields_ = [
+        ("weight1", ctypes.c_void_p),
+        ("weight1_scale", ctypes.c_void_p),
+        ("bias1", ctypes.c_void_p),
+        ("dilation", ctypes.c_int64),
+        ("in_act_a", ctypes.c_void_p),
+        ("in_act_b", ctypes.c_void_p),
+        ("mid_act_a", ctypes.c_void_p),
+        ("mid_act_b", ctypes.c_void_p),
+        ("weight2", ctypes.c_void_p),
+        ("weight2_scale", ctypes.c_void_p),
+        ("bias2", ctypes.c_void_p),
+        ("hist_pool", ctypes.c_void_p),
+        ("hist_slot_stride", ctypes.c_int64),
+    ]
+
+
+MAX_RESIDUAL_UNITS = 4
+
+
+class ResidualStackArgs(ctypes.Structure):
+    """Mirror of ``omni_residual_stack_args`` in include/omni_codec.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_stride_b", ctypes.c_int64),
+        ("x_stride_t", ctypes.c_int64),
+        ("batch", ctypes.c_int64),
+        ("length", ctypes.c_int64),
+        ("channels", ctypes.c_int64),
+        ("weight_dtype", ctypes.c_int),
+        ("num_units", ctypes.c_int),
+        ("units", ResidualUnitArgs * MAX_RESIDUAL_UNITS),
+        ("slot_index", ctypes.c_void_p),
+        ("slot_parity", ctypes.c_void_p),
+        ("hist_num_slots", ctypes.c_int64),
+        ("history_cold", ctypes.c_int),
+        ("out_act_a", ctypes.c_void_p),
+        ("out_act_b", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("out_stride_b", ctypes.c_int64),
+        ("out_stride_t", ctypes.c_int64),
+        ("x_out", ctypes.c_void_p),
+        ("x_out_stride_b", ctypes.c_int64),
+        ("x_out_stride_t", ctypes.c_int64),
+    ]
+
+
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _PTR = ctypes.c_void_p
@@ -110,6 +161,7 @@ SIGNATURES: dict[str, list] = {
     "omni_rvq_gather_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _INT, _I64, _I64,
                             _PTR, _INT, _I64, _I64, _I64, _INT, _PTR],
     "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
+    "omni_residual_stack": [ctypes.POINTER(ResidualStackArgs), _PTR],
     "omni_single_output_conv": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _PTR, _PTR,
                                 _PTR, _PTR, _I64, _I64, _PTR, _PTR, _PTR, _I64, _I64, _INT, _INT,
                                 _PTR, _INT, _I64, _PTR],

@@ -2,12 +2,20 @@
 
 from .bias_snake_beta import SnakeBetaCoefficients, fused_bias_snake_beta
 from .codec_state import history_exchange, overlap_exchange
-from .conv import PackedConv, fused_conv, pack_conv1d, pack_conv_transpose1d
+from .conv import (
+    PackedConv,
+    ResidualUnitWeights,
+    fused_conv,
+    pack_conv1d,
+    pack_conv_transpose1d,
+    residual_stack,
+)
 from .rvq import rvq_gather_sum
 from .single_output_conv import clamped_single_output_conv, single_output_conv
 
 __all__ = [
     "PackedConv",
+    "ResidualUnitWeights",
     "SnakeBetaCoefficients",
     "clamped_single_output_conv",
     "fused_bias_snake_beta",
@@ -16,6 +24,7 @@ __all__ = [
     "overlap_exchange",
     "pack_conv1d",
     "pack_conv_transpose1d",
+    "residual_stack",
     "rvq_gather_sum",
     "single_output_conv",
 ]

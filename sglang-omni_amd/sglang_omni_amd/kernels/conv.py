@@ -264,3 +264,91 @@ def fused_conv(
     N.check(lib.omni_conv1d_fused(ctypes.byref(args), N.stream_handle(x.device)),
             "omni_conv1d_fused")
     return out
+
+
+@dataclass
+class ResidualUnitWeights:
+    """One residual unit of a decoder block: Snake(in) -> conv1 (k = 7, dilation) ->
+    Snake(mid) -> conv2 (k = 1) -> + x, with the Snake coefficient pairs (a, b) as float32 [C]."""
+
+    conv1: PackedConv
+    conv2: PackedConv
+    in_a: torch.Tensor
+    in_b: torch.Tensor
+    mid_a: torch.Tensor
+    mid_b: torch.Tensor
+
+
+def residual_stack(
+    x: torch.Tensor,
+    units: list[ResidualUnitWeights],
+    out: torch.Tensor,
+    out_a: torch.Tensor,
+    out_b: torch.Tensor,
+    *,
+    x_out: torch.Tensor | None = None,
+    histories: list[torch.Tensor | None] | None = None,
+    slot_index: torch.Tensor | None = None,
+    slot_parity: torch.Tensor | None = None,
+    history_cold: bool = False,
+) -> torch.Tensor:
+    """Launch ``omni_residual_stack``: every unit in turn over x [B, L, C] float32, then
+    out = Snake(out_a, out_b)(x_last) as bf16 [B, L, C] (and x_last into x_out, float32).
+    histories[k] is unit k's conv1 history pool [slots, 2, 6 * dilation, C] bf16 (streaming)."""
+    N.require_device(x, out, x_out)
+    if not 1 <= len(units) <= N.MAX_RESIDUAL_UNITS:
+        raise ValueError(f"1..{N.MAX_RESIDUAL_UNITS} residual units per launch")
+    if x.dtype != torch.float32 or x.dim() != 3 or x.stride(2) != 1:
+        raise ValueError("x must be float32 [B, L, C] with channel stride 1")
+    batch, length, channels = x.shape
+    for t, dt in ((out, torch.bfloat16), (x_out, torch.float32)):
+        if t is None:
+            continue
+        if t.dtype != dt or t.dim() != 3 or tuple(t.shape) != (batch, length, channels) or t.stride(2) != 1:
+            raise ValueError("out / x_out must be [B, L, C] (bf16 / float32) with channel stride 1")
+        if t.data_ptr() == x.data_ptr():
+            raise ValueError("an output may not alias x")
+    wdtype = units[0].conv1.weight.dtype
+    args = N.ResidualStackArgs()
+    args.x = x.data_ptr()
+    args.x_stride_b, args.x_stride_t = x.stride(0), x.stride(1)
+    args.batch, args.length, args.channels = batch, length, channels
+    args.weight_dtype = N.omni_dtype(wdtype)
+    args.num_units = len(units)
+    for k, u in enumerate(units):
+        c1, c2 = u.conv1, u.conv2
+        if (c1.c_in != channels or c1.c_out != channels or c1.taps != 7 or c1.phases != 1
+                or c1.left_pad != 6 * c1.dilation or c2.taps != 1 or c2.c_in != channels
+                or c2.c_out != channels or c1.weight.dtype != wdtype or c2.weight.dtype != wdtype):
+            raise ValueError("a residual unit is a causal k = 7 conv and a k = 1 conv over C channels")
+        a = args.units[k]
+        a.weight1 = c1.weight.data_ptr()
+        a.weight1_scale = N.ptr(c1.scale)
+        a.bias1 = N.ptr(c1.bias)
+        a.dilation = c1.dilation
+        a.in_act_a, a.in_act_b = u.in_a.data_ptr(), u.in_b.data_ptr()
+        a.mid_act_a, a.mid_act_b = u.mid_a.data_ptr(), u.mid_b.data_ptr()
+        a.weight2 = c2.weight.data_ptr()
+        a.weight2_scale = N.ptr(c2.scale)
+        a.bias2 = N.ptr(c2.bias)
+        hist = histories[k] if histories is not None else None
+        if hist is not None:
+            if slot_index is None or slot_parity is None:
+                raise ValueError("a history pool needs slot_index and slot_parity")
+            a.hist_pool = hist.data_ptr()
+            a.hist_slot_stride = hist.stride(0)
+            args.hist_num_slots = hist.shape[0]
+    if histories is not None and any(h is not None for h in histories):
+        args.slot_index = slot_index.data_ptr()
+        args.slot_parity = slot_parity.data_ptr()
+        args.history_cold = int(history_cold)
+    args.out_act_a, args.out_act_b = out_a.data_ptr(), out_b.data_ptr()
+    args.out = out.data_ptr()
+    args.out_stride_b, args.out_stride_t = out.stride(0), out.stride(1)
+    if x_out is not None:
+        args.x_out = x_out.data_ptr()
+        args.x_out_stride_b, args.x_out_stride_t = x_out.stride(0), x_out.stride(1)
+    lib = N.load_library()
+    N.check(lib.omni_residual_stack(ctypes.byref(args), N.stream_handle(x.device)),
+            "omni_residual_stack")
+    return out

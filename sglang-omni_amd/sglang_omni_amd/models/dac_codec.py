@@ -41,7 +41,14 @@ from typing import Any
 import torch
 
 from .. import _native as N
-from ..kernels.conv import PackedConv, fused_conv, pack_conv1d, pack_conv_transpose1d
+from ..kernels.conv import (
+    PackedConv,
+    ResidualUnitWeights,
+    fused_conv,
+    pack_conv1d,
+    pack_conv_transpose1d,
+    residual_stack,
+)
 from ..kernels.rvq import rvq_gather_sum
 from ..kernels.single_output_conv import single_output_conv
 from ..quantization import reference_weights
@@ -74,10 +81,13 @@ class _Block:
     units: list[_Unit]
     stride: int
     c_out: int
+    stack: list[ResidualUnitWeights] | None = None  # the units as one residual-stack launch
 
 
 # channel counts the fused residual-unit kernel handles (one column tile holds every channel)
 FUSED_UNIT_CHANNELS = (96, 192)
+# channel counts the residual-stack kernel (every unit of a block in one launch) handles
+STACK_CHANNELS = (96,)
 
 
 def _snake_coefficients(alpha: torch.Tensor, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -151,7 +161,8 @@ class DacCodecDecoder:
     """
 
     def __init__(self, weights: dict[str, Any], config: DacDecoderConfig, *,
-                 device: torch.device | str = "cuda", weight_format: str = "bf16"):
+                 device: torch.device | str = "cuda", weight_format: str = "bf16",
+                 residual_stacks: bool = True):
         self.config = config
         self.device = torch.device(device)
         self.weight_format = weight_format
@@ -194,7 +205,14 @@ class DacCodecDecoder:
                 c2 = conv1d(uw["conv2"], ur["conv2"])
                 units.append(_Unit(c1, c2, a2, b2, an, bn,
                                    c1.conv.c_out in FUSED_UNIT_CHANNELS))
-            self.blocks.append(_Block(up, units, br["stride"], up.conv.c_out))
+            blk = _Block(up, units, br["stride"], up.conv.c_out)
+            if (residual_stacks and blk.c_out in STACK_CHANNELS
+                    and len(units) <= N.MAX_RESIDUAL_UNITS
+                    and all(u.conv1.conv.taps == 7 and u.conv1.conv.dilation <= 10 for u in units)):
+                ins = [(up.out_a, up.out_b)] + [(u.next_a, u.next_b) for u in units[:-1]]
+                blk.stack = [ResidualUnitWeights(u.conv1.conv, u.conv2, a, b, u.mid_a, u.mid_b)
+                             for u, (a, b) in zip(units, ins)]
+            self.blocks.append(blk)
         fw = ref["final"]["conv"]["weight"]  # [1, C, k]
         self.final_weight = fw[0].t().contiguous().float().to(dev)  # [k, C]
         self.final_bias = ref["final"]["conv"]["bias"].float().to(dev).contiguous()
@@ -288,13 +306,32 @@ class DacCodecDecoder:
             # the polyphase output [B, L, s*C] is the transposed conv's [B, L*s, C]
             x = self._view(ws.x, batch, out_len, c)
             u_next = self._view(ws.u[1 - cur], batch, out_len, c)
+            # with a residual stack the up conv writes only x: the stack takes its own operand
             with timer.launch("conv", 2.0 * batch * length * up.conv.macs_per_position, up.name):
-                fused_conv(u, up.conv, u_next.view(batch, length, up.conv.n_cols),
+                fused_conv(u, up.conv,
+                           None if blk.stack else u_next.view(batch, length, up.conv.n_cols),
                            sum_out=x.view(batch, length, up.conv.n_cols), activation=snake,
                            act_a=up.out_a, act_b=up.out_b, **hist(up.name))
             cur = 1 - cur
             u = u_next
             length = out_len
+            if blk.stack:
+                flops = 2.0 * batch * length * sum(
+                    u.conv1.macs_per_position + u.conv2.macs_per_position for u in blk.stack)
+                u_next = self._view(ws.u[1 - cur], batch, length, c)
+                h = {}
+                if state is not None:
+                    h = {"histories": [state["pool"].histories.get(un.conv1.name)
+                                       for un in blk.units],
+                         "slot_index": state["slot_index"],
+                         "slot_parity": state["pool"].parity,
+                         "history_cold": state["cold"]}
+                last = blk.units[-1]
+                with timer.launch(f"stack{c}", flops, f"blocks.{bi}.units"):
+                    residual_stack(x, blk.stack, u_next, last.next_a, last.next_b, **h)
+                cur = 1 - cur
+                u = u_next
+                continue
             for unit in blk.units:
                 c1 = unit.conv1
                 flops = 2.0 * batch * length * (c1.conv.macs_per_position +

@@ -241,3 +241,24 @@ def test_hifigan_matches_the_oracle(gpu):
     out = vocoder(mel.to(gpu))
     expected = O.hifigan_generator(mel, reference_weights(weights, "bf16"))
     check_waveform(out, expected, 2e-3)
+
+
+@pytest.mark.parametrize("config", [TINY_FUSED, CODEC_24K], ids=["tiny", "codec24k"])
+def test_residual_stacks_decode_like_one_launch_per_unit(gpu, config):
+    """The 96-channel stage as one residual-stack launch per block gives the bits of one fused
+    launch per residual unit, whole and streamed."""
+    weights = make_dac_weights(config, seed=0)
+    stacked = DacCodecDecoder(weights, config, device=gpu)
+    per_unit = DacCodecDecoder(weights, config, device=gpu, residual_stacks=False)
+    assert any(b.stack for b in stacked.blocks) and not any(b.stack for b in per_unit.blocks)
+    gen = torch.Generator().manual_seed(4)
+    codes = torch.randint(0, config.codebook_size, (3, config.n_codebooks, 24), generator=gen)
+    codes = codes.to(gpu)
+    assert torch.equal(stacked.from_indices(codes), per_unit.from_indices(codes))
+    idx = torch.tensor([2, 0, 1], device=gpu)
+    outs = []
+    for dec in (stacked, per_unit):
+        pool = dec.new_state_pool(num_slots=3)
+        outs.append(torch.cat([dec.decode_slots(codes[..., s:s + 8], pool, idx,
+                                                first_decode=s == 0) for s in (0, 8, 16)], -1))
+    assert torch.equal(outs[0], outs[1])

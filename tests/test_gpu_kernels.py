@@ -219,6 +219,43 @@ def test_single_output_conv_gives_a_position_the_same_bits_in_any_split(gpu):
     assert torch.equal(row, whole[1:2])
 
 
+@pytest.mark.parametrize("channels", [32, 64, 96, 128, 136])
+@pytest.mark.parametrize("taps", [7, 8])
+def test_decoder_form_single_output_conv_streams_like_the_whole_row(gpu, channels, taps):
+    """The decoder's last layer: causal conv of bf16 operands to one channel + tanh. The whole
+    rows match a float64 direct sum, and decoding them in chunks (some shorter than the context)
+    through the slot history gives the whole decode's bits."""
+    from sglang_omni_amd.kernels.single_output_conv import single_output_conv
+
+    gen = torch.Generator().manual_seed(channels + taps)
+    batch, length, ctx = 3, 700, taps - 1
+    x = (torch.randn(batch, length, channels, generator=gen) * 0.5).to(torch.bfloat16)
+    w = torch.randn(taps, channels, generator=gen) / (taps * channels) ** 0.5
+    bias = torch.tensor([0.05])
+    xg, wg, bg = x.to(gpu), w.to(gpu), bias.to(gpu)
+    whole = torch.empty(batch, 1, length, device=gpu)
+    single_output_conv(xg, wg, bg, whole, activation=N.ACT_TANH, left_pad=ctx)
+    padded = F.pad(x.double(), (0, 0, ctx, 0))
+    ref = sum(padded[:, j:j + length] @ w[j].double() for j in range(taps)) + 0.05
+    assert (whole.cpu()[:, 0].double() - torch.tanh(ref)).abs().max().item() < 2e-6
+
+    slots = 5
+    history = torch.zeros(slots, 2 * ctx * channels, dtype=torch.bfloat16, device=gpu)
+    parity = torch.zeros(slots, dtype=torch.int64, device=gpu)
+    slot_index = torch.tensor([4, 0, 2], device=gpu)
+    pieces, start = [], 0
+    for n, size in enumerate([5, 300, 1, 3, 391]):
+        out = torch.empty(batch, 1, size, device=gpu)
+        single_output_conv(xg[:, start:start + size].contiguous(), wg, bg, out,
+                           activation=N.ACT_TANH, left_pad=ctx, history=history,
+                           slot_index=slot_index, slot_parity=parity, history_cold=n == 0)
+        parity[slot_index] += 1
+        pieces.append(out)
+        start += size
+    assert start == length
+    assert torch.equal(torch.cat(pieces, dim=-1), whole)
+
+
 # ------------------------------------------------------------------ Snake family
 
 
