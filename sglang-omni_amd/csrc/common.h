@@ -47,21 +47,18 @@ OMNI_DEVICE u16 float_to_bits_f16(float x) {
   return *reinterpret_cast<u16*>(&h);
 }
 
-// sin(x) for the Snake family: reduce x to revolutions r = x / (2 pi) - rint(x / (2 pi)) in
-// [-0.5, 0.5] (Payne-Hanek is unnecessary: the activations are bounded), then the hardware
-// v_sin_f32, which takes its argument in revolutions.
-OMNI_DEVICE float snake_sin(float x) {
-  const float inv_two_pi = 0.15915494309189535f;
-  float r = x * inv_two_pi;
-  r = r - __builtin_rintf(r);
-  return __builtin_amdgcn_sinf(r);
-}
-
-// Snake: v + b * sin(a * v)^2 (one expression for every kernel, so they round alike).
-OMNI_DEVICE float snake_value(float v, float a, float b) {
-  const float s = snake_sin(a * v);
+// Snake v + b * sin(2 pi ar v)^2 with the frequency in revolutions, ar = alpha / (2 pi): the
+// hardware v_sin_f32 takes revolutions, and v_fract_f32 reduces the phase to [0, 1) (the
+// activations are bounded, so no Payne-Hanek style reduction is needed). The kernels stage
+// ar = alpha * kInvTwoPi once per coefficient; one expression serves every kernel, so a value
+// computed by different kernels rounds alike.
+constexpr float kInvTwoPi = 0.15915494309189535f;
+OMNI_DEVICE float snake_rev(float v, float ar, float b) {
+  const float s = __builtin_amdgcn_sinf(__builtin_amdgcn_fractf(ar * v));
   return v + b * (s * s);
 }
+// The same with alpha itself (a = alpha, b = 1 / (alpha + 1e-9) for Snake1d).
+OMNI_DEVICE float snake_value(float v, float a, float b) { return snake_rev(v, a * kInvTwoPi, b); }
 
 // Activations applied in the conv epilogues.
 enum {
@@ -77,8 +74,9 @@ enum {
 __device__ __noinline__ float act_tanh(float v) { return tanhf(v); }
 
 // The activations applied to conv operands (staging, between fused convs): cheap and inline.
+// For Snake, `a` is in revolutions (alpha / (2 pi), see snake_rev).
 OMNI_DEVICE float operand_act(int act, float v, float a, float b, float slope) {
-  if (act == OMNI_ACT_SNAKE) return snake_value(v, a, b);
+  if (act == OMNI_ACT_SNAKE) return snake_rev(v, a, b);
   if (act == OMNI_ACT_LEAKY_RELU) return v >= 0.f ? v : v * slope;
   return v;
 }

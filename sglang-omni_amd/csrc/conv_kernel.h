@@ -98,8 +98,11 @@ __device__ __forceinline__ float fp8_e4m3_to_float(uint32_t v) {
   return __uint_as_float(__float_as_uint(f) | s);
 }
 
+// Two floats to a bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)float_to_bits_bf16(a) | ((uint32_t)float_to_bits_bf16(b) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
 }
 
 __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 raw) {
@@ -138,7 +141,8 @@ struct ConvTile {
     return (m > epi ? m : epi) + coef_bytes();
   }
   // Per-column epilogue coefficients, staged once per workgroup at the end of LDS: rows
-  // scale, bias, mid_a, mid_b, scale2, bias2, act_a, act_b of BCO floats each.
+  // scale, bias, mid_a, mid_b, scale2, bias2, act_a, act_b of BCO floats each (the Snake
+  // frequencies mid_a and act_a in revolutions).
   static constexpr int NCOEF = 8;
   static constexpr size_t coef_bytes() { return (size_t)NCOEF * BCO * 4; }
   static constexpr size_t coef_offset(int64_t rows, int64_t taps, bool fuse2) {
@@ -316,6 +320,8 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       const float4 b1v = *reinterpret_cast<const float4*>(p.in_b + kc * kChunk + q8 + 4);
       ina[0] = a0.x; ina[1] = a0.y; ina[2] = a0.z; ina[3] = a0.w;
       ina[4] = a1.x; ina[5] = a1.y; ina[6] = a1.z; ina[7] = a1.w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ina[e] *= kInvTwoPi;  // Snake frequency in revolutions
       inb[0] = b0v.x; inb[1] = b0v.y; inb[2] = b0v.z; inb[3] = b0v.w;
       inb[4] = b1v.x; inb[5] = b1v.y; inb[6] = b1v.z; inb[7] = b1v.w;
     }
@@ -437,11 +443,11 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       switch (k) {
         case kScale: if (p.wscale) v = p.wscale[n]; break;
         case kBias: if (p.bias) v = p.bias[co]; break;
-        case kMidA: if (FUSE2 && p.mid_a) v = p.mid_a[co]; break;
+        case kMidA: if (FUSE2 && p.mid_a) v = p.mid_a[co] * kInvTwoPi; break;
         case kMidB: if (FUSE2 && p.mid_b) v = p.mid_b[co]; break;
         case kScale2: if (FUSE2 && p.wscale2) v = p.wscale2[n]; break;
         case kBias2: if (FUSE2 && p.bias2) v = p.bias2[co]; break;
-        case kActA: if (p.act_a) v = p.act_a[co]; break;
+        case kActA: if (p.act_a) v = p.act_a[co] * kInvTwoPi; break;
         default: if (p.act_b) v = p.act_b[co]; break;
       }
     }
@@ -624,7 +630,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
           f32x4 y = v[u];
           if (act == OMNI_ACT_SNAKE) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = snake_value(y[e], act_a[e], act_b[e]);
+            for (int e = 0; e < 4; ++e) y[e] = snake_rev(y[e], act_a[e], act_b[e]);
           } else if (act == OMNI_ACT_LEAKY_RELU) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;

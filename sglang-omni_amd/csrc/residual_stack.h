@@ -119,6 +119,8 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   u16* us = lds;                        // operand / h tile
   u16* ws = lds + CH * UROWS * kChunk;  // weights
   float* coef = reinterpret_cast<float*>(ws + Tile::W_ELEMS);
+  // per unit: scale1, bias1, mid Snake (a in revolutions, b), scale2, bias2, the next operand's
+  // Snake (a in revolutions, b)
   enum { kS1, kB1, kMA, kMB, kS2, kB2, kNA, kNB };
   float* in0 = coef + kMaxUnits * kCoefRows * C;  // unit 0's input Snake a, b
 
@@ -180,7 +182,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     const int n = e - k * C;
     float v;
     if (k >= p.nunits * kCoefRows) {
-      v = k == p.nunits * kCoefRows ? p.unit[0].in_a[n] : p.unit[0].in_b[n];
+      v = k == p.nunits * kCoefRows ? p.unit[0].in_a[n] * kInvTwoPi : p.unit[0].in_b[n];
       in0[(k - p.nunits * kCoefRows) * C + n] = v;
       continue;
     }
@@ -191,11 +193,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     switch (row) {
       case kS1: v = U.w1_scale ? U.w1_scale[n] : 1.f; break;
       case kB1: v = U.b1 ? U.b1[n] : 0.f; break;
-      case kMA: v = U.mid_a[n]; break;
+      case kMA: v = U.mid_a[n] * kInvTwoPi; break;
       case kMB: v = U.mid_b[n]; break;
       case kS2: v = U.w2_scale ? U.w2_scale[n] : 1.f; break;
       case kB2: v = U.b2 ? U.b2[n] : 0.f; break;
-      case kNA: v = last ? p.out_a[n] : p.unit[unit + 1].in_a[n]; break;
+      case kNA: v = (last ? p.out_a[n] : p.unit[unit + 1].in_a[n]) * kInvTwoPi; break;
       default: v = last ? p.out_b[n] : p.unit[unit + 1].in_b[n]; break;
     }
     coef[unit * kCoefRows * C + row * C + n] = v;
@@ -282,8 +284,8 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
       const f32x4 v = xv[c][t];
-      put(c, t, snake_value(v[0], a[0], b[0]), snake_value(v[1], a[1], b[1]),
-          snake_value(v[2], a[2], b[2]), snake_value(v[3], a[3], b[3]));
+      put(c, t, snake_rev(v[0], a[0], b[0]), snake_rev(v[1], a[1], b[1]),
+          snake_rev(v[2], a[2], b[2]), snake_rev(v[3], a[3], b[3]));
     }
   }
 
@@ -422,8 +424,8 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         f32x4 v = acc[c][t] * sc + bi;
         v += xv[c][t];
         xv[c][t] = v;
-        put(c, t, snake_value(v[0], na[0], nb[0]), snake_value(v[1], na[1], nb[1]),
-            snake_value(v[2], na[2], nb[2]), snake_value(v[3], na[3], nb[3]));
+        put(c, t, snake_rev(v[0], na[0], nb[0]), snake_rev(v[1], na[1], nb[1]),
+            snake_rev(v[2], na[2], nb[2]), snake_rev(v[3], na[3], nb[3]));
       }
     }
   }
