@@ -708,47 +708,55 @@ struct Config {
   }
 };
 
-// Tile configurations, largest first, for up to 7 taps (k <= 7 convs, k = 2s transposed convs)
-// and up to 11 (the HiFiGAN k = 11 resblocks). The fused residual-unit form needs one column tile
-// that holds every channel (96: 1 x 4 waves of 96 x 64; 192: 2 x 2 waves of 96 x 64).
+// Tile configurations for up to 7 taps (k <= 7 convs, k = 2s transposed convs) and up to 11 (the
+// HiFiGAN k = 11 resblocks). The fused residual-unit form needs one column tile that holds every
+// channel (96: 1 x 4 waves of 96 x 48; 192: 2 x 4 waves of 96 x 32).
 template <int T>
 struct Configs {
-  // register budgets (accumulators + staging) keep two workgroups per CU, so one workgroup's
-  // stores drain while the other computes
-  using A = Config<1, 4, 6, 3, 192 + 2 * kMaxHalo, T>;  // 96 cols x 192 positions
-  using B = Config<2, 2, 4, 4, 128 + 3 * kMaxHalo, T>;  // 128 x 128
+  // register budgets (accumulators + staging) keep two waves per SIMD
+  using A = Config<1, 4, 6, 3, 192 + 2 * kMaxHalo, T>;  // 96 cols x 192 positions, 4 waves
+  using K = Config<2, 4, 6, 2, 128 + 4 * kMaxHalo, T>;  // 192 x 128, 8 waves
+  using H = Config<2, 4, 4, 4, 256 + 2 * kMaxHalo, T>;  // 128 x 256, 8 waves
   using C = Config<1, 4, 4, 4, 256 + 2 * kMaxHalo, T>;  // 64 x 256
+  using B = Config<2, 2, 4, 4, 128 + 3 * kMaxHalo, T>;  // 128 x 128
   using D = Config<2, 2, 4, 2, 64 + 4 * kMaxHalo, T>;   // 128 x 64
   using E = Config<2, 2, 2, 2, 64 + 4 * kMaxHalo, T>;   // 64 x 64
   using F = Config<4, 1, 2, 2, 32 + 4 * kMaxHalo, T>;   // 128 x 32
 
-  // The first configuration (in order of preference) that fills the chip (two workgroups per CU);
-  // failing that, the one with the most workgroups.
+  // The first configuration, in order of measured efficiency on MI355X, that fits, wastes at
+  // most an eighth of its column tiles and still gives at least half a workgroup per CU;
+  // failing that (small problems), the fitting one with the most workgroups.
   template <int IN, bool W_FP8>
   static int launch(const ConvParams& p, hipStream_t stream) {
-    constexpr int64_t target = 512;
-    int64_t best = -1;
-    int pick = -1;
-    auto consider = [&](int id, bool fits, int64_t wgs) {
-      if (!fits || (pick >= 0 && best >= target)) return;
-      if (wgs >= target || wgs > best) {
-        best = wgs;
-        pick = id;
+    constexpr int64_t min_wgs = 128;
+    int pick = -1, most = -1;
+    int64_t most_wgs = -1;
+    auto consider = [&](int id, bool fits, int64_t wgs, int bco) {
+      if (!fits) return;
+      const int64_t padded = (p.n_cols + bco - 1) / bco * bco;
+      if (pick < 0 && wgs >= min_wgs && (padded - p.n_cols) * 8 <= p.n_cols) pick = id;
+      if (wgs > most_wgs) {
+        most_wgs = wgs;
+        most = id;
       }
     };
-    if (p.n_cols % 96 == 0) consider(0, A::fits(p, false), A::workgroups(p));
-    consider(1, B::fits(p, false), B::workgroups(p));
-    consider(2, C::fits(p, false), C::workgroups(p));
-    consider(3, D::fits(p, false), D::workgroups(p));
-    consider(4, E::fits(p, false), E::workgroups(p));
-    consider(5, F::fits(p, false), F::workgroups(p));
-    switch (pick) {
+    consider(0, A::fits(p, false), A::workgroups(p), A::Tile::BCO);
+    consider(1, K::fits(p, false), K::workgroups(p), K::Tile::BCO);
+    consider(2, H::fits(p, false), H::workgroups(p), H::Tile::BCO);
+    consider(3, C::fits(p, false), C::workgroups(p), C::Tile::BCO);
+    consider(4, B::fits(p, false), B::workgroups(p), B::Tile::BCO);
+    consider(5, D::fits(p, false), D::workgroups(p), D::Tile::BCO);
+    consider(6, E::fits(p, false), E::workgroups(p), E::Tile::BCO);
+    consider(7, F::fits(p, false), F::workgroups(p), F::Tile::BCO);
+    switch (pick >= 0 ? pick : most) {
       case 0: return A::template launch<IN, W_FP8, false>(p, stream);
-      case 1: return B::template launch<IN, W_FP8, false>(p, stream);
-      case 2: return C::template launch<IN, W_FP8, false>(p, stream);
-      case 3: return D::template launch<IN, W_FP8, false>(p, stream);
-      case 4: return E::template launch<IN, W_FP8, false>(p, stream);
-      case 5: return F::template launch<IN, W_FP8, false>(p, stream);
+      case 1: return K::template launch<IN, W_FP8, false>(p, stream);
+      case 2: return H::template launch<IN, W_FP8, false>(p, stream);
+      case 3: return C::template launch<IN, W_FP8, false>(p, stream);
+      case 4: return B::template launch<IN, W_FP8, false>(p, stream);
+      case 5: return D::template launch<IN, W_FP8, false>(p, stream);
+      case 6: return E::template launch<IN, W_FP8, false>(p, stream);
+      case 7: return F::template launch<IN, W_FP8, false>(p, stream);
       default: return OMNI_ERR_UNSUPPORTED;
     }
   }
@@ -756,7 +764,7 @@ struct Configs {
 
 using ResidualUnit96 = Config<1, 4, 6, 3, 192 + 2 * kMaxHalo, 7>;       // fused, 96 channels
 using ResidualUnit96Short = Config<1, 2, 6, 1, 32 + 4 * kMaxHalo, 7>;   // short rows
-using ResidualUnit192 = Config<2, 2, 6, 3, 96 + 3 * kMaxHalo, 7>;       // fused, 192 channels
+using ResidualUnit192 = Config<2, 4, 6, 2, 128 + 3 * kMaxHalo, 7>;      // fused, 192 channels
 using ResidualUnit192Short = Config<2, 2, 6, 1, 32 + 4 * kMaxHalo, 7>;  // short rows
 
 // Launchers, one translation unit each (they compile in parallel): taps <= 7 for each input and
