@@ -334,6 +334,9 @@ class DacCodecDecoder:
                 continue
             for unit in blk.units:
                 c1 = unit.conv1
+                # the block's last unit: only its Snake output is read again (by the next
+                # block's up conv), so the residual stream is not written back
+                x_out = None if unit is blk.units[-1] else x
                 flops = 2.0 * batch * length * (c1.conv.macs_per_position +
                                                 unit.conv2.macs_per_position)
                 u_next = self._view(ws.u[1 - cur], batch, length, c)
@@ -343,7 +346,7 @@ class DacCodecDecoder:
                         with timer.launch(f"unit{c}", flops, c1.name):
                             fused_conv(u, c1.conv, u_next, second=unit.conv2,
                                        mid_activation=snake, mid_a=unit.mid_a, mid_b=unit.mid_b,
-                                       residual=x, sum_out=x, activation=snake,
+                                       residual=x, sum_out=x_out, activation=snake,
                                        act_a=unit.next_a, act_b=unit.next_b, **hist(c1.name))
                         fused = True
                     except N.OmniCodecError as err:
@@ -358,8 +361,8 @@ class DacCodecDecoder:
                                    act_b=unit.mid_b, **hist(c1.name))
                     with timer.launch("conv", 2.0 * batch * length * unit.conv2.macs_per_position,
                                       c1.name.replace("conv1", "conv2")):
-                        fused_conv(h, unit.conv2, u_next, residual=x, sum_out=x, activation=snake,
-                                   act_a=unit.next_a, act_b=unit.next_b)
+                        fused_conv(h, unit.conv2, u_next, residual=x, sum_out=x_out,
+                                   activation=snake, act_a=unit.next_a, act_b=unit.next_b)
                 cur = 1 - cur
                 u = u_next
         wave = torch.empty(batch, 1, length, dtype=torch.float32, device=self.device)
