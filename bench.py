@@ -15,7 +15,9 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
   cpu_baseline  the float32 CPU restatement of the reference path (oracle/codec_oracle.py) timed
                 on this host's cores on a bounded sample of the same workload.
 
---workload selects another configuration (single24k, hifigan, fp8long) for manual runs.
+--only stack96 / --only copy run one kernel alone for hardware-counter profiles: the roofline
+kernel (the 96-channel residual stack of the same decoder, x [64, 23040, 96]) or a plain 1 GiB
+device copy (the calibration of the FETCH_SIZE / WRITE_SIZE counters), --launches times each.
 """
 
 from __future__ import annotations
@@ -194,7 +196,7 @@ def bench_streaming(args, device) -> dict:
                    "channels": 1536, "strides": [8, 8, 5, 6], "weights": "bf16"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": PMC_TRAFFIC_BYTES.get(dom_kind),
                      "kernel": KERNEL_NAMES.get(dom_kind, dom_kind),
                      "launches_per_step": dom["launches"] / inst_steps,
                      "flops_per_launch": dom_flops_launch, "mean_launch_ms": dom_ms_launch},
@@ -212,6 +214,47 @@ def bench_streaming(args, device) -> dict:
     return result
 
 
+# HBM bytes per launch of the roofline kernel, from two rocprofv3 --pmc runs of
+# `bench.py --only stack96` (FETCH_SIZE, then WRITE_SIZE), each scaled by the same counter's
+# reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB, WRITE_SIZE =
+# 1024 MiB: fetch x 2, write x 1); profiles/residual_stack96_pmc.md.
+PMC_TRAFFIC_BYTES = {"stack96": (435630 * 2 + 276480) * 1024}
+
+
+def run_only(args, device) -> None:
+    from sglang_omni_amd.kernels.conv import residual_stack
+    from sglang_omni_amd.models import DacCodecDecoder, make_dac_weights
+    from sglang_omni_amd.models.configs import CODEC_24K
+
+    if args.only == "copy":
+        a = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=device)
+        b = torch.empty_like(a)
+        fn = lambda: b.copy_(a)  # noqa: E731
+        what = "1 GiB copy"
+    else:
+        decoder = DacCodecDecoder(make_dac_weights(CODEC_24K, seed=0), CODEC_24K, device=device)
+        blk = decoder.blocks[-1]
+        if blk.stack is None or blk.c_out != 96:
+            raise SystemExit("the decoder's last block runs no 96-channel residual stack")
+        gen = torch.Generator().manual_seed(0)
+        x = (torch.randn(STREAMS, 23040, 96, generator=gen) * 0.3).to(device)
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=device)
+        last = blk.units[-1]
+        fn = lambda: residual_stack(x, blk.stack, out, last.next_a, last.next_b)  # noqa: E731
+        what = "residual stack, 96 channels, x [64, 23040, 96]"
+    for _ in range(2):
+        fn()
+    sync()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.launches):
+        fn()
+    end.record()
+    sync()
+    log(f"{what}: {start.elapsed_time(end) * 1e3 / args.launches:.1f} us per launch "
+        f"({args.launches} launches after 2 warmups)")
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -220,6 +263,9 @@ def main() -> None:
     parser.add_argument("--workload", default="streaming64")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-rvq-large", action="store_true")
+    parser.add_argument("--only", choices=["stack96", "copy"],
+                        help="run one kernel alone (hardware-counter profiles); prints no JSON")
+    parser.add_argument("--launches", type=int, default=2)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for "
@@ -231,6 +277,9 @@ def main() -> None:
         sys.exit(1)
     device = torch.device("cuda", 0)
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.only:
+        run_only(args, device)
+        return
     if args.workload != "streaming64":
         raise SystemExit(f"unknown workload {args.workload}")
     r = bench_streaming(args, device)
