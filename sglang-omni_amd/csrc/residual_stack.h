@@ -86,7 +86,7 @@ __device__ __forceinline__ int uaddr(int kc, int row, int slot) {
   return (kc * UROWS + row) * kChunk + ((slot ^ ((row >> 2) & 3)) << 3);
 }
 
-template <int C, int WCO, int WP, int TP>
+template <int C, int WCO, int WP, int TP, bool DMA = false>
 struct StackTile {
   static constexpr int NT = 64 * WCO * WP;
   static constexpr int TCO = C / (16 * WCO);
@@ -97,7 +97,17 @@ struct StackTile {
   static constexpr int W1_PIECES = (C * kTaps * 4 + NT - 1) / NT;
   static constexpr int W2_PIECES = (C * C / 8 + NT - 1) / NT;
   static constexpr int WPR = W1_PIECES > W2_PIECES ? W1_PIECES : W2_PIECES;
-  static constexpr int W_ELEMS = C * WROW > CH * C * kChunk ? C * WROW : CH * C * kChunk;
+  // LDS DMA ring (bf16 weights): two buffers, each holding one stage of weights: the dilated
+  // conv's chunk kc for taps 0-3 or 4-6 ([C][ntaps * 32 + 8], rows an odd multiple of 16 bytes)
+  // or the k = 1 conv ([C/32][C][32]); a stage is whole 64-lane DMA instructions of 16 bytes.
+  static constexpr int P_LO = 4 * 4 + 1;  // 16-byte slots per weight row, taps 0-3 (+1 pad)
+  static constexpr int P_HI = 3 * 4 + 1;  // taps 4-6
+  static constexpr int RING_SLOTS = (C * P_LO + 63) / 64 * 64;
+  static constexpr int RING_ELEMS = RING_SLOTS * 8;
+  static constexpr int STAGES = 7;  // per unit: 3 chunks x 2 tap halves, then the k = 1 conv
+  static_assert(CH * C * 4 <= RING_SLOTS, "the k = 1 weights fit one ring buffer");
+  static constexpr int W_ELEMS = DMA ? 2 * RING_ELEMS
+                                     : (C * WROW > CH * C * kChunk ? C * WROW : CH * C * kChunk);
   static constexpr int COEF = (kMaxUnits * kCoefRows + 2) * C;  // floats
   static constexpr size_t lds_bytes() {
     return (size_t)CH * UROWS * kChunk * 2 + (size_t)W_ELEMS * 2 + (size_t)COEF * 4;
@@ -105,9 +115,10 @@ struct StackTile {
   static_assert(C % (16 * WCO) == 0 && C % kChunk == 0, "tile shape");
 };
 
-template <int C, int WCO, int WP, int TP, bool W_FP8>
+template <int C, int WCO, int WP, int TP, bool W_FP8, bool DMA>
 __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const StackParams p) {
-  using Tile = StackTile<C, WCO, WP, TP>;
+  static_assert(!(DMA && W_FP8), "the DMA ring copies bf16 weights as they are");
+  using Tile = StackTile<C, WCO, WP, TP, DMA>;
   constexpr int NT = Tile::NT;
   constexpr int TCO = Tile::TCO;
   constexpr int CH = Tile::CH;
@@ -254,6 +265,53 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       if (piece < C * C / 8) *reinterpret_cast<u32x4*>(ws + piece * 8) = wpiece(u);
     }
   };
+  // DMA of weight stage g (g = unit * 7 + r: r < 6 the dilated conv's chunk r / 2, taps 0-3 or
+  // 4-6; r = 6 the k = 1 conv) into ring buffer g % 2: this wave's share of the stage's 64-lane
+  // 16-byte instructions. Lane i of an instruction fills ring slot 64 * instr + i, so each lane
+  // loads the global piece that belongs in its slot (pad slots reload the chunk's first piece).
+  const int nwaves = NT / 64;
+  auto dma_stage = [&](int g) __attribute__((always_inline)) {
+    if constexpr (DMA) {
+      const int k = g / Tile::STAGES;
+      const int r = g - k * Tile::STAGES;
+      if (k >= p.nunits) return;
+      u16* buf = ws + (g & 1) * Tile::RING_ELEMS;
+      if (r < 6) {
+        const int kc = r >> 1;
+        const int t0 = (r & 1) ? 4 : 0;
+        const int nt = (r & 1) ? 3 : 4;
+        const int P = nt * 4 + 1;
+        const auto rs = buffer_rsrc(p.unit[k].w1, p.unit[k].w1_bytes);
+        const int instrs = (C * P + 63) / 64;
+        for (int di = wave; di < instrs; di += nwaves) {
+          const int slot = di * 64 + lane;
+          const int n = slot / P;
+          const int j = slot - n * P;
+          const bool real = n < C && j < nt * 4;
+          const uint32_t off =
+              real ? (uint32_t)((((kc * C + n) * kTaps + t0 + (j >> 2)) * kChunk + (j & 3) * 8) * 2)
+                   : (uint32_t)(kc * C * kTaps * kChunk * 2);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16, off, 0, 0, 0);
+        }
+      } else {
+        const auto rs = buffer_rsrc(p.unit[k].w2, p.unit[k].w2_bytes);
+        constexpr int instrs = CH * C * 4 / 64;
+        for (int di = wave; di < instrs; di += nwaves)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16,
+              (uint32_t)((di * 64 + lane) * 16), 0, 0, 0);
+      }
+    }
+  };
+  // Start of weight stage g: this wave's DMA of stage g is complete, then every wave's (the
+  // barrier), which also retires every read of the other buffer; stage g + 1 goes into it.
+  auto stage_begin = [&](int g) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    dma_stage(g + 1);
+  };
+
   // LDS addressing of the operand tile from the accumulator layout. Staged rows of this lane are
   // kGuard + wave_p * TP * 16 + t * 16 + lrow, so the slot rotation (row / 4) % 4 is the lane's
   // (lrow / 4) % 4 for every t: each access is a per-lane base plus a compile-time offset.
@@ -273,7 +331,8 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     *reinterpret_cast<uint2*>(us + base + (c >> 1) * UROWS * kChunk + t * 16 * kChunk) = o;
   };
 
-  load_w1(0, 0);
+  if constexpr (DMA) dma_stage(0);
+  else load_w1(0, 0);
   __syncthreads();  // coefficients and guard rows
   // unit 0's operand
 #pragma unroll
@@ -344,30 +403,59 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     for (int c = 0; c < TCO; ++c)
 #pragma unroll
       for (int t = 0; t < TP; ++t) acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kc = 0; kc < CH; ++kc) {
-      if (kc > 0) __syncthreads();  // the previous chunk's weights are no longer read
-      store_w1();
-      __syncthreads();
-      if (kc + 1 < CH) load_w1(k, kc + 1);
-      else load_w2(k);
-      const u16* wtap = ws + (wco0 + lrow) * WROW + lk;
-      const u16* ukc = us + kc * UROWS * kChunk;
+    if constexpr (DMA) {
+      for (int r = 0; r < 6; ++r) {
+        const int g = k * Tile::STAGES + r;
+        stage_begin(g);
+        const int kc = r >> 1;
+        const int t0 = (r & 1) ? 4 : 0;
+        const int nt = (r & 1) ? 3 : 4;
+        const int P8 = (nt * 4 + 1) * 8;  // elements per weight row
+        const u16* wtap = ws + (g & 1) * Tile::RING_ELEMS + (wco0 + lrow) * P8 + lk;
+        const u16* ukc = us + kc * UROWS * kChunk;
 #pragma unroll 1
-      for (int j = 0; j < kTaps; ++j) {
-        bf16x8 a[TCO];
+        for (int jj = 0; jj < nt; ++jj) {
+          bf16x8 a[TCO];
 #pragma unroll
-        for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * WROW);
-        // rows row0 + j * d - h + 16 t: one rotation for every t
-        const int rj = row0 + j * d - h;
-        const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+          for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * P8);
+          const int rj = row0 + (t0 + jj) * d - h;
+          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
 #pragma unroll
-        for (int t = 0; t < TP; ++t) {
-          const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
+          for (int t = 0; t < TP; ++t) {
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
 #pragma unroll
-          for (int c = 0; c < TCO; ++c)
-            acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
+            for (int c = 0; c < TCO; ++c)
+              acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
+          }
+          wtap += kChunk;
         }
-        wtap += kChunk;
+      }
+    } else {
+      for (int kc = 0; kc < CH; ++kc) {
+        if (kc > 0) __syncthreads();  // the previous chunk's weights are no longer read
+        store_w1();
+        __syncthreads();
+        if (kc + 1 < CH) load_w1(k, kc + 1);
+        else load_w2(k);
+        const u16* wtap = ws + (wco0 + lrow) * WROW + lk;
+        const u16* ukc = us + kc * UROWS * kChunk;
+#pragma unroll 1
+        for (int j = 0; j < kTaps; ++j) {
+          bf16x8 a[TCO];
+#pragma unroll
+          for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * WROW);
+          // rows row0 + j * d - h + 16 t: one rotation for every t
+          const int rj = row0 + j * d - h;
+          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+#pragma unroll
+          for (int t = 0; t < TP; ++t) {
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
+#pragma unroll
+            for (int c = 0; c < TCO; ++c)
+              acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
+          }
+          wtap += kChunk;
+        }
       }
     }
     __syncthreads();  // the operand and the weights are no longer read
@@ -390,16 +478,24 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    store_w2();
-    __syncthreads();
-    if (k + 1 < p.nunits) load_w1(k + 1, 0);
+    const u16* w2s = ws;
+    if constexpr (DMA) {
+      // the k = 1 weights' stage (its DMA ran during the last tap half); h is complete too
+      const int g = k * Tile::STAGES + 6;
+      stage_begin(g);
+      w2s = ws + (g & 1) * Tile::RING_ELEMS;
+    } else {
+      store_w2();
+      __syncthreads();
+      if (k + 1 < p.nunits) load_w1(k + 1, 0);
+    }
     // (e) the k = 1 conv
 #pragma unroll
     for (int kc = 0; kc < CH; ++kc) {
       bf16x8 a[TCO];
 #pragma unroll
       for (int c = 0; c < TCO; ++c)
-        a[c] = *reinterpret_cast<const bf16x8*>(ws + (kc * C + wco0 + c * 16 + lrow) * kChunk + lk);
+        a[c] = *reinterpret_cast<const bf16x8*>(w2s + (kc * C + wco0 + c * 16 + lrow) * kChunk + lk);
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
         const bf16x8 bv = *reinterpret_cast<const bf16x8*>(
@@ -461,9 +557,12 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   }
 }
 
-// 96 channels: 8 waves, each with all 96 columns and 32 of the 256 staged rows (the register
-// budget of two waves per SIMD: x and the accumulators take 96 of them).
+// 96 channels, 8 waves, each with all 96 columns. fp8 weights are converted to bf16 on their way
+// to LDS, so they are staged through registers, and the register budget of two waves per SIMD
+// (x and the accumulators) leaves 32 of 256 staged rows per wave; bf16 weights arrive by LDS
+// DMA, which frees the staging registers: 48 of 384 rows per wave.
 using Stack96 = StackTile<96, 1, 8, 2>;
+using Stack96Dma = StackTile<96, 1, 8, 3, true>;
 
 template <bool W_FP8>
 int launch_stack96(const StackParams& p, int grid, hipStream_t stream);

@@ -46,7 +46,8 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   if (any_hist && (!a->slot_index || !a->slot_parity || a->hist_num_slots < 1))
     return OMNI_ERR_INVALID_ARG;
   if (a->batch == 0 || a->length == 0) return OMNI_OK;
-  if (H + 16 > Stack96::R) return OMNI_ERR_UNSUPPORTED;
+  const int64_t R = fp8 ? Stack96::R : Stack96Dma::R;  // staged rows per tile
+  if (H + 16 > R) return OMNI_ERR_UNSUPPORTED;
 
   // byte extents (buffer offsets are 32-bit)
   const int64_t B = a->batch, L = a->length;
@@ -109,7 +110,6 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
 
   // Long rows: tiles inside one row, as many as the staged rows need, evened out; short rows:
   // as many whole rows (each with its halo) as the staged rows hold.
-  constexpr int64_t R = Stack96::R;
   int64_t grid;
   if (L + H > R) {
     const int64_t tiles = (L + (R - H) - 1) / (R - H);

@@ -5,10 +5,10 @@ namespace omni_stack {
 
 template <>
 int launch_stack96<false>(const StackParams& p, int grid, hipStream_t stream) {
-  auto k = residual_stack_kernel<96, 1, 8, 2, false>;
+  auto k = residual_stack_kernel<96, 1, 8, 3, false, true>;
   static const bool raised = omni_conv::raise_lds_limit((const void*)k);
   (void)raised;
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(Stack96::NT), Stack96::lds_bytes(), stream, p);
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(Stack96Dma::NT), Stack96Dma::lds_bytes(), stream, p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
 }

@@ -5,7 +5,7 @@ namespace omni_stack {
 
 template <>
 int launch_stack96<true>(const StackParams& p, int grid, hipStream_t stream) {
-  auto k = residual_stack_kernel<96, 1, 8, 2, true>;
+  auto k = residual_stack_kernel<96, 1, 8, 2, true, false>;
   static const bool raised = omni_conv::raise_lds_limit((const void*)k);
   (void)raised;
   hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(Stack96::NT), Stack96::lds_bytes(), stream, p);
