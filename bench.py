@@ -13,7 +13,10 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
                 timed with HIP events on the launch stream;
   rvq_gather    the RVQ gather-sum's achieved bytes/s, in the step and on a large batch;
   cpu_baseline  the float32 CPU restatement of the reference path (oracle/codec_oracle.py) timed
-                on this host's cores on a bounded sample of the same workload.
+                on this host's cores on a bounded sample of the same workload;
+  other_configs the xRT of the other decoder configurations: the single 20 s utterance, the
+                HiFiGAN mel vocoder (16 x 10 s) and the fp8-weight long form (8 x 120 s);
+  calibration   the box's practical peaks: a 1 GiB copy and a bf16 8192^3 GEMM.
 
 --only stack96 / --only copy run one kernel alone for hardware-counter profiles: the roofline
 kernel (the 96-channel residual stack of the same decoder, x [64, 23040, 96]) or a plain 1 GiB
@@ -218,7 +221,7 @@ def bench_streaming(args, device) -> dict:
 # `bench.py --only stack96` (FETCH_SIZE, then WRITE_SIZE), each scaled by the same counter's
 # reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB, WRITE_SIZE =
 # 1024 MiB: fetch x 2, write x 1); profiles/residual_stack96_pmc.md.
-PMC_TRAFFIC_BYTES = {"stack96": (435630 * 2 + 276480) * 1024}
+PMC_TRAFFIC_BYTES = {"stack96": (380356 * 2 + 276480) * 1024}
 
 
 def run_only(args, device) -> None:
@@ -255,6 +258,60 @@ def run_only(args, device) -> None:
         f"({args.launches} launches after 2 warmups)")
 
 
+def timed_call(fn, reps: int = 3) -> float:
+    fn()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    sync()
+    return (time.perf_counter() - t0) / reps
+
+
+def bench_other_configs(device) -> dict:
+    """xRT of the other decoder configurations (one call each, inputs resident in HBM)."""
+    from sglang_omni_amd.models import (DacCodecDecoder, HifiGanVocoder, make_dac_weights,
+                                        make_hifigan_weights)
+    from sglang_omni_amd.models.configs import CODEC_24K, CODEC_24K_LONG, HIFIGAN_24K
+
+    out = {}
+    gen = torch.Generator().manual_seed(0)
+    dec = DacCodecDecoder(make_dac_weights(CODEC_24K, seed=0), CODEC_24K, device=device)
+    codes = torch.randint(0, 2048, (1, 16, 250), generator=gen).to(device)
+    dt = timed_call(lambda: dec.from_indices(codes))
+    out["single_utterance"] = {"workload": "24 kHz codec, 1 x 250 frames (20 s), bf16",
+                               "xRT": round(20.0 / dt, 1), "ms": round(dt * 1e3, 3)}
+    del dec
+    voc = HifiGanVocoder(make_hifigan_weights(HIFIGAN_24K, seed=0), HIFIGAN_24K, device=device)
+    mel = (torch.randn(16, 80, 500, generator=gen) * 2 - 5).to(device)
+    dt = timed_call(lambda: voc(mel))
+    out["hifigan"] = {"workload": "HiFiGAN mel->wave, 16 x 500 mel frames (160 s), bf16",
+                      "xRT": round(160.0 / dt, 1), "ms": round(dt * 1e3, 3)}
+    del voc
+    dec = DacCodecDecoder(make_dac_weights(CODEC_24K_LONG, seed=0), CODEC_24K_LONG,
+                          device=device, weight_format="fp8")
+    codes = torch.randint(0, 1024, (8, 32, 1500), generator=gen).to(device)
+    dt = timed_call(lambda: dec.from_indices(codes), reps=2)
+    out["fp8_long_form"] = {"workload": "24 kHz codec, fp8 e4m3 weights, 8 x 1500 frames "
+                                        "(960 s), whole utterances",
+                            "xRT": round(960.0 / dt, 1), "ms": round(dt * 1e3, 3)}
+    return out
+
+
+def calibrate(device) -> dict:
+    """The box's practical peaks: a 1 GiB device copy (HBM) and a 8192^3 bf16 GEMM (torch's
+    hipBLASLt, the MFMA reference point)."""
+    a = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=device)
+    b = torch.empty_like(a)
+    dt = timed_call(lambda: b.copy_(a), reps=5)
+    copy = 2.0 * a.numel() * 4 / dt / 1e9
+    del a, b
+    x = torch.randn(8192, 8192, device=device).to(torch.bfloat16)
+    y = torch.randn(8192, 8192, device=device).to(torch.bfloat16)
+    dt = timed_call(lambda: torch.matmul(x, y), reps=5)
+    return {"copy_GBps": round(copy, 1), "bf16_gemm_8192_TFLOPs": round(2.0 * 8192 ** 3 / dt / 1e12, 1)}
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -266,6 +323,8 @@ def main() -> None:
     parser.add_argument("--only", choices=["stack96", "copy"],
                         help="run one kernel alone (hardware-counter profiles); prints no JSON")
     parser.add_argument("--launches", type=int, default=2)
+    parser.add_argument("--no-other-configs", action="store_true",
+                        help="skip the xRT of the other configurations and the peak calibration")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for "
@@ -304,6 +363,10 @@ def main() -> None:
     }
     if "cpu_baseline" in r:
         line["cpu_baseline"] = r["cpu_baseline"]
+    if not args.no_other_configs:
+        log("other configurations ...")
+        line["other_configs"] = bench_other_configs(device)
+        line["calibration"] = calibrate(device)
     print(json.dumps(line), flush=True)
 
 

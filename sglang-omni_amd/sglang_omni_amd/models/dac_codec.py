@@ -378,11 +378,35 @@ class DacCodecDecoder:
                                            N.stream_handle(self.device)), "omni_advance_slots")
         return wave
 
+    # the largest activation buffer of one call stays below this many bytes (the kernels address
+    # each buffer with 32-bit byte offsets)
+    MAX_BUFFER_BYTES = 1 << 30
+
+    def frames_per_call(self, batch: int) -> int:
+        """Frames one decode call takes for ``batch`` rows: longer inputs are decoded in chunks of
+        this many frames through per-row slot state, which gives the same bits."""
+        per_frame, samples = 0, 1
+        for blk in self.blocks:
+            samples *= blk.stride
+            per_frame = max(per_frame, samples * blk.c_out * 4)
+        return max(1, self.MAX_BUFFER_BYTES // (max(batch, 1) * per_frame))
+
     @torch.no_grad()
     def from_indices(self, indices: torch.Tensor) -> torch.Tensor:
         """[B, Q, T] codes -> [B, 1, T * frame_length] float32 waveform (``DAC.from_indices``,
         modded_dac.py:990-992). Codes above the codebook size read its last entry."""
-        return self._decode(indices, None)
+        if indices.dim() != 3:
+            raise ValueError(f"codes must be [B, Q, T], got {tuple(indices.shape)}")
+        batch, _, frames = indices.shape
+        step = self.frames_per_call(batch)
+        if frames <= step:
+            return self._decode(indices, None)
+        pool = self.new_state_pool(num_slots=batch)
+        rows = torch.arange(batch, device=self.device)
+        parts = [self._decode(indices[..., s:s + step],
+                              {"pool": pool, "slot_index": rows, "cold": s == 0})
+                 for s in range(0, frames, step)]
+        return torch.cat(parts, dim=-1)
 
     __call__ = from_indices
 

@@ -262,3 +262,21 @@ def test_residual_stacks_decode_like_one_launch_per_unit(gpu, config):
         outs.append(torch.cat([dec.decode_slots(codes[..., s:s + 8], pool, idx,
                                                 first_decode=s == 0) for s in (0, 8, 16)], -1))
     assert torch.equal(outs[0], outs[1])
+
+
+def test_long_inputs_decode_in_chunks_with_the_whole_decodes_bits(gpu):
+    """from_indices splits inputs longer than its buffers allow into frame chunks through slot
+    state; forcing small chunks gives the single call's bits."""
+    weights = make_dac_weights(TINY_FUSED, seed=0)
+    decoder = DacCodecDecoder(weights, TINY_FUSED, device=gpu)
+    gen = torch.Generator().manual_seed(11)
+    codes = torch.randint(0, 64, (3, 4, 23), generator=gen).to(gpu)
+    whole = decoder.from_indices(codes)
+    per_frame, samples = 0, 1  # bytes of the largest float32 activation per frame
+    for rate, channels in zip(TINY_FUSED.rates, TINY_FUSED.stage_channels()[1:]):
+        samples *= rate
+        per_frame = max(per_frame, samples * channels * 4)
+    for frames in (1, 6):
+        decoder.MAX_BUFFER_BYTES = 3 * frames * per_frame
+        assert decoder.frames_per_call(3) == frames
+        assert torch.equal(decoder.from_indices(codes), whole)
