@@ -722,10 +722,13 @@ struct Configs {
   using D = Config<2, 2, 4, 2, 64 + 4 * kMaxHalo, T>;   // 128 x 64
   using E = Config<2, 2, 2, 2, 64 + 4 * kMaxHalo, T>;   // 64 x 64
   using F = Config<4, 1, 2, 2, 32 + 4 * kMaxHalo, T>;   // 128 x 32
+  using S = Config<1, 8, 2, 4, 512 + 2 * kMaxHalo, T>;  // 32 x 512, 8 waves (32-channel layers)
 
   // The first configuration, in order of measured efficiency on MI355X, that fits, wastes at
   // most an eighth of its column tiles and still gives at least half a workgroup per CU;
-  // failing that (small problems), the fitting one with the most workgroups.
+  // failing that (small problems), the fitting one with the most workgroups. The 32-column tile
+  // comes last: it is for layers with 32 output columns, where every wider tile wastes most of
+  // its matrix work.
   template <int IN, bool W_FP8>
   static int launch(const ConvParams& p, hipStream_t stream) {
     constexpr int64_t min_wgs = 128;
@@ -748,6 +751,7 @@ struct Configs {
     consider(5, D::fits(p, false), D::workgroups(p), D::Tile::BCO);
     consider(6, E::fits(p, false), E::workgroups(p), E::Tile::BCO);
     consider(7, F::fits(p, false), F::workgroups(p), F::Tile::BCO);
+    consider(8, S::fits(p, false), S::workgroups(p), S::Tile::BCO);
     switch (pick >= 0 ? pick : most) {
       case 0: return A::template launch<IN, W_FP8, false>(p, stream);
       case 1: return K::template launch<IN, W_FP8, false>(p, stream);
@@ -757,6 +761,7 @@ struct Configs {
       case 5: return D::template launch<IN, W_FP8, false>(p, stream);
       case 6: return E::template launch<IN, W_FP8, false>(p, stream);
       case 7: return F::template launch<IN, W_FP8, false>(p, stream);
+      case 8: return S::template launch<IN, W_FP8, false>(p, stream);
       default: return OMNI_ERR_UNSUPPORTED;
     }
   }
