@@ -1,5 +1,6 @@
 // C ABI of the fused convolution: argument validation and the choice of kernel configuration.
 // The kernel template and its tile configurations are in conv_kernel.h.
+#include "conv_dma.h"
 #include "conv_kernel.h"
 
 namespace omni_conv {
@@ -8,6 +9,13 @@ namespace {
 int dispatch(const ConvParams& p, bool x_f32, bool fp8, bool fuse2, hipStream_t stream) {
   if (p.halo > kMaxHalo) return OMNI_ERR_UNSUPPORTED;
   const int in_mode = x_f32 ? IN_F32 : (p.in_act != OMNI_ACT_NONE ? IN_ACT : IN_RAW);
+  if (in_mode == IN_RAW && !fp8 && !fuse2 && p.c_in % kChunk == 0) {
+    int status = OMNI_ERR_UNSUPPORTED;
+    if (p.taps == 7) status = launch_dma_taps7(p, stream);
+    else if (p.taps == 2) status = launch_dma_taps2(p, stream);
+    else if (p.taps == 1) status = launch_dma_taps1(p, stream);
+    if (status != OMNI_ERR_UNSUPPORTED) return status;
+  }
   if (fuse2) return fp8 ? launch_fused<true>(p, in_mode, stream) : launch_fused<false>(p, in_mode, stream);
   if (p.taps <= 7) {
     switch (in_mode) {
@@ -30,8 +38,11 @@ bool valid_act(int act, const float* a, const float* b) {
 }  // namespace
 }  // namespace omni_conv
 
-extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) {
-  using namespace omni_conv;
+namespace omni_conv {
+
+// Validates the C-ABI arguments and fills the kernel parameters; OMNI_OK when there is work to
+// launch, OMNI_ERR_* on a contract violation, and -1 when the call is valid but empty.
+int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& fp8, bool& fuse2) {
   if (!a || !a->x || !a->weight) return OMNI_ERR_INVALID_ARG;
   if (!a->out && !a->sum_out) return OMNI_ERR_INVALID_ARG;
   if (a->batch < 0 || a->length < 0 || a->c_in < 1 || a->n_cols < 1 || a->c_out < 1 ||
@@ -41,7 +52,7 @@ extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) 
     return OMNI_ERR_UNSUPPORTED;
   if (a->left_pad > (a->taps - 1) * a->dilation) return OMNI_ERR_INVALID_ARG;
   if (a->x_dtype != OMNI_DTYPE_BF16 && a->x_dtype != OMNI_DTYPE_F32) return OMNI_ERR_INVALID_ARG;
-  const bool x_f32 = a->x_dtype == OMNI_DTYPE_F32;
+  x_f32 = a->x_dtype == OMNI_DTYPE_F32;
   if (a->in_activation != OMNI_ACTIVATION_NONE && a->in_activation != OMNI_ACTIVATION_SNAKE &&
       a->in_activation != OMNI_ACTIVATION_LEAKY_RELU)
     return OMNI_ERR_INVALID_ARG;
@@ -51,9 +62,9 @@ extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) 
     return OMNI_ERR_INVALID_ARG;
   if (a->weight_dtype != OMNI_DTYPE_BF16 && a->weight_dtype != OMNI_DTYPE_FP8_E4M3)
     return OMNI_ERR_INVALID_ARG;
-  const bool fp8 = a->weight_dtype == OMNI_DTYPE_FP8_E4M3;
+  fp8 = a->weight_dtype == OMNI_DTYPE_FP8_E4M3;
   if (fp8 && !a->weight_scale) return OMNI_ERR_INVALID_ARG;
-  const bool fuse2 = a->weight2 != nullptr;
+  fuse2 = a->weight2 != nullptr;
   if (fuse2) {
     if (a->n_cols != a->c_out || (fp8 && !a->weight2_scale) || !aligned16(a->weight2))
       return OMNI_ERR_INVALID_ARG;
@@ -89,7 +100,7 @@ extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) 
     if (a->hist_slot_stride < 2 * a->left_pad * a->c_in || a->hist_slot_stride % 8)
       return OMNI_ERR_INVALID_ARG;
   }
-  if (a->batch == 0 || a->length == 0) return OMNI_OK;
+  if (a->batch == 0 || a->length == 0) return -1;
   const int64_t x_length = a->x_length ? a->x_length : a->length;
   // byte extents of every buffer the kernel touches; buffer offsets are 32-bit
   const int64_t x_elem = x_f32 ? 4 : 2, w_elem = fp8 ? 1 : 2;
@@ -120,7 +131,7 @@ extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) 
       (a->hist_pool && a->hist_num_slots * a->hist_slot_stride > 0x7fffffffLL))
     return OMNI_ERR_UNSUPPORTED;
 
-  ConvParams p{};
+  p = ConvParams{};
   p.x = a->x;
   p.x_sb = a->x_stride_b;
   p.x_st = a->x_stride_t;
@@ -175,5 +186,16 @@ extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) 
   p.hist_bytes = (uint32_t)hist_bytes;
   p.r_bytes = (uint32_t)r_bytes;
   p.o_bytes = (uint32_t)o_bytes;
+  return OMNI_OK;
+}
+
+}  // namespace omni_conv
+
+extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) {
+  using namespace omni_conv;
+  ConvParams p;
+  bool x_f32 = false, fp8 = false, fuse2 = false;
+  const int status = make_conv_params(a, p, x_f32, fp8, fuse2);
+  if (status != OMNI_OK) return status < 0 ? OMNI_OK : status;
   return dispatch(p, x_f32, fp8, fuse2, reinterpret_cast<hipStream_t>(stream));
 }

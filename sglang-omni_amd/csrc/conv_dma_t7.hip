@@ -1,0 +1,13 @@
+// LDS-DMA convolution kernels for k = 7 convs (bf16 operand and weights).
+#include "conv_dma.h"
+
+namespace omni_conv {
+
+int launch_dma_taps7(const ConvParams& p, hipStream_t stream) {
+  // 96 columns x 384 positions, 8 waves of 96 x 48 (two per SIMD); 96 x 192, 4 waves of 96 x 48;
+  // 96 x 256, 8 waves of 96 x 32 (staged rows: positions plus a halo of up to 54 per segment)
+  return launch_first_fit<DmaConfig<1, 8, 6, 3, 496, 7, 1>, DmaConfig<1, 4, 6, 3, 368, 7, 1>,
+                          DmaConfig<1, 8, 6, 2, 480, 7, 1>>(p, stream);
+}
+
+}  // namespace omni_conv

@@ -143,7 +143,7 @@ struct ConvTile {
   // Per-column epilogue coefficients, staged once per workgroup at the end of LDS: rows
   // scale, bias, mid_a, mid_b, scale2, bias2, act_a, act_b of BCO floats each (the Snake
   // frequencies mid_a and act_a in revolutions).
-  static constexpr int NCOEF = 8;
+  static constexpr int NCOEF = 8;  // kNumCoefRows
   static constexpr size_t coef_bytes() { return (size_t)NCOEF * BCO * 4; }
   static constexpr size_t coef_offset(int64_t rows, int64_t taps, bool fuse2) {
     return lds_bytes(rows, taps, fuse2) - coef_bytes();
@@ -153,6 +153,163 @@ struct ConvTile {
 // The activation the staging applies to an input element of channel c.
 __device__ __forceinline__ float in_activation(int act, float v, float a, float b, float slope) {
   return operand_act(act, v, a, b, slope);
+}
+
+// Rows of the per-column epilogue coefficient table (ConvTile::NCOEF rows of BCO floats).
+enum CoefRow { kScale, kBias, kMidA, kMidB, kScale2, kBias2, kActA, kActB, kNumCoefRows };
+
+// The epilogue's per-column coefficients of column tile n0 into LDS (visible after the caller's
+// next barrier): the fp8 weight scale, bias, the fused k = 1 conv's middle Snake, scale and bias,
+// and the output activation's coefficients (Snake frequencies in revolutions).
+template <int BCO, int NT, bool FUSE2>
+__device__ __forceinline__ void stage_coefficients(const ConvParams& p, float* coef, int n0) {
+  const int tid = threadIdx.x;
+  const int n_cols = p.n_cols;
+  for (int e = tid; e < kNumCoefRows * BCO; e += NT) {
+    const int k = e / BCO;
+    const int j = e - k * BCO;
+    const int n = n0 + j;
+    const bool real = n < n_cols;
+    const int co = real ? n % p.c_out : 0;
+    float v = (k == kScale || k == kScale2) ? 1.f : 0.f;
+    if (real) {
+      switch (k) {
+        case kScale: if (p.wscale) v = p.wscale[n]; break;
+        case kBias: if (p.bias) v = p.bias[co]; break;
+        case kMidA: if (FUSE2 && p.mid_a) v = p.mid_a[co] * kInvTwoPi; break;
+        case kMidB: if (FUSE2 && p.mid_b) v = p.mid_b[co]; break;
+        case kScale2: if (FUSE2 && p.wscale2) v = p.wscale2[n]; break;
+        case kBias2: if (FUSE2 && p.bias2) v = p.bias2[co]; break;
+        case kActA: if (p.act_a) v = p.act_a[co] * kInvTwoPi; break;
+        default: if (p.act_b) v = p.act_b[co]; break;
+      }
+    }
+    coef[e] = v;
+  }
+}
+
+// The epilogue shared by the conv kernels, from the accumulators of a BCO x BP tile (column
+// tile n0, positions [m0, m_end)) to HBM, in two steps per pass over half the position waves:
+// (1) in the accumulator layout (lane = position, 4 consecutive columns per lane) each wave adds
+// the weight scale and bias and writes float32 rows into LDS; (2) the workgroup walks those rows
+// 16 bytes per thread, so the residual / mix loads and the sum_out / out stores are whole
+// contiguous rows of HBM. `lds` must be free for Tile::EPI_ROWS x Tile::EPITCH floats (the first
+// pass begins with a barrier); `coef` holds the tile's coefficient table.
+template <typename Tile, int WAVES_P, int TCO, int TP>
+__device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[TCO][TP], u16* lds,
+                                              const float* coef, int coef_scale, int coef_bias,
+                                              int n0, int m0, int m_end, int wave_p, int wco0) {
+  constexpr int NT = Tile::NT;
+  constexpr int BCO = Tile::BCO;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int lrow = lane & 15;
+  const int ch_in_tile = (lane >> 4) * 4;
+  const int L = p.length;
+  const int n_cols = p.n_cols;
+  constexpr int EPITCH = Tile::EPITCH;
+  constexpr int EPI_WAVES = Tile::EPI_ROWS / (TP * 16);  // position waves per pass
+  constexpr int QUADS = BCO / 4;                         // 16-byte column groups per row
+  constexpr int RSTEP = NT / QUADS;                      // rows a workgroup pass walks at once
+  float* ep = reinterpret_cast<float*>(lds);
+  // step 2's fixed column group per thread, and its activation coefficients
+  const int q = tid % QUADS;
+  const int r_first = tid / QUADS;
+  const bool walker = r_first < RSTEP;
+  const int n_q = n0 + q * 4;
+  const f32x4 act_a = *reinterpret_cast<const f32x4*>(coef + kActA * BCO + q * 4);
+  const f32x4 act_b = *reinterpret_cast<const f32x4*>(coef + kActB * BCO + q * 4);
+  const float inv_l = 1.f / (float)L;
+  for (int pass = 0; pass * EPI_WAVES < WAVES_P; ++pass) {
+    __syncthreads();
+    const int wl = wave_p - pass * EPI_WAVES;  // this wave's slot in the pass
+    if (wl >= 0 && wl < EPI_WAVES) {
+#pragma unroll
+      for (int c = 0; c < TCO; ++c) {
+        const int col = wco0 + c * 16 + ch_in_tile;
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(coef + coef_scale * BCO + col);
+        const f32x4 bi = *reinterpret_cast<const f32x4*>(coef + coef_bias * BCO + col);
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+          float* row = ep + (wl * TP * 16 + t * 16 + lrow) * EPITCH + col;
+          *reinterpret_cast<f32x4*>(row) = acc[c][t] * sc + bi;
+        }
+      }
+    }
+    __syncthreads();
+    const int mp = m0 + pass * Tile::EPI_ROWS;  // first position of the pass
+    const int prow = min(Tile::EPI_ROWS, m_end - mp);
+    const bool live = walker && n_q < n_cols;
+    constexpr int U = 4;  // rows in flight per thread
+    for (int r0 = r_first; r0 < prow; r0 += U * RSTEP) {
+      uint32_t roff[U], ooff[U];
+      f32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = min(r0 + u * RSTEP, prow - 1);
+        const int m = mp + r;
+        int b = (int)((float)m * inv_l);  // m / L, corrected below
+        int i = m - b * L;
+        if (i < 0) { --b; i += L; }
+        if (i >= L) { ++b; i -= L; }
+        const bool ok = live && r0 + u * RSTEP < prow;
+        roff[u] = ok ? (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q) * 4 : kOutOfRange;
+        ooff[u] = ok ? (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q) : kOutOfRange;
+        v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
+      }
+      if (p.residual) {
+        const auto rr = buffer_rsrc(p.residual, p.r_bytes);
+        f32x4 res[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          res[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, roff[u], 0, 0));
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] += res[u];
+      }
+      if (p.mix_a) {
+        const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
+        const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const f32x4 ma = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, roff[u], 0, 0));
+          const f32x4 mb = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, roff[u], 0, 0));
+          v[u] = ((ma + mb) + v[u]) * p.mix_scale;
+        }
+      }
+      if (p.sum_out) {
+        const auto rs = buffer_rsrc(p.sum_out, p.r_bytes);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rs, roff[u], 0, 0);
+      }
+      if (p.out != nullptr) {
+        const int act = p.act;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          f32x4 y = v[u];
+          if (act == OMNI_ACT_SNAKE) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = snake_rev(y[e], act_a[e], act_b[e]);
+          } else if (act == OMNI_ACT_LEAKY_RELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;
+          } else if (act != OMNI_ACT_NONE) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = apply_act(act, y[e], 0.f, 0.f, p.slope);
+          }
+          const auto ro = buffer_rsrc(p.out, p.o_bytes);
+          if (p.out_bf16) {
+            const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 2;
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, oo, 0, 0);
+          } else {
+            const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 4;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, oo, 0, 0);
+          }
+        }
+      }
+    }
+  }
 }
 
 // Input modes: bf16 used as is; bf16 activated while staged; float32 activated while staged.
@@ -431,28 +588,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   // The epilogue's per-column coefficients into LDS (visible after the first barrier below).
   float* coef = reinterpret_cast<float*>(
       reinterpret_cast<uint8_t*>(lds) + Tile::coef_offset(MAX_ROWS, taps, FUSE2));
-  enum { kScale, kBias, kMidA, kMidB, kScale2, kBias2, kActA, kActB };
-  for (int e = tid; e < Tile::NCOEF * BCO; e += NT) {
-    const int k = e / BCO;
-    const int j = e - k * BCO;
-    const int n = n0 + j;
-    const bool real = n < n_cols;
-    const int co = real ? n % p.c_out : 0;
-    float v = (k == kScale || k == kScale2) ? 1.f : 0.f;
-    if (real) {
-      switch (k) {
-        case kScale: if (p.wscale) v = p.wscale[n]; break;
-        case kBias: if (p.bias) v = p.bias[co]; break;
-        case kMidA: if (FUSE2 && p.mid_a) v = p.mid_a[co] * kInvTwoPi; break;
-        case kMidB: if (FUSE2 && p.mid_b) v = p.mid_b[co]; break;
-        case kScale2: if (FUSE2 && p.wscale2) v = p.wscale2[n]; break;
-        case kBias2: if (FUSE2 && p.bias2) v = p.bias2[co]; break;
-        case kActA: if (p.act_a) v = p.act_a[co] * kInvTwoPi; break;
-        default: if (p.act_b) v = p.act_b[co]; break;
-      }
-    }
-    coef[e] = v;
-  }
+  stage_coefficients<BCO, NT, FUSE2>(p, coef, n0);
 
   load_chunk(0);
   for (int kc = 0; kc < chunks; ++kc) {
@@ -544,113 +680,8 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     coef_bias = kBias2;
   }
 
-  // Epilogue, in two steps per pass over half the position waves: (1) in the accumulator layout
-  // (lane = position, 4 consecutive columns per lane) each wave adds the weight scale and bias and
-  // writes float32 rows into LDS; (2) the workgroup walks those rows 16 bytes per thread, so the
-  // residual / mix loads and the sum_out / out stores are whole contiguous rows of HBM.
-  constexpr int EPITCH = Tile::EPITCH;
-  constexpr int EPI_WAVES = Tile::EPI_ROWS / (TP * 16);  // position waves per pass
-  constexpr int QUADS = BCO / 4;                         // 16-byte column groups per row
-  constexpr int RSTEP = NT / QUADS;                      // rows a workgroup pass walks at once
-  float* ep = reinterpret_cast<float*>(lds);
-  // step 2's fixed column group per thread, and its activation coefficients
-  const int q = tid % QUADS;
-  const int r_first = tid / QUADS;
-  const bool walker = r_first < RSTEP;
-  const int n_q = n0 + q * 4;
-  const f32x4 act_a = *reinterpret_cast<const f32x4*>(coef + kActA * BCO + q * 4);
-  const f32x4 act_b = *reinterpret_cast<const f32x4*>(coef + kActB * BCO + q * 4);
-  const float inv_l = 1.f / (float)L;
-  for (int pass = 0; pass * EPI_WAVES < WAVES_P; ++pass) {
-    __syncthreads();
-    const int wl = wave_p - pass * EPI_WAVES;  // this wave's slot in the pass
-    if (wl >= 0 && wl < EPI_WAVES) {
-#pragma unroll
-      for (int c = 0; c < TCO; ++c) {
-        const int col = wco0 + c * 16 + ch_in_tile;
-        const f32x4 sc = *reinterpret_cast<const f32x4*>(coef + coef_scale * BCO + col);
-        const f32x4 bi = *reinterpret_cast<const f32x4*>(coef + coef_bias * BCO + col);
-#pragma unroll
-        for (int t = 0; t < TP; ++t) {
-          float* row = ep + (wl * TP * 16 + t * 16 + lrow) * EPITCH + col;
-          *reinterpret_cast<f32x4*>(row) = acc[c][t] * sc + bi;
-        }
-      }
-    }
-    __syncthreads();
-    const int mp = m0 + pass * Tile::EPI_ROWS;  // first position of the pass
-    const int prow = min(Tile::EPI_ROWS, m_end - mp);
-    const bool live = walker && n_q < n_cols;
-    constexpr int U = 4;  // rows in flight per thread
-    for (int r0 = r_first; r0 < prow; r0 += U * RSTEP) {
-      uint32_t roff[U], ooff[U];
-      f32x4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int r = min(r0 + u * RSTEP, prow - 1);
-        const int m = mp + r;
-        int b = (int)((float)m * inv_l);  // m / L, corrected below
-        int i = m - b * L;
-        if (i < 0) { --b; i += L; }
-        if (i >= L) { ++b; i -= L; }
-        const bool ok = live && r0 + u * RSTEP < prow;
-        roff[u] = ok ? (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q) * 4 : kOutOfRange;
-        ooff[u] = ok ? (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q) : kOutOfRange;
-        v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
-      }
-      if (p.residual) {
-        const auto rr = buffer_rsrc(p.residual, p.r_bytes);
-        f32x4 res[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          res[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, roff[u], 0, 0));
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] += res[u];
-      }
-      if (p.mix_a) {
-        const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
-        const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const f32x4 ma = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, roff[u], 0, 0));
-          const f32x4 mb = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, roff[u], 0, 0));
-          v[u] = ((ma + mb) + v[u]) * p.mix_scale;
-        }
-      }
-      if (p.sum_out) {
-        const auto rs = buffer_rsrc(p.sum_out, p.r_bytes);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rs, roff[u], 0, 0);
-      }
-      if (p.out != nullptr) {
-        const int act = p.act;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          f32x4 y = v[u];
-          if (act == OMNI_ACT_SNAKE) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = snake_rev(y[e], act_a[e], act_b[e]);
-          } else if (act == OMNI_ACT_LEAKY_RELU) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;
-          } else if (act != OMNI_ACT_NONE) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = apply_act(act, y[e], 0.f, 0.f, p.slope);
-          }
-          const auto ro = buffer_rsrc(p.out, p.o_bytes);
-          if (p.out_bf16) {
-            const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 2;
-            __builtin_amdgcn_raw_buffer_store_b64(
-                u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, oo, 0, 0);
-          } else {
-            const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 4;
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, oo, 0, 0);
-          }
-        }
-      }
-    }
-  }
+  conv_epilogue<Tile, WAVES_P, TCO, TP>(p, acc, lds, coef, coef_scale, coef_bias, n0, m0, m_end,
+                                       wave_p, wco0);
 }
 
 // Raise a kernel's dynamic-LDS limit to the CU's 160 KiB. A refusal is not an error here (the
