@@ -269,7 +269,30 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   // 4-6; r = 6 the k = 1 conv) into ring buffer g % 2: this wave's share of the stage's 64-lane
   // 16-byte instructions. Lane i of an instruction fills ring slot 64 * instr + i, so each lane
   // loads the global piece that belongs in its slot (pad slots reload the chunk's first piece).
-  const int nwaves = NT / 64;
+  //
+  // The per-lane byte offsets of the two dilated-conv patterns (taps 0-3: 17 slots per column
+  // row, taps 4-6: 13) are the same for every chunk and unit up to the chunk's base, which goes
+  // in the scalar offset, so they are computed once here.
+  constexpr int NWAVES = NT / 64;
+  constexpr int LO_INSTRS = (C * Tile::P_LO + 63) / 64;
+  constexpr int HI_INSTRS = (C * Tile::P_HI + 63) / 64;
+  constexpr int W2_INSTRS = CH * C * 4 / 64;
+  constexpr int LO_PER_WAVE = (LO_INSTRS + NWAVES - 1) / NWAVES;
+  constexpr int HI_PER_WAVE = (HI_INSTRS + NWAVES - 1) / NWAVES;
+  uint32_t lo_off[DMA ? LO_PER_WAVE : 1], hi_off[DMA ? HI_PER_WAVE : 1];
+  if constexpr (DMA) {
+    auto slot_offset = [&](int di, int P, int t0, int nt) __attribute__((always_inline)) {
+      const int slot = di * 64 + lane;
+      const int n = slot / P;
+      const int j = slot - n * P;
+      return (n < C && j < nt * 4)
+                 ? (uint32_t)(((n * kTaps + t0 + (j >> 2)) * kChunk + (j & 3) * 8) * 2) : 0u;
+    };
+#pragma unroll
+    for (int i = 0; i < LO_PER_WAVE; ++i) lo_off[i] = slot_offset(wave + i * NWAVES, Tile::P_LO, 0, 4);
+#pragma unroll
+    for (int i = 0; i < HI_PER_WAVE; ++i) hi_off[i] = slot_offset(wave + i * NWAVES, Tile::P_HI, 4, 3);
+  }
   auto dma_stage = [&](int g) __attribute__((always_inline)) {
     if constexpr (DMA) {
       const int k = g / Tile::STAGES;
@@ -277,30 +300,37 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       if (k >= p.nunits) return;
       u16* buf = ws + (g & 1) * Tile::RING_ELEMS;
       if (r < 6) {
-        const int kc = r >> 1;
-        const int t0 = (r & 1) ? 4 : 0;
-        const int nt = (r & 1) ? 3 : 4;
-        const int P = nt * 4 + 1;
         const auto rs = buffer_rsrc(p.unit[k].w1, p.unit[k].w1_bytes);
-        const int instrs = (C * P + 63) / 64;
-        for (int di = wave; di < instrs; di += nwaves) {
-          const int slot = di * 64 + lane;
-          const int n = slot / P;
-          const int j = slot - n * P;
-          const bool real = n < C && j < nt * 4;
-          const uint32_t off =
-              real ? (uint32_t)((((kc * C + n) * kTaps + t0 + (j >> 2)) * kChunk + (j & 3) * 8) * 2)
-                   : (uint32_t)(kc * C * kTaps * kChunk * 2);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16, off, 0, 0, 0);
+        const int chunk_base = (r >> 1) * C * kTaps * kChunk * 2;  // bytes
+        if (r & 1) {
+#pragma unroll
+          for (int i = 0; i < HI_PER_WAVE; ++i) {
+            const int di = wave + i * NWAVES;
+            if (di < HI_INSTRS)
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                  rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16,
+                  (int)hi_off[i], chunk_base, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < LO_PER_WAVE; ++i) {
+            const int di = wave + i * NWAVES;
+            if (di < LO_INSTRS)
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                  rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16,
+                  (int)lo_off[i], chunk_base, 0, 0);
+          }
         }
       } else {
         const auto rs = buffer_rsrc(p.unit[k].w2, p.unit[k].w2_bytes);
-        constexpr int instrs = CH * C * 4 / 64;
-        for (int di = wave; di < instrs; di += nwaves)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16,
-              (uint32_t)((di * 64 + lane) * 16), 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < (W2_INSTRS + NWAVES - 1) / NWAVES; ++i) {
+          const int di = wave + i * NWAVES;
+          if (di < W2_INSTRS)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16,
+                (int)((uint32_t)(di * 64 + lane) * 16u), 0, 0, 0);
+        }
       }
     }
   };

@@ -19,10 +19,11 @@ bf16 operand:
     per block:
       polyphase ConvTranspose (k = 2s)   u -> x (float32), u = Snake(unit 0 act1)(x)
       per residual unit (d = 1, 3, 9):
-        96 / 192 channels: one launch    conv k7 dilation d; bias + Snake(act2) -> bf16 tile in
+        96 channels (192 with fp8 weights): one launch
+                                         conv k7 dilation d; bias + Snake(act2) -> bf16 tile in
                                          LDS; conv k1; bias + x -> x (float32, in place),
                                          u' = Snake(next)(x) (bf16)
-        wider:             two launches  conv k7; bias + Snake(act2) -> h (bf16)
+        otherwise:         two launches  conv k7; bias + Snake(act2) -> h (bf16)
                                          conv k1 of h; bias + x -> x (in place), u' = Snake(next)(x)
     conv to one channel k7               u = Snake(final)(x); tanh -> float32 waveform
 
@@ -86,6 +87,11 @@ class _Block:
 
 # channel counts the fused residual-unit kernel handles (one column tile holds every channel)
 FUSED_UNIT_CHANNELS = (96, 192)
+# ... and those where it is the faster form: with bf16 weights the 192-channel units run as two
+# LDS-DMA conv launches (conv k7 at 96 x 384 tiles, conv k1 at 192 x 192), which beat the fused
+# register-staged kernel even with h (bf16) through HBM between them; with fp8 weights (staged
+# through registers by both forms) the fused launch stays faster
+FUSED_UNIT_CHANNELS_BF16 = (96,)
 # channel counts the residual-stack kernel (every unit of a block in one launch) handles
 STACK_CHANNELS = (96,)
 
@@ -204,7 +210,8 @@ class DacCodecDecoder:
                             conv1d(uw["conv1"], ur["conv1"], ur["dilation"]), a2, b2)
                 c2 = conv1d(uw["conv2"], ur["conv2"])
                 units.append(_Unit(c1, c2, a2, b2, an, bn,
-                                   c1.conv.c_out in FUSED_UNIT_CHANNELS))
+                                   c1.conv.c_out in (FUSED_UNIT_CHANNELS if fp8
+                                                     else FUSED_UNIT_CHANNELS_BF16)))
             blk = _Block(up, units, br["stride"], up.conv.c_out)
             if (residual_stacks and blk.c_out in STACK_CHANNELS
                     and len(units) <= N.MAX_RESIDUAL_UNITS
