@@ -89,7 +89,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 3: omni_residual_stack */
+int omni_codec_abi_version(void); /* 4: omni_residual_stack's fused final conv */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -203,6 +203,7 @@ int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
  *     x_{k+1} = (sum_n' W2_k[n, n'] * h[n']) * w2_scale + bias2 + x_k
  *   out   = Snake(out_act_a, out_act_b)(x_last) rounded to bf16   (the next layer's operand)
  *   x_out = x_last                                                   (float32, optional)
+ *   final_out = the decoder's final conv of out (optional, below)
  *
  * with the arithmetic of one omni_conv1d_fused residual-unit call per unit, so the results are
  * the same bits. Weights use omni_conv1d_fused's packing ([C/32][C][7][32] and [C/32][C][32],
@@ -251,6 +252,24 @@ typedef struct omni_residual_stack_args {
   int64_t out_stride_b, out_stride_t;
   float* x_out; /* optional */
   int64_t x_out_stride_b, x_out_stride_t;
+  /* Optional (final_weight != NULL): the decoder's conv to one channel fused behind the stack,
+   * over u = Snake(out_act)(x_last) rounded to bf16:
+   *   final_out[b, i] = final_act(final_bias + sum_{j < taps} sum_c
+   *                               final_weight[j * C + c] * u[b, i + j - (taps - 1), c])
+   * on the matrix cores: the weights are rounded to bf16 (the decoder's are bf16 values) and the
+   * products summed in float32 in the MFMA's order, one fixed order per position (so any split
+   * of positions or rows gives the same bits; they can differ from omni_single_output_conv's in
+   * the last places). taps = final_taps <= 8; positions left of 0 come from final_hist_pool (bf16
+   * [slots][2][taps - 1][C], the omni_conv1d_fused history contract, sharing slot_index,
+   * slot_parity and history_cold) or are zero. out may be NULL when final_weight is given. */
+  const float* final_weight;
+  const float* final_bias;
+  int64_t final_taps;
+  int final_activation; /* OMNI_ACTIVATION_TANH, _CLAMP or _NONE */
+  void* final_hist_pool;
+  int64_t final_hist_slot_stride;
+  float* final_out; /* float32, element (b, i) at b * final_out_stride_b + i */
+  int64_t final_out_stride_b;
 } omni_residual_stack_args;
 
 int omni_residual_stack(const omni_residual_stack_args* args, omni_stream_t stream);

@@ -74,7 +74,17 @@ struct StackParams {
   float* x_out;
   int xo_sb, xo_st;
   uint32_t x_bytes, o_bytes, xo_bytes;
-  int H;              // staged rows ahead of each segment (sum of the unit halos)
+  // the decoder's final conv to one channel (fin_w != NULL): [fin_taps][C] float32 weights
+  const float* fin_w;
+  const float* fin_b;
+  int fin_taps, fin_act;
+  u16* fin_hist;  // [slots][2][fin_taps - 1][C] bf16, or NULL
+  int fin_hist_stride;
+  uint32_t fin_hist_bytes;
+  float* fin_out;
+  int64_t fin_o_sb;
+  int H;              // staged rows ahead of each segment (sum of the unit halos and the
+                      // final conv's taps - 1)
   int seg_len;        // long rows: output positions per tile; short rows: the row length
   int tiles_per_row;  // long rows: tiles per stream row; 0: short rows, whole rows per tile
   int rows_per_tile;  // short rows: stream rows per tile
@@ -557,7 +567,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   }
   __syncthreads();
   // ---- the output operand rows of the tile's positions, 16 contiguous bytes per thread
-  {
+  if (p.out != nullptr) {
     const auto orsrc = buffer_rsrc(p.out, p.o_bytes);
     for (int e = tid; e < nseg * len * PIECES_PER_ROW; e += NT) {
       const int s = e / (len * PIECES_PER_ROW);
@@ -568,6 +578,90 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
       const uint32_t off = (uint32_t)((b0 + s) * p.o_sb + (i0 + q) * p.o_st + piece * 8) * 2;
       __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, off, 0, 0);
+    }
+  }
+  // ---- the decoder's final conv to one channel over the output operand u in LDS, in the
+  // summation order of single_output_conv_bf16_kernel (j outer, channels ascending, one fma each)
+  if (p.fin_w != nullptr) {
+    const int fh = p.fin_taps - 1;  // its causal context: staged rows H - fh .. H - 1
+    const auto fr = buffer_rsrc(p.fin_hist, p.fin_hist_bytes);
+    // (a) context rows left of position 0 (segments that start a stream row): the history copy
+    // of the row's slot, or zeros
+    if (i0 == 0 && fh > 0) {
+      for (int e = tid; e < nseg * fh * PIECES_PER_ROW; e += NT) {
+        const int s = e / (fh * PIECES_PER_ROW);
+        const int rem = e - s * fh * PIECES_PER_ROW;
+        const int j = rem / PIECES_PER_ROW;  // sample j of the history: position j - fh
+        const int piece = rem - j * PIECES_PER_ROW;
+        uint32_t off = kOutOfRange;
+        if (p.fin_hist != nullptr && !p.hist_cold) {
+          const int64_t slot = p.slot_index[b0 + s];
+          if (slot >= 0 && slot < p.hist_slots) {
+            const int parity = (int)(p.slot_parity[slot] & 1);
+            off = (uint32_t)((int)slot * p.fin_hist_stride + (parity * fh + j) * C + piece * 8) * 2;
+          }
+        }
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(fr, off, 0, 0);
+        const int row = kGuard + s * span + H - fh + j;
+        *reinterpret_cast<u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3)) = v;
+      }
+    }
+    __syncthreads();
+    // (b) its new history: the last fh operand samples of each stream row, written by the
+    // workgroup holding them (those left of 0 by the one holding position 0)
+    if (p.fin_hist != nullptr) {
+      for (int e = tid; e < nseg * fh * PIECES_PER_ROW; e += NT) {
+        const int s = e / (fh * PIECES_PER_ROW);
+        const int rem = e - s * fh * PIECES_PER_ROW;
+        const int j = rem / PIECES_PER_ROW;
+        const int piece = rem - j * PIECES_PER_ROW;
+        const int pos = L - fh + j;
+        const bool own = pos >= 0 ? (pos >= i0 && pos < i0 + len) : i0 == 0;
+        const int64_t slot = p.slot_index[b0 + s];
+        if (own && slot >= 0 && slot < p.hist_slots) {
+          const int parity = (int)(p.slot_parity[slot] & 1);
+          const int row = kGuard + s * span + (pos - i0) + H;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
+          const uint32_t off =
+              (uint32_t)((int)slot * p.fin_hist_stride + ((1 - parity) * fh + j) * C + piece * 8) * 2;
+          __builtin_amdgcn_raw_buffer_store_b128(v, fr, off, 0, 0);
+        }
+      }
+    }
+    // (c) the conv on the matrix cores, as a conv with one real column: column 0 of the A
+    // operand holds the weights (rounded to bf16), columns 1..15 zeros, and the B operand is the
+    // operand tile read at the taps' row shifts exactly as the units' dilated conv reads it
+    // (dilation 1). The weights go to LDS first (the ring is free now): [fin_taps][C] bf16.
+    u16* wf = ws;
+    for (int e = tid; e < p.fin_taps * C; e += NT) wf[e] = float_to_bits_bf16(p.fin_w[e]);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TP; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j <= fh; ++j) {
+      const int rj = row0 + j - fh;
+      const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+#pragma unroll
+      for (int kc = 0; kc < CH; ++kc) {
+        bf16x8 a = bf16x8{};
+        if (lrow == 0) a = *reinterpret_cast<const bf16x8*>(wf + j * C + kc * kChunk + lk);
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+          const bf16x8 bv =
+              *reinterpret_cast<const bf16x8*>(us + kc * UROWS * kChunk + bj + t * 16 * kChunk);
+          acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[0][t], 0, 0, 0);
+        }
+      }
+    }
+    // column 0 of each accumulator block: lanes 0..15, element 0, row lrow + 16 t
+    const float bias = p.fin_b ? p.fin_b[0] : 0.f;
+    if (lane < 16) {
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const int q = rrow[t] - (rrow[t] / span) * span;
+        if (rrow[t] < rows && q >= H)
+          p.fin_out[(int64_t)rb[t] * p.fin_o_sb + rpos[t]] =
+              apply_act(p.fin_act, acc[0][t][0] + bias, 0.f, 0.f, 0.f);
+      }
     }
   }
   if (p.x_out != nullptr) {

@@ -9,7 +9,9 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 
 extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_stream_t stream) {
   using namespace omni_stack;
-  if (!a || !a->x || !a->out || !a->out_act_a || !a->out_act_b) return OMNI_ERR_INVALID_ARG;
+  if (!a || !a->x || !a->out_act_a || !a->out_act_b) return OMNI_ERR_INVALID_ARG;
+  const bool fin = a->final_weight != nullptr;
+  if (!a->out && !fin) return OMNI_ERR_INVALID_ARG;
   if (a->batch < 0 || a->length < 0 || a->num_units < 1 || a->num_units > kMaxUnits)
     return OMNI_ERR_INVALID_ARG;
   if (a->weight_dtype != OMNI_DTYPE_BF16 && a->weight_dtype != OMNI_DTYPE_FP8_E4M3)
@@ -20,8 +22,21 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   // 16-byte accesses of x, out and x_out rows
   if (!aligned16(a->x) || a->x_stride_t < C || a->x_stride_t % 4 || a->x_stride_b % 4)
     return OMNI_ERR_INVALID_ARG;
-  if (!aligned16(a->out) || a->out_stride_t < C || a->out_stride_t % 8 || a->out_stride_b % 8)
+  if (a->out &&
+      (!aligned16(a->out) || a->out_stride_t < C || a->out_stride_t % 8 || a->out_stride_b % 8))
     return OMNI_ERR_INVALID_ARG;
+  if (fin) {
+    if (!a->final_out || a->final_taps < 1 || a->final_out_stride_b < a->length)
+      return OMNI_ERR_INVALID_ARG;
+    if (a->final_taps > 8) return OMNI_ERR_UNSUPPORTED;
+    if (a->final_activation != OMNI_ACTIVATION_NONE && a->final_activation != OMNI_ACTIVATION_TANH &&
+        a->final_activation != OMNI_ACTIVATION_CLAMP)
+      return OMNI_ERR_INVALID_ARG;
+    if (a->final_hist_pool &&
+        (!aligned16(a->final_hist_pool) || a->final_taps < 2 ||
+         a->final_hist_slot_stride < 2 * (a->final_taps - 1) * C || a->final_hist_slot_stride % 8))
+      return OMNI_ERR_INVALID_ARG;
+  }
   if (a->x_out && (!aligned16(a->x_out) || a->x_out_stride_t < C || a->x_out_stride_t % 4 ||
                    a->x_out_stride_b % 4))
     return OMNI_ERR_INVALID_ARG;
@@ -43,6 +58,10 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
     }
     H += 6 * u.dilation;
   }
+  if (fin) {
+    H += a->final_taps - 1;
+    if (a->final_hist_pool) any_hist = true;
+  }
   if (any_hist && (!a->slot_index || !a->slot_parity || a->hist_num_slots < 1))
     return OMNI_ERR_INVALID_ARG;
   if (a->batch == 0 || a->length == 0) return OMNI_OK;
@@ -53,7 +72,12 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   const int64_t B = a->batch, L = a->length;
   const int64_t limit = 0x7fffffffLL;
   const int64_t x_bytes = ((B - 1) * a->x_stride_b + (L - 1) * a->x_stride_t + C) * 4;
-  const int64_t o_bytes = ((B - 1) * a->out_stride_b + (L - 1) * a->out_stride_t + C) * 2;
+  const int64_t o_bytes =
+      a->out ? ((B - 1) * a->out_stride_b + (L - 1) * a->out_stride_t + C) * 2 : 0;
+  const int64_t fh_bytes =
+      fin && a->final_hist_pool ? a->hist_num_slots * a->final_hist_slot_stride * 2 : 0;
+  if (fin && ((B - 1) * a->final_out_stride_b + L > limit || fh_bytes > limit))
+    return OMNI_ERR_UNSUPPORTED;
   const int64_t xo_bytes =
       a->x_out ? ((B - 1) * a->x_out_stride_b + (L - 1) * a->x_out_stride_t + C) * 4 : 0;
   if (x_bytes > limit || o_bytes > limit || xo_bytes > limit) return OMNI_ERR_UNSUPPORTED;
@@ -107,6 +131,17 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   p.o_bytes = (uint32_t)o_bytes;
   p.xo_bytes = (uint32_t)xo_bytes;
   p.H = (int)H;
+  if (fin) {
+    p.fin_w = a->final_weight;
+    p.fin_b = a->final_bias;
+    p.fin_taps = (int)a->final_taps;
+    p.fin_act = a->final_activation;
+    p.fin_hist = reinterpret_cast<u16*>(a->final_hist_pool);
+    p.fin_hist_stride = (int)a->final_hist_slot_stride;
+    p.fin_hist_bytes = (uint32_t)fh_bytes;
+    p.fin_out = a->final_out;
+    p.fin_o_sb = a->final_out_stride_b;
+  }
 
   // Long rows: tiles inside one row, as many as the staged rows need, evened out; short rows:
   // as many whole rows (each with its halo) as the staged rows hold.

@@ -145,6 +145,14 @@ class ResidualStackArgs(ctypes.Structure):
         ("x_out", ctypes.c_void_p),
         ("x_out_stride_b", ctypes.c_int64),
         ("x_out_stride_t", ctypes.c_int64),
+        ("final_weight", ctypes.c_void_p),
+        ("final_bias", ctypes.c_void_p),
+        ("final_taps", ctypes.c_int64),
+        ("final_activation", ctypes.c_int),
+        ("final_hist_pool", ctypes.c_void_p),
+        ("final_hist_slot_stride", ctypes.c_int64),
+        ("final_out", ctypes.c_void_p),
+        ("final_out_stride_b", ctypes.c_int64),
     ]
 
 

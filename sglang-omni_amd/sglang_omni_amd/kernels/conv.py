@@ -267,6 +267,19 @@ def fused_conv(
 
 
 @dataclass
+class FinalConv:
+    """The decoder's conv to one channel when it runs inside the residual stack: weight
+    [taps, C] float32 (tap-major), bias [1] or None, activation (ACT_TANH, ACT_CLAMP, ACT_NONE),
+    out [B, 1, L] float32, and its streaming history pool [slots, 2, taps - 1, C] bf16 or None."""
+
+    weight: torch.Tensor
+    bias: torch.Tensor | None
+    activation: int
+    out: torch.Tensor
+    history: torch.Tensor | None = None
+
+
+@dataclass
 class ResidualUnitWeights:
     """One residual unit of a decoder block: Snake(in) -> conv1 (k = 7, dilation) ->
     Snake(mid) -> conv2 (k = 1) -> + x, with the Snake coefficient pairs (a, b) as float32 [C]."""
@@ -291,16 +304,22 @@ def residual_stack(
     slot_index: torch.Tensor | None = None,
     slot_parity: torch.Tensor | None = None,
     history_cold: bool = False,
+    final: FinalConv | None = None,
 ) -> torch.Tensor:
     """Launch ``omni_residual_stack``: every unit in turn over x [B, L, C] float32, then
     out = Snake(out_a, out_b)(x_last) as bf16 [B, L, C] (and x_last into x_out, float32).
-    histories[k] is unit k's conv1 history pool [slots, 2, 6 * dilation, C] bf16 (streaming)."""
+    histories[k] is unit k's conv1 history pool [slots, 2, 6 * dilation, C] bf16 (streaming).
+    With ``final`` the decoder's conv to one channel runs over out inside the same launch and
+    writes final.out [B, 1, L] float32 (out may then be None: the operand stays on chip); returns
+    final.out, else out."""
     N.require_device(x, out, x_out)
     if not 1 <= len(units) <= N.MAX_RESIDUAL_UNITS:
         raise ValueError(f"1..{N.MAX_RESIDUAL_UNITS} residual units per launch")
     if x.dtype != torch.float32 or x.dim() != 3 or x.stride(2) != 1:
         raise ValueError("x must be float32 [B, L, C] with channel stride 1")
     batch, length, channels = x.shape
+    if out is None and final is None:
+        raise ValueError("the stack needs an output: out, or a final conv")
     for t, dt in ((out, torch.bfloat16), (x_out, torch.float32)):
         if t is None:
             continue
@@ -343,12 +362,38 @@ def residual_stack(
         args.slot_parity = slot_parity.data_ptr()
         args.history_cold = int(history_cold)
     args.out_act_a, args.out_act_b = out_a.data_ptr(), out_b.data_ptr()
-    args.out = out.data_ptr()
-    args.out_stride_b, args.out_stride_t = out.stride(0), out.stride(1)
+    if out is not None:
+        args.out = out.data_ptr()
+        args.out_stride_b, args.out_stride_t = out.stride(0), out.stride(1)
+    if final is not None:
+        f = final
+        N.require_device(f.weight, f.out)
+        taps = f.weight.shape[0]
+        if (f.weight.dtype != torch.float32 or tuple(f.weight.shape) != (taps, channels)
+                or not f.weight.is_contiguous()):
+            raise ValueError("final.weight must be float32 [taps, C] contiguous")
+        if (f.out.dtype != torch.float32 or tuple(f.out.shape) != (batch, 1, length)
+                or f.out.stride(2) != 1):
+            raise ValueError("final.out must be float32 [B, 1, L] with unit position stride")
+        args.final_weight = f.weight.data_ptr()
+        args.final_bias = N.ptr(f.bias)
+        args.final_taps = taps
+        args.final_activation = f.activation
+        args.final_out = f.out.data_ptr()
+        args.final_out_stride_b = f.out.stride(0)
+        if f.history is not None:
+            if slot_index is None or slot_parity is None:
+                raise ValueError("a history pool needs slot_index and slot_parity")
+            args.final_hist_pool = f.history.data_ptr()
+            args.final_hist_slot_stride = f.history.stride(0)
+            args.hist_num_slots = f.history.shape[0]
+            args.slot_index = slot_index.data_ptr()
+            args.slot_parity = slot_parity.data_ptr()
+            args.history_cold = int(history_cold)
     if x_out is not None:
         args.x_out = x_out.data_ptr()
         args.x_out_stride_b, args.x_out_stride_t = x_out.stride(0), x_out.stride(1)
     lib = N.load_library()
     N.check(lib.omni_residual_stack(ctypes.byref(args), N.stream_handle(x.device)),
             "omni_residual_stack")
-    return out
+    return final.out if final is not None else out

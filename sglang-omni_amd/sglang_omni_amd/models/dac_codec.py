@@ -43,6 +43,7 @@ import torch
 
 from .. import _native as N
 from ..kernels.conv import (
+    FinalConv,
     PackedConv,
     ResidualUnitWeights,
     fused_conv,
@@ -225,6 +226,11 @@ class DacCodecDecoder:
         self.final_bias = ref["final"]["conv"]["bias"].float().to(dev).contiguous()
         self.final_taps = fw.shape[-1]
         self.final_channels = fw.shape[1]
+        # the final conv runs inside the last block's residual-stack launch (its operand never
+        # leaves the chip) when that block has a stack over the final conv's channels
+        self.final_in_stack = (bool(self.blocks) and self.blocks[-1].stack is not None
+                               and self.blocks[-1].c_out == self.final_channels
+                               and self.final_taps <= 8)
         self._workspaces: dict[tuple[int, int], _Workspace] = {}
         # a utils.timing.LaunchTimer installed here records every launch with its work
         self.timer = NO_TIMER
@@ -334,6 +340,17 @@ class DacCodecDecoder:
                          "slot_parity": state["pool"].parity,
                          "history_cold": state["cold"]}
                 last = blk.units[-1]
+                if bi + 1 == len(self.blocks) and self.final_in_stack:
+                    # the last block: the final conv runs inside the stack launch
+                    final = FinalConv(self.final_weight, self.final_bias, N.ACT_TANH,
+                                      torch.empty(batch, 1, length, dtype=torch.float32,
+                                                  device=self.device),
+                                      hist("final").get("history"))
+                    flops += 2.0 * batch * length * self.final_taps * self.final_channels
+                    with timer.launch(f"stack{c}", flops, f"blocks.{bi}.units+final"):
+                        wave = residual_stack(x, blk.stack, None, last.next_a, last.next_b,
+                                              final=final, **h)
+                    return self._finish_step(wave, state, batch)
                 with timer.launch(f"stack{c}", flops, f"blocks.{bi}.units"):
                     residual_stack(x, blk.stack, u_next, last.next_a, last.next_b, **h)
                 cur = 1 - cur
@@ -377,6 +394,10 @@ class DacCodecDecoder:
             single_output_conv(u, self.final_weight, self.final_bias, wave,
                                activation=N.ACT_TANH, left_pad=self.final_taps - 1,
                                **hist("final"))
+        return self._finish_step(wave, state, batch)
+
+    def _finish_step(self, wave: torch.Tensor, state: dict | None, batch: int) -> torch.Tensor:
+        """End of a decode step: flip the slot parity of the step's rows (streaming)."""
         if state is not None:
             lib = N.load_library()
             parity = state["pool"].parity

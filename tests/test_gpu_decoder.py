@@ -245,23 +245,27 @@ def test_hifigan_matches_the_oracle(gpu):
 
 @pytest.mark.parametrize("config", [TINY_FUSED, CODEC_24K], ids=["tiny", "codec24k"])
 def test_residual_stacks_decode_like_one_launch_per_unit(gpu, config):
-    """The 96-channel stage as one residual-stack launch per block gives the bits of one fused
-    launch per residual unit, whole and streamed."""
+    """The 96-channel stage as one residual-stack launch per block (the final conv to one
+    channel inside it) against one fused launch per residual unit and a separate final conv: the
+    residual units give the same bits, and the final conv's two forms sum the same products in
+    different float32 orders, so the waveforms agree to float32 summation error. Streamed decodes
+    give each decoder's whole-decode bits."""
     weights = make_dac_weights(config, seed=0)
     stacked = DacCodecDecoder(weights, config, device=gpu)
     per_unit = DacCodecDecoder(weights, config, device=gpu, residual_stacks=False)
     assert any(b.stack for b in stacked.blocks) and not any(b.stack for b in per_unit.blocks)
+    assert stacked.final_in_stack and not per_unit.final_in_stack
     gen = torch.Generator().manual_seed(4)
     codes = torch.randint(0, config.codebook_size, (3, config.n_codebooks, 24), generator=gen)
     codes = codes.to(gpu)
-    assert torch.equal(stacked.from_indices(codes), per_unit.from_indices(codes))
+    wholes = [stacked.from_indices(codes), per_unit.from_indices(codes)]
+    torch.testing.assert_close(wholes[0], wholes[1], rtol=0, atol=2e-6)
     idx = torch.tensor([2, 0, 1], device=gpu)
-    outs = []
-    for dec in (stacked, per_unit):
+    for dec, whole in zip((stacked, per_unit), wholes):
         pool = dec.new_state_pool(num_slots=3)
-        outs.append(torch.cat([dec.decode_slots(codes[..., s:s + 8], pool, idx,
-                                                first_decode=s == 0) for s in (0, 8, 16)], -1))
-    assert torch.equal(outs[0], outs[1])
+        streamed = torch.cat([dec.decode_slots(codes[..., s:s + 8], pool, idx, first_decode=s == 0)
+                              for s in (0, 8, 16)], -1)
+        assert torch.equal(streamed, whole)
 
 
 def test_long_inputs_decode_in_chunks_with_the_whole_decodes_bits(gpu):

@@ -2,7 +2,9 @@
 same units run one omni_conv1d_fused launch each — bit for bit, since the kernel repeats their
 arithmetic — on long rows, short rows (several stream rows per tile), ragged tails, one to four
 units and bf16 / fp8 weights; and its streaming form (per-unit slot histories, chunks shorter
-than the receptive field) against the whole-row launch."""
+than the receptive field) against the whole-row launch. The decoder's final conv to one channel,
+fused behind the stack, against omni_single_output_conv over the stack's output, bit for bit,
+whole and streamed."""
 
 from __future__ import annotations
 
@@ -11,11 +13,13 @@ import torch
 
 from sglang_omni_amd import _native as N
 from sglang_omni_amd.kernels.conv import (
+    FinalConv,
     ResidualUnitWeights,
     fused_conv,
     pack_conv1d,
     residual_stack,
 )
+from sglang_omni_amd.kernels.single_output_conv import single_output_conv
 
 pytestmark = pytest.mark.gpu
 
@@ -129,3 +133,62 @@ def test_residual_stack_rejects_what_it_has_no_kernel_for(gpu):
     big, _, _ = make_units((11,), gpu)  # context 66 rows: past the kernel's guard rows
     with pytest.raises(N.OmniCodecError):
         residual_stack(x, big, out, out_a, out_b)
+
+
+def final_conv_weights(device, taps=7, seed=7):
+    """bf16-valued weights, as the decoder's (the fused form multiplies bf16 weights)."""
+    gen = torch.Generator().manual_seed(seed)
+    w = (torch.randn(taps, C, generator=gen) / (C * taps) ** 0.5).to(torch.bfloat16).float().to(device)
+    b = (torch.randn(1, generator=gen) * 0.05).to(device)
+    return w, b
+
+
+@pytest.mark.parametrize("batch,length", [(2, 1000), (3, 37), (1, 5), (64, 12), (5, 179), (1, 2000)])
+def test_residual_stack_final_conv_matches_the_separate_launch(gpu, batch, length):
+    """The decoder's conv to one channel fused behind the stack (on MFMA) against
+    omni_single_output_conv over the stack's bf16 output: the same products, summed in another
+    float32 order, so within float32 summation error (672 terms, outputs of order 0.1)."""
+    units, out_a, out_b = make_units((1, 3, 9), gpu, seed=batch * 7 + length)
+    gen = torch.Generator().manual_seed(length + 1)
+    x = (torch.randn(batch, length, C, generator=gen) * 0.3).to(gpu)
+    w, b = final_conv_weights(gpu)
+    u = torch.empty(batch, length, C, dtype=torch.bfloat16, device=gpu)
+    residual_stack(x, units, u, out_a, out_b)
+    expected = torch.empty(batch, 1, length, dtype=torch.float32, device=gpu)
+    single_output_conv(u, w, b, expected, activation=N.ACT_TANH, left_pad=6)
+    wave = torch.full((batch, 1, length), float("nan"), device=gpu)
+    got = residual_stack(x, units, None, out_a, out_b,
+                         final=FinalConv(w, b, N.ACT_TANH, wave))
+    assert got is wave
+    torch.testing.assert_close(wave, expected, rtol=0, atol=2e-6)
+    assert expected.abs().max().item() > 0.05
+
+
+@pytest.mark.parametrize("splits", [(5, 300, 1, 700, 994), (3, 3, 1994), (60, 60, 1880)])
+def test_residual_stack_final_conv_streams_through_its_slot_history(gpu, splits):
+    """Chunked decode with every unit's history and the final conv's own history (chunks shorter
+    than its six-sample context included) equals the whole rows, bit for bit."""
+    dilations = (1, 3, 9)
+    units, out_a, out_b = make_units(dilations, gpu, seed=13)
+    w, b = final_conv_weights(gpu, seed=3)
+    batch, length = 3, sum(splits)
+    gen = torch.Generator().manual_seed(9)
+    x = (torch.randn(batch, length, C, generator=gen) * 0.3).to(gpu)
+    whole = torch.empty(batch, 1, length, device=gpu)
+    residual_stack(x, units, None, out_a, out_b, final=FinalConv(w, b, N.ACT_TANH, whole))
+    slots = 5
+    hists = [torch.zeros(slots, 2, 6 * d, C, dtype=torch.bfloat16, device=gpu) for d in dilations]
+    fhist = torch.randn(slots, 2, 6, C, device=gpu).to(torch.bfloat16)  # cold start ignores it
+    parity = torch.zeros(slots, dtype=torch.int64, device=gpu)
+    slot_index = torch.tensor([4, 1, 2], device=gpu)
+    parts, start = [], 0
+    for n, size in enumerate(splits):
+        xc = x[:, start:start + size].contiguous()
+        wave = torch.empty(batch, 1, size, device=gpu)
+        residual_stack(xc, units, None, out_a, out_b, histories=hists, slot_index=slot_index,
+                       slot_parity=parity, history_cold=n == 0,
+                       final=FinalConv(w, b, N.ACT_TANH, wave, fhist))
+        parity[slot_index] += 1
+        parts.append(wave)
+        start += size
+    assert torch.equal(torch.cat(parts, dim=-1), whole)
