@@ -50,7 +50,7 @@ STREAMS = 64
 
 KERNEL_NAMES = {
     "stack96": "residual_stack_kernel, 96 channels: 3 residual units (conv k7 dilation 1/3/9 + "
-               "Snake + conv k1 + residual) per launch",
+               "Snake + conv k1 + residual) and the final conv 96->1 k7 + tanh per launch",
     "unit96": "conv_mfma_kernel fused residual unit, 96 channels (conv k7 + Snake + conv k1 + "
               "residual)",
     "unit192": "conv_mfma_kernel fused residual unit, 192 channels (conv k7 + Snake + conv k1 + "
@@ -213,7 +213,7 @@ def bench_streaming(args, device) -> dict:
         result["rvq_gather"]["large_batch"] = measure_rvq_large(device)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(config, weights, frames=24, streams=2)
+        result["cpu_baseline"] = cpu_baseline(config, weights, frames=240, streams=6)
     return result
 
 
@@ -221,11 +221,12 @@ def bench_streaming(args, device) -> dict:
 # `bench.py --only stack96` (FETCH_SIZE, then WRITE_SIZE), each scaled by the same counter's
 # reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB, WRITE_SIZE =
 # 1024 MiB: fetch x 2, write x 1); profiles/residual_stack96_pmc.md.
-PMC_TRAFFIC_BYTES = {"stack96": (380356 * 2 + 276480) * 1024}
+PMC_TRAFFIC_BYTES = {"stack96": (385682 * 2 + 5836) * 1024}
 
 
 def run_only(args, device) -> None:
-    from sglang_omni_amd.kernels.conv import residual_stack
+    from sglang_omni_amd import _native as N
+    from sglang_omni_amd.kernels.conv import FinalConv, residual_stack
     from sglang_omni_amd.models import DacCodecDecoder, make_dac_weights
     from sglang_omni_amd.models.configs import CODEC_24K
 
@@ -241,10 +242,12 @@ def run_only(args, device) -> None:
             raise SystemExit("the decoder's last block runs no 96-channel residual stack")
         gen = torch.Generator().manual_seed(0)
         x = (torch.randn(STREAMS, 23040, 96, generator=gen) * 0.3).to(device)
-        out = torch.empty(x.shape, dtype=torch.bfloat16, device=device)
+        wave = torch.empty(STREAMS, 1, 23040, dtype=torch.float32, device=device)
+        final = FinalConv(decoder.final_weight, decoder.final_bias, N.ACT_TANH, wave)
         last = blk.units[-1]
-        fn = lambda: residual_stack(x, blk.stack, out, last.next_a, last.next_b)  # noqa: E731
-        what = "residual stack, 96 channels, x [64, 23040, 96]"
+        fn = lambda: residual_stack(x, blk.stack, None, last.next_a, last.next_b,  # noqa: E731
+                                    final=final)
+        what = "residual stack + final conv, 96 channels, x [64, 23040, 96]"
     for _ in range(2):
         fn()
     sync()
