@@ -213,7 +213,7 @@ def bench_streaming(args, device) -> dict:
         result["rvq_gather"]["large_batch"] = measure_rvq_large(device)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(config, weights, frames=240, streams=6)
+        result["cpu_baseline"] = cpu_baseline(config, weights, frames=240, streams=10)
     return result
 
 

@@ -4,10 +4,10 @@
 namespace omni_conv {
 
 int launch_dma_taps1(const ConvParams& p, hipStream_t stream) {
-  // 192 columns x 192 positions, 8 waves of 96 x 48; 96 x 256, 8 waves of 96 x 32; 96 x 192,
-  // 4 waves of 96 x 48 with three chunks per stage
-  return launch_first_fit<DmaConfig<2, 4, 6, 3, 192, 1, 2>, DmaConfig<1, 8, 6, 2, 256, 1, 2>,
-                          DmaConfig<1, 4, 6, 3, 192, 1, 3>>(p, stream);
+  // 192 columns x 192 positions, 8 waves of 96 x 48 with two chunks per stage; 96 x 192, 8 waves
+  // of 48 x 48 with three chunks per stage; 96 x 256, 8 waves of 96 x 32
+  return launch_first_fit<DmaConfig<2, 4, 6, 3, 192, 1, 2>, DmaConfig<2, 4, 3, 3, 192, 1, 3>,
+                          DmaConfig<1, 8, 6, 2, 256, 1, 2>>(p, stream);
 }
 
 }  // namespace omni_conv

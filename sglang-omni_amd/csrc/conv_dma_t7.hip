@@ -4,10 +4,10 @@
 namespace omni_conv {
 
 int launch_dma_taps7(const ConvParams& p, hipStream_t stream) {
-  // 96 columns x 384 positions, 8 waves of 96 x 48 (two per SIMD); 96 x 192, 4 waves of 96 x 48;
-  // 96 x 256, 8 waves of 96 x 32 (staged rows: positions plus a halo of up to 54 per segment)
-  return launch_first_fit<DmaConfig<1, 8, 6, 3, 496, 7, 1>, DmaConfig<1, 4, 6, 3, 368, 7, 1>,
-                          DmaConfig<1, 8, 6, 2, 480, 7, 1>>(p, stream);
+  // 96 columns x 384 positions, 8 waves of 96 x 48 (two per SIMD); 96 x 192, 8 waves of 48 x 48;
+  // 96 x 192, 4 waves of 96 x 48 (staged rows: positions plus a halo of up to 54 per segment)
+  return launch_first_fit<DmaConfig<1, 8, 6, 3, 496, 7, 1>, DmaConfig<2, 4, 3, 3, 368, 7, 1>,
+                          DmaConfig<1, 4, 6, 3, 368, 7, 1>>(p, stream);
 }
 
 }  // namespace omni_conv
