@@ -10,15 +10,18 @@ from .configs import (
     make_hifigan_weights,
 )
 from .dac_codec import CodecStatePool, DacCodecDecoder
+from .graph_runner import CodecGraphRunner, GraphKey
 from .hifigan import HifiGanVocoder
 
 __all__ = [
     "CODEC_24K",
     "CODEC_24K_LONG",
     "HIFIGAN_24K",
+    "CodecGraphRunner",
     "CodecStatePool",
     "DacCodecDecoder",
     "DacDecoderConfig",
+    "GraphKey",
     "HifiGanConfig",
     "HifiGanVocoder",
     "make_dac_weights",
