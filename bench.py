@@ -16,6 +16,7 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
                 on this host's cores on a bounded sample of the same workload;
   other_configs the xRT of the other decoder configurations: the single 20 s utterance, the
                 HiFiGAN mel vocoder (16 x 10 s) and the fp8-weight long form (8 x 120 s);
+  hift_transforms  HiFT's source spectrum and fused iSTFT tail at the HiFiGAN size, in HBM GB/s;
   calibration   the box's practical peaks: a 1 GiB copy and a bf16 8192^3 GEMM.
 
 --only stack96 / --only copy run one kernel alone for hardware-counter profiles: the roofline
@@ -301,6 +302,29 @@ def bench_other_configs(device) -> dict:
     return out
 
 
+def bench_hift_transforms(device) -> dict:
+    """HiFT's transforms at the HiFiGAN configuration's size (16 rows x 10 s at 24 kHz, n_fft 16,
+    hop 4): the source spectrum (240 000 samples -> 18 x 60 001) and the fused iSTFT tail
+    (18 x 60 001 channels-last -> 240 000 samples), as HBM bytes per second."""
+    from sglang_omni_amd.kernels.hift import HiftStft
+
+    st = HiftStft(torch.hann_window(16, periodic=True), 4, device=device)
+    gen = torch.Generator().manual_seed(0)
+    rows, samples = 16, 240000
+    frames = samples // 4 + 1
+    x = torch.randn(rows, samples, generator=gen).to(device)
+    h = (torch.randn(rows, frames, 18, generator=gen) * 0.5 - 3.0).to(device)
+    out = {}
+    for name, fn, nbytes in (
+            ("spectrum", lambda: st.spectrum(x), 4 * rows * (samples + 18 * frames)),
+            ("istft_tail", lambda: st.tail(h), 4 * rows * (18 * frames + 4 * (frames - 1)))):
+        dt = timed_call(fn, reps=10)
+        gbps = nbytes / dt / 1e9
+        out[name] = {"us": round(dt * 1e6, 1), "bytes": nbytes, "achieved_GBps": round(gbps, 1),
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4)}
+    return out
+
+
 def calibrate(device) -> dict:
     """The box's practical peaks: a 1 GiB device copy (HBM) and a 8192^3 bf16 GEMM (torch's
     hipBLASLt, the MFMA reference point)."""
@@ -369,6 +393,7 @@ def main() -> None:
     if not args.no_other_configs:
         log("other configurations ...")
         line["other_configs"] = bench_other_configs(device)
+        line["hift_transforms"] = bench_hift_transforms(device)
         line["calibration"] = calibrate(device)
     print(json.dumps(line), flush=True)
 

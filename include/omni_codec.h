@@ -42,6 +42,13 @@
  *                                (sglang_omni/models/qwen3_omni/components/code2wav.py:459)
  *   omni_codec_capabilities      no kernel counterpart; the platform query of
  *                                sglang_omni/platforms/rocm.py:22-131
+ *   omni_short_time_spectrum     short_time_spectrum (sglang_omni/models/fun_cosyvoice3/
+ *                                hift_kernels.py:116-146,304-330); with centring, the reflect
+ *                                padding of HiftChannelsLast.spectrum (hift_channels_last.py:
+ *                                108-115) folded in
+ *   omni_overlap_add_inverse     overlap_add_inverse (hift_kernels.py:148-191,333-360)
+ *   omni_istft_tail              HiftChannelsLast's exp / sin of the last conv's output, inverse
+ *                                and clamp (hift_channels_last.py:117-125,269-276) in one launch
  */
 #ifndef OMNI_CODEC_H_
 #define OMNI_CODEC_H_
@@ -355,6 +362,39 @@ int omni_snake(const void* x, void* y, int dtype, int64_t batch, int64_t frames,
    step (graph-capturable). */
 int omni_advance_slots(int64_t* slot_parity, int64_t num_slots, const int64_t* slot_index,
                        int64_t rows, omni_stream_t stream);
+
+/*
+ * HiFT's short-time Fourier transform and its inverse (n_fft <= 64, hop divides n_fft,
+ * bins = n_fft / 2 + 1; every output summed in one fixed order, float32).
+ *
+ * omni_short_time_spectrum: spectrum [rows][2 * bins][frames] (real parts, then imaginary) with
+ *   spectrum[r, c, f] = sum_{k < n_fft} xp[r, f * hop + k] * basis[c * n_fft + k], where xp is the
+ *   signal reflect-padded by n_fft / 2 on both sides when center (needs samples > n_fft / 2), else
+ *   the signal itself (already padded); frames = (padded_samples - n_fft) / hop + 1. basis is
+ *   [2 * bins][n_fft]: the windowed cosines, then the windowed negative sines.
+ * omni_overlap_add_inverse: torch.istft (center = True, one-sided) of real / imag
+ *   [rows][bins][frames]: out[r, i] = (sum over the frames f covering padded position
+ *   p = i + n_fft / 2 of sum_{b < bins} real[r, b, f] * basis[b, t] + imag[r, b, f] *
+ *   basis[bins + b, t]) / (sum over the same frames of squared_window[t]), t = p - f * hop, for
+ *   i < hop * (frames - 1); basis [2 * bins][n_fft] is the one-sided inverse's windowed cosines and
+ *   negative sines (bins 1 .. bins-2 doubled) divided by n_fft.
+ * omni_istft_tail: the same inverse of magnitude = min(exp(h[r, f, b]), magnitude_clip) and
+ *   phase = sin(h[r, f, bins + b]) (real = magnitude * cos(phase), imag = magnitude * sin(phase)),
+ *   h the vocoder's last conv output, channels-last float32 at r * h_stride_row +
+ *   f * h_stride_frame + c, then clamped to [-audio_limit, audio_limit].
+ */
+int omni_short_time_spectrum(const float* signal, int64_t rows, int64_t samples,
+                             int64_t signal_stride_row, int center, const float* basis,
+                             int64_t bins, int64_t n_fft, int64_t hop, float* spectrum,
+                             int64_t frames, omni_stream_t stream);
+int omni_overlap_add_inverse(const float* real, const float* imag, int64_t rows, int64_t bins,
+                             int64_t frames, const float* basis, const float* squared_window,
+                             int64_t n_fft, int64_t hop, float* out, int64_t out_stride_row,
+                             omni_stream_t stream);
+int omni_istft_tail(const float* h, int64_t rows, int64_t frames, int64_t h_stride_row,
+                    int64_t h_stride_frame, const float* basis, const float* squared_window,
+                    int64_t bins, int64_t n_fft, int64_t hop, float magnitude_clip,
+                    float audio_limit, float* out, int64_t out_stride_row, omni_stream_t stream);
 
 #ifdef __cplusplus
 }

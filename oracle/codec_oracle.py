@@ -26,6 +26,11 @@ Parity pins (what fixes each function independently of this file's own formulas)
                             pure-torch reference functions (tests/unit_test/kernels/
                             test_codec_state.py:17-49), pinned by the whole-stream invariants of
                             the same test file (:52-130).
+* ``stft_reference`` / ``istft_reference`` / ``hift_istft_tail`` — torch.stft / torch.istft
+                            (the library routines HiFT calls, hift.py:209-247) in float64; the
+                            round trip istft(stft(x)) = x (Hann window at hop n_fft / 4 sums to a
+                            constant); the DC and Nyquist bins of a constant / alternating signal;
+                            ``hann_window`` against scipy's get_window.
 """
 
 from __future__ import annotations
@@ -317,6 +322,81 @@ def dequantize_fp8_per_channel(q: torch.Tensor, scale: torch.Tensor) -> torch.Te
     """W_deq[co] = float(q[co]) * s[co]."""
     shape = [-1] + [1] * (q.dim() - 1)
     return q.float() * scale.reshape(shape)
+
+
+# --------------------------------------------------------------------------------------------
+# HiFT's iSTFT tail (the next row after the config-4 body)
+# --------------------------------------------------------------------------------------------
+
+
+def hann_window(n_fft: int) -> torch.Tensor:
+    """The periodic Hann window scipy's get_window("hann", n_fft, fftbins=True) returns, as
+    float32 (sglang_omni/models/minicpm_o/components/token2wav/hift.py:197-205):
+    0.5 - 0.5 cos(2 pi k / n_fft)."""
+    k = torch.arange(n_fft, dtype=torch.float64)
+    return (0.5 - 0.5 * torch.cos(2 * math.pi * k / n_fft)).float()
+
+
+def stft_reference(signal: torch.Tensor, window: torch.Tensor, n_fft: int, hop: int) -> torch.Tensor:
+    """The centred one-sided STFT of HiFT.stft (hift.py:209-227: torch.stft with win_length =
+    n_fft, reflect padding of n_fft / 2) from its definition, in float64: X[r, b, f] =
+    sum_k xp[r, f hop + k] w[k] exp(-2 pi i b k / n_fft). Returns (rows, 2 * bins, frames), the
+    real parts then the imaginary parts (the layout of hift_kernels.py:304-330)."""
+    x = signal.to(torch.float64)
+    half = n_fft // 2
+    xp = F.pad(x[:, None], (half, half), mode="reflect")[:, 0]
+    frames = (xp.shape[1] - n_fft) // hop + 1
+    idx = torch.arange(frames)[:, None] * hop + torch.arange(n_fft)[None, :]
+    seg = xp[:, idx] * window.to(torch.float64)  # (rows, frames, n_fft)
+    bins = n_fft // 2 + 1
+    angle = 2 * math.pi / n_fft * torch.outer(torch.arange(bins, dtype=torch.float64),
+                                              torch.arange(n_fft, dtype=torch.float64))
+    real = torch.einsum("rfk,bk->rbf", seg, torch.cos(angle))
+    imag = -torch.einsum("rfk,bk->rbf", seg, torch.sin(angle))
+    return torch.cat([real, imag], dim=1)
+
+
+def istft_reference(real: torch.Tensor, imag: torch.Tensor, window: torch.Tensor, n_fft: int,
+                    hop: int) -> torch.Tensor:
+    """HiFT.istft's torch.istft (hift.py:229-247, center = True, one-sided, win_length = n_fft)
+    from its definition, in float64: each frame's inverse DFT y_f[k] = (1 / n_fft) sum_b c_b
+    Re(X[b, f] exp(2 pi i b k / n_fft)) with c_b = 1 for DC and Nyquist and 2 between, windowed
+    and overlap-added, divided by the overlap-added squared window, with n_fft / 2 samples
+    trimmed at each end: (rows, hop * (frames - 1))."""
+    re, im = real.to(torch.float64), imag.to(torch.float64)
+    rows, bins, frames = re.shape
+    w = window.to(torch.float64)
+    angle = 2 * math.pi / n_fft * torch.outer(torch.arange(bins, dtype=torch.float64),
+                                              torch.arange(n_fft, dtype=torch.float64))
+    c = torch.full((bins, 1), 2.0, dtype=torch.float64)
+    c[0] = 1.0
+    c[-1] = 1.0
+    yf = (torch.einsum("rbf,bk->rfk", re, c * torch.cos(angle))
+          - torch.einsum("rbf,bk->rfk", im, c * torch.sin(angle))) / n_fft
+    total = n_fft + hop * (frames - 1)
+    y = torch.zeros(rows, total, dtype=torch.float64)
+    env = torch.zeros(total, dtype=torch.float64)
+    for f in range(frames):
+        y[:, f * hop:f * hop + n_fft] += yf[:, f] * w
+        env[f * hop:f * hop + n_fft] += w * w
+    half = n_fft // 2
+    return (y / env)[:, half:half + hop * (frames - 1)]
+
+
+def hift_istft_tail(h: torch.Tensor, window: torch.Tensor, n_fft: int, hop: int, *,
+                    magnitude_clip: float = 100.0, audio_limit: float = 0.99) -> torch.Tensor:
+    """The tail of HiFT's decode from the last conv's output h (rows, frames, >= 2 * bins
+    channels-last): magnitude = exp(h[..., :bins]) clipped above at magnitude_clip, phase =
+    sin(h[..., bins:2 bins]), inverse transform, clamp to +-audio_limit
+    (sglang_omni/models/fun_cosyvoice3/hift_channels_last.py:117-125,269-276; hift.py:229-251).
+    Float64 throughout."""
+    bins = n_fft // 2 + 1
+    hd = h.to(torch.float64)
+    magnitude = torch.clip(torch.exp(hd[..., :bins]), max=magnitude_clip).transpose(1, 2)
+    phase = torch.sin(hd[..., bins:2 * bins]).transpose(1, 2)
+    y = istft_reference(magnitude * torch.cos(phase), magnitude * torch.sin(phase), window,
+                        n_fft, hop)
+    return torch.clamp(y, -audio_limit, audio_limit)
 
 
 def snr_db(reference: torch.Tensor, actual: torch.Tensor) -> float:

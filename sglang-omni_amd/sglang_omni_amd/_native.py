@@ -38,6 +38,7 @@ class OmniCodecError(RuntimeError):
         self.status = status
 
 
+INVALID_ARG = 1
 UNSUPPORTED = 2
 
 
@@ -181,6 +182,12 @@ SIGNATURES: dict[str, list] = {
                              _PTR, _I64, _INT, _PTR],
     "omni_snake": [_PTR, _PTR, _INT, _I64, _I64, _I64, _INT, _PTR, _PTR, _INT, _PTR],
     "omni_advance_slots": [_PTR, _I64, _PTR, _I64, _PTR],
+    "omni_short_time_spectrum": [_PTR, _I64, _I64, _I64, _INT, _PTR, _I64, _I64, _I64, _PTR, _I64,
+                                 _PTR],
+    "omni_overlap_add_inverse": [_PTR, _PTR, _I64, _I64, _I64, _PTR, _PTR, _I64, _I64, _PTR, _I64,
+                                 _PTR],
+    "omni_istft_tail": [_PTR, _I64, _I64, _I64, _I64, _PTR, _PTR, _I64, _I64, _I64,
+                        ctypes.c_float, ctypes.c_float, _PTR, _I64, _PTR],
 }
 _RESTYPES = {"omni_codec_error_string": ctypes.c_char_p}
 

@@ -475,3 +475,93 @@ def test_snr_db():
     # noise at 1 % of the signal amplitude is 40 dB (1.01 is inexact in float32)
     assert abs(O.snr_db(ref, ref * 1.01) - 40.0) < 1e-4
     assert abs(O.snr_db(ref, ref * 1.1) - 20.0) < 1e-4
+
+
+# ------------------------------------------------------------------ HiFT iSTFT tail
+
+
+def test_hann_window_is_scipys_periodic_hann():
+    from scipy.signal import get_window
+
+    for n in (8, 16, 32):
+        assert torch.equal(O.hann_window(n),
+                           torch.from_numpy(get_window("hann", n, fftbins=True).astype("float32")))
+
+
+@pytest.mark.parametrize("n_fft,hop,length", [(16, 4, 101), (16, 4, 9), (32, 8, 257), (8, 2, 40)])
+def test_stft_reference_is_torch_stft(n_fft, hop, length):
+    gen = torch.Generator().manual_seed(n_fft + length)
+    x = torch.randn(3, length, generator=gen, dtype=torch.float64)
+    w = O.hann_window(n_fft)
+    spec = O.stft_reference(x, w, n_fft, hop)
+    ref = torch.stft(x, n_fft, hop, n_fft, window=w.double(), return_complex=True)
+    bins = n_fft // 2 + 1
+    torch.testing.assert_close(spec[:, :bins], ref.real, rtol=0, atol=1e-12)
+    torch.testing.assert_close(spec[:, bins:], ref.imag, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("n_fft,hop,frames", [(16, 4, 26), (16, 4, 3), (32, 8, 40)])
+def test_istft_reference_is_torch_istft(n_fft, hop, frames):
+    gen = torch.Generator().manual_seed(frames)
+    bins = n_fft // 2 + 1
+    re = torch.randn(2, bins, frames, generator=gen, dtype=torch.float64)
+    im = torch.randn(2, bins, frames, generator=gen, dtype=torch.float64)
+    im[:, 0] = 0  # a real signal's DC and Nyquist bins are real
+    im[:, -1] = 0
+    w = O.hann_window(n_fft)
+    y = O.istft_reference(re, im, w, n_fft, hop)
+    ref = torch.istft(torch.complex(re, im), n_fft, hop, n_fft, window=w.double())
+    torch.testing.assert_close(y, ref, rtol=0, atol=1e-12)
+
+
+def test_istft_of_stft_reconstructs_the_signal():
+    """The Hann window at hop n_fft / 4 overlap-adds to a constant: istft(stft(x)) = x."""
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 400, generator=gen, dtype=torch.float64)
+    w = O.hann_window(16)
+    spec = O.stft_reference(x, w, 16, 4)
+    y = O.istft_reference(spec[:, :9], spec[:, 9:], w, 16, 4)
+    torch.testing.assert_close(y, x[:, :y.shape[1]], rtol=0, atol=1e-12)
+
+
+def test_stft_reference_dc_and_nyquist_bins():
+    """The periodic Hann window's DFT is N/2 at bin 0 and -N/4 at bins +-1 (w = 1/2 - cos / 2):
+    a constant signal gives X[0] = N/2, X[1] = -N/4 and nothing else; an alternating one
+    |X[N/2]| = N/2, |X[N/2 - 1]| = N/4 and nothing else (frames clear of the reflected edges;
+    the float32 window rounds at 1e-7)."""
+    n = 16
+    w = O.hann_window(n)
+    mid = O.stft_reference(torch.ones(1, 64, dtype=torch.float64), w, n, 4)[0, :, 4:-4]
+    torch.testing.assert_close(mid[0], torch.full_like(mid[0], n / 2), rtol=0, atol=1e-6)
+    torch.testing.assert_close(mid[1], torch.full_like(mid[1], -n / 4), rtol=0, atol=1e-6)
+    assert mid[2:].abs().max().item() < 1e-6
+    alt = (-1.0) ** torch.arange(64, dtype=torch.float64)[None]
+    spec = O.stft_reference(alt, w, n, 4)[0, :, 4:-4]
+    bins = n // 2 + 1
+    mag = torch.sqrt(spec[:bins] ** 2 + spec[bins:] ** 2)
+    torch.testing.assert_close(mag[n // 2], torch.full_like(mag[0], n / 2), rtol=0, atol=1e-6)
+    torch.testing.assert_close(mag[n // 2 - 1], torch.full_like(mag[0], n / 4), rtol=0, atol=1e-6)
+    assert mag[:n // 2 - 1].abs().max().item() < 1e-6
+
+
+def test_hift_tail_reference_clips_and_clamps():
+    """Magnitudes above the clip count as the clip; the output never leaves +-audio_limit, and
+    small inputs pass through unclamped (equal to the unclamped inverse)."""
+    gen = torch.Generator().manual_seed(4)
+    n_fft, hop, bins = 16, 4, 9
+    h = torch.randn(2, 30, 2 * bins, generator=gen, dtype=torch.float64)
+    h[..., :bins] = h[..., :bins] * 0.5 - 4.0  # magnitudes around e^-4
+    w = O.hann_window(n_fft)
+    y = O.hift_istft_tail(h, w, n_fft, hop)
+    mag = torch.exp(h[..., :bins]).transpose(1, 2)
+    ph = torch.sin(h[..., bins:]).transpose(1, 2)
+    free = O.istft_reference(mag * torch.cos(ph), mag * torch.sin(ph), w, n_fft, hop)
+    assert free.abs().max().item() < 0.99
+    torch.testing.assert_close(y, free, rtol=0, atol=0)
+    h2 = h.clone()
+    h2[..., :bins] = 10.0  # exp(10) > 100: clipped to 100
+    y2 = O.hift_istft_tail(h2, w, n_fft, hop)
+    h3 = h2.clone()
+    h3[..., :bins] = math.log(100.0)
+    torch.testing.assert_close(y2, O.hift_istft_tail(h3, w, n_fft, hop), rtol=0, atol=1e-12)
+    assert y2.abs().max().item() <= 0.99
