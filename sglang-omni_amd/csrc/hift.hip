@@ -2,7 +2,8 @@
 // MiniCPM-o vocoders), on gfx950. Both are HBM-bound: a 16-point transform does 16 MACs per
 // output component, so the kernels read their input once, keep the small bases and the
 // workgroup's window of frames in LDS, and give every output one fixed summation order (so a row's
-// result does not depend on the batch or the tiling).
+// result does not depend on the batch or the tiling). HiFT's geometry (n_fft 16, hop 4) has its
+// own instantiation with the loops unrolled; other sizes take the runtime-sized kernels.
 //
 //   short_time_spectrum: spectrum[r, c, f] = sum_{k < n_fft} x[r, f * hop + k - pad] * basis[c, k]
 //     (c < bins the windowed cosines, c >= bins the windowed negative sines; pad = n_fft / 2 with
@@ -48,34 +49,53 @@ size_t stft_lds_bytes(int n_fft, int hop, int bins) {
   return (size_t)(2 * bins * n_fft + (kFramesPerBlock - 1) * hop + n_fft) * sizeof(float);
 }
 
+// NF, HP: the transform's n_fft and hop when known at compile time (the loops unroll and the
+// frame's samples stay in registers), 0 for the runtime values of the parameters.
+template <int NF, int HP>
 __global__ void __launch_bounds__(kThreads) short_time_spectrum_kernel(const StftParams p) {
   extern __shared__ float smem[];
+  const int n_fft = NF ? NF : p.n_fft;
+  const int hop = HP ? HP : p.hop;
+  const int bins = n_fft / 2 + 1;
+  const int comps = 2 * bins;
   float* basis = smem;
-  float* seg = smem + 2 * p.bins * p.n_fft;
+  float* seg = smem + comps * n_fft;
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.y;
   const int64_t f0 = (int64_t)blockIdx.x * kFramesPerBlock;
-  const int comps = 2 * p.bins;
-  for (int e = tid; e < comps * p.n_fft; e += kThreads) basis[e] = p.basis[e];
+  for (int e = tid; e < comps * n_fft; e += kThreads) basis[e] = p.basis[e];
   // the block's signal span: frames f0 .. f0 + kFramesPerBlock - 1 read padded samples
   // f0 * hop .. (f0 + kFramesPerBlock - 1) * hop + n_fft - 1
   const int64_t nframes = min((int64_t)kFramesPerBlock, p.frames - f0);
-  const int span = (int)((nframes - 1) * p.hop + p.n_fft);
-  const int pad = p.center ? p.n_fft / 2 : 0;
+  const int span = (int)((nframes - 1) * hop + n_fft);
+  const int pad = p.center ? n_fft / 2 : 0;
   const float* xr = p.x + row * p.x_stride;
   for (int e = tid; e < span; e += kThreads) {
-    int64_t i = f0 * p.hop + e - pad;
+    int64_t i = f0 * hop + e - pad;
     if (p.center) i = reflect(i, p.samples);
     seg[e] = xr[i];
   }
   __syncthreads();
-  if (tid < nframes) {
-    const float* s = seg + tid * p.hop;
-    float* o = p.out + (row * comps) * p.frames + f0 + tid;
+  if (tid >= nframes) return;
+  float* o = p.out + (row * comps) * p.frames + f0 + tid;
+  if constexpr (NF != 0) {
+    float s[NF];
+#pragma unroll
+    for (int k = 0; k < NF; ++k) s[k] = seg[tid * hop + k];
+#pragma unroll 2
     for (int c = 0; c < comps; ++c) {
-      const float* b = basis + c * p.n_fft;
+      const float* b = basis + c * NF;
       float acc = 0.f;
-      for (int k = 0; k < p.n_fft; ++k) acc = __builtin_fmaf(s[k], b[k], acc);
+#pragma unroll
+      for (int k = 0; k < NF; ++k) acc = __builtin_fmaf(s[k], b[k], acc);
+      o[(int64_t)c * p.frames] = acc;
+    }
+  } else {
+    const float* s = seg + tid * hop;
+    for (int c = 0; c < comps; ++c) {
+      const float* b = basis + c * n_fft;
+      float acc = 0.f;
+      for (int k = 0; k < n_fft; ++k) acc = __builtin_fmaf(s[k], b[k], acc);
       o[(int64_t)c * p.frames] = acc;
     }
   }
@@ -111,60 +131,77 @@ size_t inverse_lds_bytes(int n_fft, int hop, int bins) {
          sizeof(float);
 }
 
+template <int NF, int HP>
 __global__ void __launch_bounds__(kThreads) overlap_add_inverse_kernel(const IstftParams p) {
   extern __shared__ float smem[];
+  const int n_fft = NF ? NF : p.n_fft;
+  const int hop = HP ? HP : p.hop;
+  const int bins = n_fft / 2 + 1;
+  const int comps = 2 * bins;
+  const int half = n_fft / 2;
+  const int overlaps = n_fft / hop;
   float* basis = smem;
-  float* win2 = basis + 2 * p.bins * p.n_fft;
-  float* spec = win2 + p.n_fft;
+  float* win2 = basis + comps * n_fft;
+  float* spec = win2 + n_fft;
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.y;
   const int64_t i0 = (int64_t)blockIdx.x * kSamplesPerBlock;
-  const int bins = p.bins;
-  const int comps = 2 * bins;
-  const int half = p.n_fft / 2;
-  const int overlaps = p.n_fft / p.hop;
-  for (int e = tid; e < comps * p.n_fft; e += kThreads) basis[e] = p.basis[e];
-  for (int e = tid; e < p.n_fft; e += kThreads) win2[e] = p.win2[e];
+  for (int e = tid; e < comps * n_fft; e += kThreads) basis[e] = p.basis[e];
+  for (int e = tid; e < n_fft; e += kThreads) win2[e] = p.win2[e];
   // frames whose window covers samples i0 .. i0 + kSamplesPerBlock - 1 (padded positions
   // i + half): from (i0 + half) / hop - (overlaps - 1) to (i0 + kSamplesPerBlock - 1 + half) / hop
-  const int64_t fa = (i0 + half) / p.hop - (overlaps - 1);
-  const int64_t fb = (i0 + kSamplesPerBlock - 1 + half) / p.hop;
+  const int64_t fa = (i0 + half) / hop - (overlaps - 1);
+  const int64_t fb = (i0 + kSamplesPerBlock - 1 + half) / hop;
   const int nf = (int)(fb - fa + 1);
-  for (int e = tid; e < nf * comps; e += kThreads) {
-    const int j = e / comps;  // frame within the window
-    const int c = e - j * comps;
-    const int64_t f = fa + j;
-    float v = 0.f;
-    if (f >= 0 && f < p.frames) {
-      if (p.tail) {
-        // one (magnitude, phase) pair per bin; component c < bins the real part, else the
-        // imaginary part of bin c - bins
-        const int b = c < bins ? c : c - bins;
+  if (p.tail) {
+    // one thread per (frame, bin): magnitude and phase once, both parts out
+    for (int e = tid; e < nf * bins; e += kThreads) {
+      const int j = e / bins;  // frame within the window
+      const int b = e - j * bins;
+      const int64_t f = fa + j;
+      float re = 0.f, im = 0.f;
+      if (f >= 0 && f < p.frames) {
         const float* hf = p.h + row * p.h_row_stride + f * p.h_frame_stride;
         const float mag = fminf(expf(hf[b]), p.mag_clip);
         const float phase = sinf(hf[bins + b]);
-        v = c < bins ? mag * cosf(phase) : mag * sinf(phase);
-      } else {
+        re = mag * cosf(phase);
+        im = mag * sinf(phase);
+      }
+      spec[j * comps + b] = re;
+      spec[j * comps + bins + b] = im;
+    }
+  } else {
+    for (int e = tid; e < nf * comps; e += kThreads) {
+      const int j = e / comps;  // frame within the window
+      const int c = e - j * comps;
+      const int64_t f = fa + j;
+      float v = 0.f;
+      if (f >= 0 && f < p.frames) {
         const float* src = c < bins ? p.re : p.im;
         const int b = c < bins ? c : c - bins;
         v = src[(row * bins + b) * p.frames + f];
       }
+      spec[j * comps + c] = v;
     }
-    spec[j * comps + c] = v;
   }
   __syncthreads();
   const int64_t i = i0 + tid;
   if (i >= p.samples) return;
   const int64_t pos = i + half;
   float signal = 0.f, envelope = 0.f;
-  for (int o = 0; o < overlaps; ++o) {
-    const int64_t f = pos / p.hop - o;
+#pragma unroll
+  for (int o = 0; o < (NF ? NF / HP : kMaxFft); ++o) {
+    if (!NF && o >= overlaps) break;
+    const int64_t f = pos / hop - o;
     if (f < 0 || f >= p.frames) continue;
-    const int t = (int)(pos - f * p.hop);
+    const int t = (int)(pos - f * hop);
     const float* s = spec + (int)(f - fa) * comps;
-    for (int b = 0; b < bins; ++b)
-      signal += __builtin_fmaf(s[b], basis[b * p.n_fft + t],
-                               s[bins + b] * basis[(bins + b) * p.n_fft + t]);
+#pragma unroll
+    for (int b = 0; b < (NF ? NF / 2 + 1 : kMaxFft / 2 + 1); ++b) {
+      if (!NF && b >= bins) break;
+      signal += __builtin_fmaf(s[b], basis[b * n_fft + t],
+                               s[bins + b] * basis[(bins + b) * n_fft + t]);
+    }
     envelope += win2[t];
   }
   float y = signal / envelope;
@@ -204,9 +241,12 @@ extern "C" int omni_short_time_spectrum(const float* signal, int64_t rows, int64
   p.frames = frames;
   p.out = spectrum;
   dim3 grid((unsigned)((frames + kFramesPerBlock - 1) / kFramesPerBlock), (unsigned)rows);
-  hipLaunchKernelGGL(short_time_spectrum_kernel, grid, dim3(kThreads),
-                     stft_lds_bytes(p.n_fft, p.hop, p.bins), reinterpret_cast<hipStream_t>(stream),
-                     p);
+  const size_t lds = stft_lds_bytes(p.n_fft, p.hop, p.bins);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (p.n_fft == 16 && p.hop == 4)
+    hipLaunchKernelGGL((short_time_spectrum_kernel<16, 4>), grid, dim3(kThreads), lds, s, p);
+  else
+    hipLaunchKernelGGL((short_time_spectrum_kernel<0, 0>), grid, dim3(kThreads), lds, s, p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
 }
@@ -220,9 +260,12 @@ int launch_inverse(IstftParams& p, int64_t rows, omni_stream_t stream) {
   if (rows == 0 || p.samples == 0) return OMNI_OK;
   if (rows > 65535 || p.samples > 0x7fffffffLL - kSamplesPerBlock) return OMNI_ERR_UNSUPPORTED;
   dim3 grid((unsigned)((p.samples + kSamplesPerBlock - 1) / kSamplesPerBlock), (unsigned)rows);
-  hipLaunchKernelGGL(overlap_add_inverse_kernel, grid, dim3(kThreads),
-                     inverse_lds_bytes(p.n_fft, p.hop, p.bins), reinterpret_cast<hipStream_t>(stream),
-                     p);
+  const size_t lds = inverse_lds_bytes(p.n_fft, p.hop, p.bins);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (p.n_fft == 16 && p.hop == 4)
+    hipLaunchKernelGGL((overlap_add_inverse_kernel<16, 4>), grid, dim3(kThreads), lds, s, p);
+  else
+    hipLaunchKernelGGL((overlap_add_inverse_kernel<0, 0>), grid, dim3(kThreads), lds, s, p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
 }
