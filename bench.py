@@ -17,6 +17,8 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
   other_configs the xRT of the other decoder configurations: the single 20 s utterance, the
                 HiFiGAN mel vocoder (16 x 10 s) and the fp8-weight long form (8 x 120 s);
   hift_transforms  HiFT's source spectrum and fused iSTFT tail at the HiFiGAN size, in HBM GB/s;
+  egress        one step's waveform leaving the device: the PCM16 egress kernel (HBM GB/s) and
+                the staging of the step through a pinned slot to host arrays (PCIe-inclusive);
   calibration   the box's practical peaks: a 1 GiB copy and a bf16 8192^3 GEMM.
 
 --only stack96 / --only copy run one kernel alone for hardware-counter profiles: the roofline
@@ -325,6 +327,48 @@ def bench_hift_transforms(device) -> dict:
     return out
 
 
+def bench_egress(device) -> dict:
+    """One streaming decode step's waveform (64 rows x 23 040 samples) leaving the device: the
+    PCM16 egress kernel alone (HBM bytes per second), and the host-visible time of staging the
+    step through a pinned slot and reading every row back (PCIe-inclusive), as float32 and as
+    PCM16."""
+    from sglang_omni_amd.kernels.egress import waveform_egress
+    from sglang_omni_amd.scheduling import WaveformEgress
+    from sglang_omni_amd.utils.timing import LaunchTimer
+
+    rows, samples = 64, 23040
+    w = (torch.rand(rows, 1, samples, device=device) * 2.2 - 1.1).contiguous()
+    out = torch.empty(rows, samples, dtype=torch.int16, device=device)
+    waveform_egress(w, format="pcm16", out=out)
+    # one event pair around 50 back-to-back launches: a single launch is too short for a pair
+    timer = LaunchTimer()
+    with timer.launch("egress", 0.0):
+        for _ in range(50):
+            waveform_egress(w, format="pcm16", out=out)
+    sync()
+    dt = timer.summary()["egress"]["ms"] / 50 / 1e3
+    nbytes = rows * samples * (4 + 2)
+    line = {"pcm16_kernel": {"us": round(dt * 1e6, 2), "bytes": nbytes,
+                             "achieved_GBps": round(nbytes / dt / 1e9, 1),
+                             "frac": round(nbytes / dt / 1e9 / PEAK_HBM_GBPS, 4)}}
+    ids = list(range(rows))
+    for fmt in ("f32", "pcm16"):
+        egress = WaveformEgress(device, format=fmt, max_pinned_slots=2)
+        egress.stage_step(ids, w)
+        egress.flush()
+        reps = 20
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            egress.stage_step(ids, w)
+            egress.flush()
+        dt = (time.perf_counter() - t0) / reps
+        host_bytes = rows * samples * (2 if fmt == "pcm16" else 4)
+        line[f"step_to_host_{fmt}"] = {"ms": round(dt * 1e3, 3), "host_bytes": host_bytes,
+                                       "GBps": round(host_bytes / dt / 1e9, 2)}
+    return line
+
+
 def calibrate(device) -> dict:
     """The box's practical peaks: a 1 GiB device copy (HBM) and a 8192^3 bf16 GEMM (torch's
     hipBLASLt, the MFMA reference point)."""
@@ -394,6 +438,7 @@ def main() -> None:
         log("other configurations ...")
         line["other_configs"] = bench_other_configs(device)
         line["hift_transforms"] = bench_hift_transforms(device)
+        line["egress"] = bench_egress(device)
         line["calibration"] = calibrate(device)
     print(json.dumps(line), flush=True)
 

@@ -396,6 +396,26 @@ int omni_istft_tail(const float* h, int64_t rows, int64_t frames, int64_t h_stri
                     int64_t bins, int64_t n_fft, int64_t hop, float magnitude_clip,
                     float audio_limit, float* out, int64_t out_stride_row, omni_stream_t stream);
 
+/*
+ * Waveform egress (no reference counterpart as one call: it replaces the per-request
+ * `slot.view(samples).copy_(waveform)` staging of code2wav_scheduler.py:756-800 and the float32 ->
+ * PCM16 encoding of serve/realtime/session_bridge.py:86-88). Packs rows of a float32 waveform
+ * (wave[r * wave_stride_row + i], i < samples) into out[r * out_stride_row + i] so that one
+ * device-to-host copy moves a whole decode step:
+ *   OMNI_EGRESS_F32    out is float32, the samples unchanged;
+ *   OMNI_EGRESS_PCM16  out is int16: (int16) trunc(clip(v, -1, 1) * 32767.0f), NaN -> 0.
+ * row_samples (nullable, device int64[rows]) stops row r after min(row_samples[r], samples)
+ * samples; the rest of that output row is not written.
+ */
+enum omni_egress_format {
+  OMNI_EGRESS_F32 = 0,
+  OMNI_EGRESS_PCM16 = 1
+};
+
+int omni_waveform_egress(const float* wave, int64_t rows, int64_t samples,
+                         int64_t wave_stride_row, const int64_t* row_samples, int format,
+                         void* out, int64_t out_stride_row, omni_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

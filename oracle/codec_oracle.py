@@ -31,6 +31,9 @@ Parity pins (what fixes each function independently of this file's own formulas)
                             round trip istft(stft(x)) = x (Hann window at hop n_fft / 4 sums to a
                             constant); the DC and Nyquist bins of a constant / alternating signal;
                             ``hann_window`` against scipy's get_window.
+* ``pcm16_encode``        — known answers of the clip / scale / truncate encoding (full scale,
+                            half scale, just below one step, out-of-range and NaN samples) and
+                            numpy's own float32 -> int16 cast of the same clipped product.
 """
 
 from __future__ import annotations
@@ -397,6 +400,35 @@ def hift_istft_tail(h: torch.Tensor, window: torch.Tensor, n_fft: int, hop: int,
     y = istft_reference(magnitude * torch.cos(phase), magnitude * torch.sin(phase), window,
                         n_fft, hop)
     return torch.clamp(y, -audio_limit, audio_limit)
+
+
+# --------------------------------------------------------------------------------------------
+# host egress: the waveform's wire encodings
+# --------------------------------------------------------------------------------------------
+
+
+def pcm16_encode(samples: torch.Tensor) -> torch.Tensor:
+    """float32 samples -> int16 PCM as the realtime bridge encodes them
+    (sglang_omni/serve/realtime/session_bridge.py:86-88): clip to [-1, 1], multiply by 32767 in
+    float32, truncate toward zero. NaN (passed through by the clip) encodes as 0, what numpy's
+    float32 -> int16 cast gives on x86 and what the device conversion gives."""
+    x = samples.to(torch.float32)
+    clipped = torch.where(torch.isnan(x), torch.zeros_like(x), torch.clamp(x, -1.0, 1.0))
+    return torch.trunc(clipped * torch.tensor(32767.0, dtype=torch.float32)).to(torch.int16)
+
+
+def waveform_egress_reference(wave: torch.Tensor, row_samples: list[int] | None = None, *,
+                              format: str = "f32") -> list[torch.Tensor]:
+    """Each row of a (B, 1, samples) or (B, samples) float32 waveform cut to its sample count
+    (the reference's ``audio[i, 0, :n * hop]``, sglang_omni/scheduling/audio_vocoder.py:204-217),
+    as float32 or as PCM16."""
+    rows = wave[:, 0] if wave.dim() == 3 else wave
+    counts = [rows.shape[1]] * rows.shape[0] if row_samples is None else list(row_samples)
+    out = []
+    for r, n in enumerate(counts):
+        row = rows[r, :n].to(torch.float32)
+        out.append(pcm16_encode(row) if format == "pcm16" else row.clone())
+    return out
 
 
 def snr_db(reference: torch.Tensor, actual: torch.Tensor) -> float:

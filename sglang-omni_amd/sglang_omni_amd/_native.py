@@ -18,6 +18,7 @@ OK = 0
 DTYPE_F32, DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_I32, DTYPE_I64 = range(6)
 ACT_NONE, ACT_SNAKE, ACT_LEAKY_RELU, ACT_TANH, ACT_CLAMP = range(5)
 RVQ_MEAN, RVQ_CLAMP = 1, 2
+EGRESS_F32, EGRESS_PCM16 = 0, 1
 
 TORCH_TO_OMNI = {
     torch.float32: DTYPE_F32,
@@ -188,6 +189,7 @@ SIGNATURES: dict[str, list] = {
                                  _PTR],
     "omni_istft_tail": [_PTR, _I64, _I64, _I64, _I64, _PTR, _PTR, _I64, _I64, _I64,
                         ctypes.c_float, ctypes.c_float, _PTR, _I64, _PTR],
+    "omni_waveform_egress": [_PTR, _I64, _I64, _I64, _PTR, _INT, _PTR, _I64, _PTR],
 }
 _RESTYPES = {"omni_codec_error_string": ctypes.c_char_p}
 

@@ -565,3 +565,39 @@ def test_hift_tail_reference_clips_and_clamps():
     h3[..., :bins] = math.log(100.0)
     torch.testing.assert_close(y2, O.hift_istft_tail(h3, w, n_fft, hop), rtol=0, atol=1e-12)
     assert y2.abs().max().item() <= 0.99
+
+
+# ------------------------------------------------------------------------------ host egress
+
+
+def test_pcm16_encode_known_answers():
+    """Hand-computed codes of the clip / scale-by-32767 / truncate encoding: a rounding encoder
+    (0.5 -> 16384), a 32768 scale (1.0 -> overflow), a missing clip or a floor (negative
+    half-scale -> -16384) each fails one of them."""
+    x = torch.tensor([0.0, 1.0, -1.0, 0.5, -0.5, 0.99999, -0.99999, 1.0 / 32767, 0.9 / 32767,
+                      -0.9 / 32767, 2.0, -7.5, float("inf"), float("-inf"), float("nan"),
+                      0.25, -0.000030517578125], dtype=torch.float32)
+    expected = [0, 32767, -32767, 16383, -16383, 32766, -32766, 1, 0, 0, 32767, -32767, 32767,
+                -32767, 0, 8191, 0]
+    got = O.pcm16_encode(x)
+    assert got.dtype == torch.int16
+    assert got.tolist() == expected
+
+
+def test_pcm16_encode_matches_numpy_cast():
+    """numpy's own float32 -> int16 cast of the clipped product (the reference encoder's
+    arithmetic, session_bridge.py:86-88) on finite samples, bit for bit."""
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(50_000, generator=g) * 0.7).float()
+    x[::97] *= 3.0
+    ref = (np.clip(x.numpy(), -1.0, 1.0) * (32768 - 1)).astype("<i2")
+    assert np.array_equal(O.pcm16_encode(x).numpy(), ref)
+
+
+def test_waveform_egress_reference_trims_rows():
+    wave = torch.arange(24, dtype=torch.float32).view(3, 1, 8) / 32.0
+    rows = O.waveform_egress_reference(wave, [8, 3, 0])
+    assert [r.numel() for r in rows] == [8, 3, 0]
+    assert torch.equal(rows[1], wave[1, 0, :3])
+    pcm = O.waveform_egress_reference(wave, None, format="pcm16")
+    assert pcm[2].tolist() == [int(v / 32.0 * 32767) for v in range(16, 24)]
