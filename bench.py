@@ -17,6 +17,8 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
   other_configs the xRT of the other decoder configurations: the single 20 s utterance, the
                 HiFiGAN mel vocoder (16 x 10 s) and the fp8-weight long form (8 x 120 s);
   hift_transforms  HiFT's source spectrum and fused iSTFT tail at the HiFiGAN size, in HBM GB/s;
+  qwen3_code2wav the Qwen3-Omni code2wav (pre-transformer + ConvNeXt + decoder) streaming 64
+                streams x 12-frame chunks, eager and HIP-graph replayed, per-kind kernel times;
   egress        one step's waveform leaving the device: the PCM16 egress kernel (HBM GB/s) and
                 the staging of the step through a pinned slot to host arrays (PCIe-inclusive);
   calibration   the box's practical peaks: a 1 GiB copy and a bf16 8192^3 GEMM.
@@ -304,6 +306,66 @@ def bench_other_configs(device) -> dict:
     return out
 
 
+def bench_qwen3_code2wav(device, steps: int = 20, warmup: int = 3) -> dict:
+    """The Qwen3-Omni code2wav (1024-hidden 8-layer pre-transformer, ConvNeXt upsamplers,
+    1536-channel decoder, x1920 to 24 kHz; seeded random weights) in the streaming serving
+    pattern: 64 streams, one step = one 12-frame chunk of every stream through the slot pool
+    (K / V rings, conv histories), eagerly and replayed from a HIP graph; per-kind kernel times
+    from HIP events on the launch stream."""
+    from sglang_omni_amd.models import (CodecGraphRunner, GraphKey, Qwen3Code2WavDecoder,
+                                        make_qwen3_code2wav_weights)
+    from sglang_omni_amd.models.configs import QWEN3_CODE2WAV, qwen3_code2wav_macs_per_frame
+    from sglang_omni_amd.utils.timing import NO_TIMER, LaunchTimer
+
+    cfg = QWEN3_CODE2WAV
+    dec = Qwen3Code2WavDecoder(make_qwen3_code2wav_weights(cfg, seed=0), cfg, device=device)
+    codes = torch.stack([
+        torch.randint(0, cfg.codebook_size, (cfg.num_quantizers, CHUNK_FRAMES * CHUNKS_PER_STREAM),
+                      generator=torch.Generator().manual_seed(1 + s)) for s in range(STREAMS)])
+    chunks = [codes[..., c * CHUNK_FRAMES:(c + 1) * CHUNK_FRAMES].contiguous().to(device)
+              for c in range(CHUNKS_PER_STREAM)]
+    pool = dec.new_state_pool(num_slots=STREAMS, capture_slots=STREAMS)
+    index = torch.arange(STREAMS, device=device)
+    audio_per_step = STREAMS * CHUNK_FRAMES * cfg.hop_length / cfg.sample_rate
+    flops_per_step = 2.0 * qwen3_code2wav_macs_per_frame(cfg) * STREAMS * CHUNK_FRAMES
+
+    def eager(i: int) -> None:
+        c = i % CHUNKS_PER_STREAM
+        dec.decode_slots(chunks[c], pool, index, first_decode=c == 0)
+
+    out = {"workload": f"Qwen3-Omni code2wav, {STREAMS} streams x {CHUNK_FRAMES}-frame chunks "
+                       f"(72-frame attention window and conv state in the slot pool), bf16",
+           "gflop_per_step": round(flops_per_step / 1e9, 1)}
+    dt = timed_steps(eager, steps, warmup) / steps
+    out["eager"] = {"ms_per_step": round(dt * 1e3, 3), "xRT": round(audio_per_step / dt, 1)}
+    runner = CodecGraphRunner(dec, pool, [GraphKey(STREAMS, CHUNK_FRAMES, "first"),
+                                          GraphKey(STREAMS, CHUNK_FRAMES, "next")])
+    runner.capture_all()
+
+    def graphed(i: int) -> None:
+        c = i % CHUNKS_PER_STREAM
+        runner.run(chunks[c], index, first_decode=c == 0)
+
+    dt = timed_steps(graphed, steps, warmup) / steps
+    out["graph"] = {"ms_per_step": round(dt * 1e3, 3), "xRT": round(audio_per_step / dt, 1),
+                    "TFLOPs": round(flops_per_step / dt / 1e12, 1)}
+    timer = LaunchTimer()
+    dec.timer = timer
+    for i in range(CHUNKS_PER_STREAM):
+        eager(i)
+    sync()
+    dec.timer = NO_TIMER
+    kinds = {}
+    for kind, v in timer.summary().items():
+        entry = {"launches_per_step": round(v["launches"] / CHUNKS_PER_STREAM, 1),
+                 "us_per_step": round(v["ms"] * 1e3 / CHUNKS_PER_STREAM, 1)}
+        if v["work"]:
+            entry["TFLOPs"] = round(v["work"] / (v["ms"] * 1e-3) / 1e12, 1)
+        kinds[kind] = entry
+    out["kernels"] = kinds
+    return out
+
+
 def bench_hift_transforms(device) -> dict:
     """HiFT's transforms at the HiFiGAN configuration's size (16 rows x 10 s at 24 kHz, n_fft 16,
     hop 4): the source spectrum (240 000 samples -> 18 x 60 001) and the fused iSTFT tail
@@ -439,6 +501,7 @@ def main() -> None:
         line["other_configs"] = bench_other_configs(device)
         line["hift_transforms"] = bench_hift_transforms(device)
         line["egress"] = bench_egress(device)
+        line["qwen3_code2wav"] = bench_qwen3_code2wav(device)
         line["calibration"] = calibrate(device)
     print(json.dumps(line), flush=True)
 

@@ -416,6 +416,68 @@ int omni_waveform_egress(const float* wave, int64_t rows, int64_t samples,
                          int64_t wave_stride_row, const int64_t* row_samples, int format,
                          void* out, int64_t out_stride_row, omni_stream_t stream);
 
+/*
+ * The Qwen3-Omni code2wav front (pre-transformer and ConvNeXt upsamplers): the ops around its
+ * plain GEMMs. Activations are bf16 rows (GEMM operands / outputs) and float32 residual streams.
+ *
+ * omni_rms_norm_residual: per row of h [rows][channels] float32 (contiguous): if delta, h +=
+ *   scale[c] * delta[row, c] (the layer-scaled residual add, code2wav.py:338-356's addcmul);
+ *   then normed[row, c] = weight[c] * h[row, c] / sqrt(mean_c(h^2) + eps) as bf16 (rmsnorm).
+ *   channels a multiple of 256, at most 4096.
+ * omni_rope_kv_write: qkv [batch * frames][qkv_stride] bf16 holds q (heads * head_dim), k, v
+ *   (kv_heads * head_dim each); q and k get the neox rotary embedding in place at position
+ *   start(b) + t, angle = position * inv_freq[i] in float32 (start(b) = 0 if cold, else
+ *   positions[slot_index[b]]); with key_ring / value_ring ([slots * ring_frames][kv_heads *
+ *   head_dim] bf16) the rotated k and the v of each frame also go to ring row
+ *   slot * ring_frames + position % ring_frames (apply_rope_inplace_with_kvcache,
+ *   code2wav.py:216-226).
+ * omni_window_attention: out[b * frames + t, h * 64 + d] (bf16) = softmax over the keys at
+ *   positions p with 0 <= P - p < window (P the query's position) of scale * q . k, times v;
+ *   keys / values from the rings (which must hold the window before the new frames, ring_frames >=
+ *   window - 1 + frames) or, for a first decode (cold, rings NULL), from qkv itself
+ *   (code2wav.py:227-256,295-316). head_dim 64, window <= 104 (the window's keys sit in LDS).
+ * omni_silu_mul: out[row, i] = silu(gate_up[row, i]) * gate_up[row, inter + i], bf16.
+ * omni_dwconv_layernorm: ConvNeXt's depthwise causal conv (7 taps, weight [7][channels]
+ *   float32, tap 6 on the current sample) over x [batch][length][channels] float32 with slot
+ *   history (pool [slots][2][6][channels] float32, copy slot_parity & 1 read, the other written),
+ *   plus bias, then LayerNorm(eps) with ln_weight / ln_bias, written as bf16
+ *   (incremental_codec.py:160-175, modeling_qwen3_omni_moe.py:3231-3264).
+ * omni_bias_gelu: y = GELU(y + bias[col]) in place (erf form), bf16.
+ * omni_bias_scale_residual: r[row, c] += gamma[c] * (y[row, c] + bias[c]) (r float32
+ *   contiguous, y bf16); if out, also out[row, c] = bf16(r[row, c]).
+ * omni_advance_positions: positions[slot_index[r]] = (cold ? 0 : positions[slot_index[r]]) +
+ *   new_frames, the end of a slot decode (code2wav.py:459).
+ */
+int omni_rms_norm_residual(float* h, int64_t rows, int64_t channels, const void* delta,
+                           int64_t delta_stride, const float* scale, const float* weight,
+                           float eps, void* normed, int64_t normed_stride, omni_stream_t stream);
+int omni_rope_kv_write(void* qkv, int64_t batch, int64_t frames, int64_t qkv_stride,
+                       int64_t heads, int64_t kv_heads, int64_t head_dim, const float* inv_freq,
+                       const int64_t* slot_index, const int64_t* positions, int cold,
+                       int64_t num_slots, void* key_ring, void* value_ring, int64_t ring_frames,
+                       omni_stream_t stream);
+int omni_window_attention(const void* qkv, int64_t batch, int64_t frames, int64_t qkv_stride,
+                          int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t window,
+                          float scale, const void* key_ring, const void* value_ring,
+                          int64_t ring_frames, const int64_t* slot_index,
+                          const int64_t* positions, int cold, int64_t num_slots, void* out,
+                          int64_t out_stride, omni_stream_t stream);
+int omni_silu_mul(const void* gate_up, int64_t rows, int64_t inter, int64_t in_stride, void* out,
+                  int64_t out_stride, omni_stream_t stream);
+int omni_dwconv_layernorm(const float* x, int64_t batch, int64_t length, int64_t channels,
+                          int64_t x_stride_b, const float* weight, const float* bias,
+                          const float* ln_weight, const float* ln_bias, float eps,
+                          float* hist_pool, int64_t hist_slot_stride, const int64_t* slot_index,
+                          const int64_t* slot_parity, int64_t num_slots, int cold, void* out,
+                          int64_t out_stride_b, omni_stream_t stream);
+int omni_bias_gelu(void* y, int64_t rows, int64_t cols, int64_t stride, const float* bias,
+                   omni_stream_t stream);
+int omni_bias_scale_residual(float* r, int64_t rows, int64_t channels, const void* y,
+                             int64_t y_stride, const float* bias, const float* gamma, void* out,
+                             int64_t out_stride, omni_stream_t stream);
+int omni_advance_positions(int64_t* positions, int64_t num_slots, const int64_t* slot_index,
+                           int64_t rows, int64_t new_frames, int cold, omni_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

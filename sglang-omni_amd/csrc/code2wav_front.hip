@@ -1,0 +1,727 @@
+// The Qwen3-Omni code2wav front on gfx950: every op of the pre-transformer and the ConvNeXt
+// upsamplers that is not a plain GEMM (the GEMMs are hipBLASLt calls between these launches).
+//
+//   rms_norm_residual_kernel   h += scale * delta (layer scale + residual, float32 h), then
+//                              normed = RMSNorm(h) * weight as the next GEMM's bf16 operand
+//                              (code2wav.py:338-356's addcmul + rmsnorm; the layer's input norm)
+//   rope_kv_kernel             neox rotary on q and k in the qkv GEMM output, in place, at the
+//                              rows' absolute positions, and the new K / V into the slots' rings
+//                              (apply_rope_inplace_with_kvcache, code2wav.py:216-226)
+//   window_attention_kernel    causal sliding-window softmax attention of the new frames over
+//                              their window: the rows' rings or, for a stream's first decode, the
+//                              qkv buffer itself (code2wav.py:227-256,295-316)
+//   silu_mul_kernel            silu(gate) * up of the merged gate / up GEMM (code2wav.py:353)
+//   dwconv_layernorm_kernel    ConvNeXt's depthwise causal conv (k = 7) over the float32
+//                              residual stream with per-slot history, then LayerNorm, as the
+//                              first MLP GEMM's bf16 operand (incremental_codec.py:160-175)
+//   bias_gelu_kernel           GELU(y + b) in place (erf form, nn.GELU())
+//   bias_scale_residual_kernel r += gamma * (y + b), and the next conv's bf16 operand
+//   advance_positions_kernel   frame_positions[slot] = start + new frames (code2wav.py:459)
+//
+// One wave per row wherever a row is reduced (RMSNorm, LayerNorm): the channels sit in
+// registers, 4 per lane per 256-channel group, and the reduction is a wave shuffle.
+#include "common.h"
+
+namespace {
+
+constexpr int kWave = 64;
+
+OMNI_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+OMNI_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+OMNI_DEVICE void load_bf16x4(const u16* p, float v[4]) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  v[0] = __uint_as_float(w.x << 16);
+  v[1] = __uint_as_float(w.x & 0xffff0000u);
+  v[2] = __uint_as_float(w.y << 16);
+  v[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+
+OMNI_DEVICE void store_bf16x4(u16* p, const float v[4]) {
+  uint2 w;
+  w.x = (uint32_t)float_to_bits_bf16(v[0]) | ((uint32_t)float_to_bits_bf16(v[1]) << 16);
+  w.y = (uint32_t)float_to_bits_bf16(v[2]) | ((uint32_t)float_to_bits_bf16(v[3]) << 16);
+  *reinterpret_cast<uint2*>(p) = w;
+}
+
+OMNI_DEVICE void load_bf16x8(const u16* p, float v[8]) {
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(a[i] << 16);
+    v[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+  }
+}
+
+OMNI_DEVICE void store_bf16x8(u16* p, const float v[8]) {
+  uint4 w;
+  w.x = (uint32_t)float_to_bits_bf16(v[0]) | ((uint32_t)float_to_bits_bf16(v[1]) << 16);
+  w.y = (uint32_t)float_to_bits_bf16(v[2]) | ((uint32_t)float_to_bits_bf16(v[3]) << 16);
+  w.z = (uint32_t)float_to_bits_bf16(v[4]) | ((uint32_t)float_to_bits_bf16(v[5]) << 16);
+  w.w = (uint32_t)float_to_bits_bf16(v[6]) | ((uint32_t)float_to_bits_bf16(v[7]) << 16);
+  *reinterpret_cast<uint4*>(p) = w;
+}
+
+// A row's start position in its stream: 0 for a first decode (or no slot state), else the
+// slot's frame count. Rows whose slot is out of range read position 0 and write no state.
+OMNI_DEVICE int64_t row_start(const int64_t* slot_index, const int64_t* positions, int cold,
+                              int64_t num_slots, int64_t b, int64_t* slot_out) {
+  int64_t slot = -1;
+  if (slot_index) {
+    slot = slot_index[b];
+    if (slot < 0 || slot >= num_slots) slot = -1;
+  }
+  *slot_out = slot;
+  if (cold || !positions || slot < 0) return 0;
+  return positions[slot];
+}
+
+// ------------------------------------------------------------------------------ RMSNorm
+
+constexpr int kMaxGroups = 16;  // channels <= 16 * 256
+
+struct RmsParams {
+  float* h;
+  int64_t rows;
+  int channels;
+  int groups;  // channels / 256
+  const u16* delta;
+  int64_t delta_stride;
+  const float* scale;
+  const float* weight;
+  float eps;
+  u16* normed;
+  int64_t normed_stride;
+};
+
+__global__ __launch_bounds__(256) void rms_norm_residual_kernel(RmsParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  float* hr = p.h + row * p.channels;
+  float v[kMaxGroups][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int g = 0; g < kMaxGroups; ++g) {
+    if (g < p.groups) {
+      const int c = (g * kWave + lane) * 4;
+      const float4 x = *reinterpret_cast<const float4*>(hr + c);
+      float a[4] = {x.x, x.y, x.z, x.w};
+      if (p.delta) {
+        float d[4];
+        load_bf16x4(p.delta + row * p.delta_stride + c, d);
+        const float4 s = *reinterpret_cast<const float4*>(p.scale + c);
+        a[0] += s.x * d[0];
+        a[1] += s.y * d[1];
+        a[2] += s.z * d[2];
+        a[3] += s.w * d[3];
+        *reinterpret_cast<float4*>(hr + c) = make_float4(a[0], a[1], a[2], a[3]);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[g][k] = a[k];
+        ss += a[k] * a[k];
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)p.channels + p.eps);
+#pragma unroll
+  for (int g = 0; g < kMaxGroups; ++g) {
+    if (g < p.groups) {
+      const int c = (g * kWave + lane) * 4;
+      const float4 w = *reinterpret_cast<const float4*>(p.weight + c);
+      const float o[4] = {w.x * (v[g][0] * inv), w.y * (v[g][1] * inv), w.z * (v[g][2] * inv),
+                          w.w * (v[g][3] * inv)};
+      store_bf16x4(p.normed + row * p.normed_stride + c, o);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ rotary + rings
+
+struct RopeParams {
+  u16* qkv;
+  int64_t frames;  // T, rows per batch row
+  int64_t qkv_stride;
+  int heads, kv_heads, head_dim;
+  const float* inv_freq;  // [head_dim / 2]
+  const int64_t* slot_index;
+  const int64_t* positions;
+  int cold;
+  int64_t num_slots;
+  u16* key_ring;
+  u16* value_ring;
+  int64_t ring_frames;
+};
+
+// One workgroup per token (b * T + t): the rotary pairs of its q and k heads, then its V row
+// into the ring.
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeParams p) {
+  const int64_t token = blockIdx.x;
+  const int64_t b = token / p.frames;
+  const int64_t t = token - b * p.frames;
+  int64_t slot;
+  const int64_t pos = row_start(p.slot_index, p.positions, p.cold, p.num_slots, b, &slot) + t;
+  u16* row = p.qkv + token * p.qkv_stride;
+  const int half = p.head_dim / 2;
+  const int kv_width = p.kv_heads * p.head_dim;
+  const bool ring = p.key_ring != nullptr && slot >= 0;
+  const int64_t ring_row = ring ? slot * p.ring_frames + pos % p.ring_frames : 0;
+  const int pairs = (p.heads + p.kv_heads) * half;
+  const float fpos = (float)pos;
+  for (int item = threadIdx.x; item < pairs; item += blockDim.x) {
+    const int head = item / half;
+    const int i = item - head * half;
+    const int col = head * p.head_dim + i;  // q heads, then k heads, are contiguous
+    float s, c;
+    sincosf(fpos * p.inv_freq[i], &s, &c);
+    const float x1 = bits_to_float_bf16(row[col]);
+    const float x2 = bits_to_float_bf16(row[col + half]);
+    const u16 y1 = float_to_bits_bf16(x1 * c - x2 * s);
+    const u16 y2 = float_to_bits_bf16(x2 * c + x1 * s);
+    row[col] = y1;
+    row[col + half] = y2;
+    if (ring && head >= p.heads) {
+      u16* k = p.key_ring + ring_row * kv_width + (col - p.heads * p.head_dim);
+      k[0] = y1;
+      k[half] = y2;
+    }
+  }
+  if (ring) {
+    const u16* v = row + (p.heads + p.kv_heads) * p.head_dim;
+    u16* dst = p.value_ring + ring_row * kv_width;
+    for (int e = threadIdx.x; e < kv_width; e += blockDim.x) dst[e] = v[e];
+  }
+}
+
+// ------------------------------------------------------------------------------ attention
+
+constexpr int kQueries = 16;  // queries per workgroup, 4 per wave
+constexpr int kHeadDim = 64;  // one dimension per lane in the P . V product
+constexpr int kKPitch = kHeadDim + 1;  // float pitch of a K row in LDS (conflict-free reads)
+
+struct AttnParams {
+  const u16* qkv;
+  int64_t frames;
+  int64_t qkv_stride;
+  int heads, kv_heads;
+  int window;
+  float scale;
+  const u16* key_ring;  // null: keys and values come from qkv (a first decode)
+  const u16* value_ring;
+  int64_t ring_frames;
+  const int64_t* slot_index;
+  const int64_t* positions;
+  int cold;
+  int64_t num_slots;
+  u16* out;
+  int64_t out_stride;
+};
+
+size_t attention_lds_bytes(int window) {
+  const int keys = window - 1 + kQueries;
+  return sizeof(float) * ((size_t)keys * kKPitch + (size_t)keys * kHeadDim + kQueries * kHeadDim);
+}
+
+__global__ __launch_bounds__(256) void window_attention_kernel(AttnParams p) {
+  extern __shared__ float lds[];
+  const int64_t b = blockIdx.z;
+  const int head = blockIdx.y;
+  const int64_t t0 = (int64_t)blockIdx.x * kQueries;
+  const int kvh = head / (p.heads / p.kv_heads);
+  const int max_keys = p.window - 1 + kQueries;
+  float* ks = lds;                                  // [max_keys][kKPitch]
+  float* vs = ks + (size_t)max_keys * kKPitch;       // [max_keys][kHeadDim]
+  float* qs = vs + (size_t)max_keys * kHeadDim;      // [kQueries][kHeadDim]
+  int64_t slot;
+  const int64_t start = row_start(p.slot_index, p.positions, p.cold, p.num_slots, b, &slot);
+  const bool ring = p.key_ring != nullptr;
+  const int64_t p0 = start + t0;
+  const int64_t last_t = min(t0 + kQueries, p.frames) - 1;
+  const int64_t kp0 = max(p0 - (p.window - 1), (int64_t)0);
+  const int64_t kp1 = start + last_t;
+  const int nk = (int)(kp1 - kp0 + 1);  // <= max_keys
+  const int kv_width = p.kv_heads * kHeadDim;
+  // stage K and V of positions kp0..kp1 and the block's queries, 8 bf16 per thread and step
+  const int chunks = nk * (kHeadDim / 8);
+  for (int e = threadIdx.x; e < chunks; e += blockDim.x) {
+    const int r = e / (kHeadDim / 8);
+    const int c8 = (e - r * (kHeadDim / 8)) * 8;
+    const int64_t kpos = kp0 + r;
+    const u16* ksrc;
+    const u16* vsrc;
+    if (ring) {
+      const int64_t rr = (slot < 0 ? 0 : slot) * p.ring_frames + kpos % p.ring_frames;
+      ksrc = p.key_ring + rr * kv_width + kvh * kHeadDim + c8;
+      vsrc = p.value_ring + rr * kv_width + kvh * kHeadDim + c8;
+    } else {
+      const u16* tok = p.qkv + (b * p.frames + (kpos - start)) * p.qkv_stride;
+      ksrc = tok + (p.heads + kvh) * kHeadDim + c8;
+      vsrc = tok + (p.heads + p.kv_heads + kvh) * kHeadDim + c8;
+    }
+    float kv[8];
+    load_bf16x8(ksrc, kv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ks[r * kKPitch + c8 + i] = kv[i];
+    load_bf16x8(vsrc, kv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vs[r * kHeadDim + c8 + i] = kv[i];
+  }
+  const int nq = (int)(last_t - t0 + 1);
+  for (int e = threadIdx.x; e < nq * (kHeadDim / 8); e += blockDim.x) {
+    const int q = e / (kHeadDim / 8);
+    const int c8 = (e - q * (kHeadDim / 8)) * 8;
+    float qv[8];
+    load_bf16x8(p.qkv + (b * p.frames + t0 + q) * p.qkv_stride + head * kHeadDim + c8, qv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qs[q * kHeadDim + c8 + i] = qv[i];
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int qi = 0; qi < kQueries / 4; ++qi) {
+    const int q = wave * (kQueries / 4) + qi;
+    if (q >= nq) break;
+    const int64_t pos = p0 + q;
+    const int lo = (int)(max(pos - (p.window - 1), (int64_t)0) - kp0);
+    const int n = (int)(pos - kp0) - lo + 1;  // keys of this query, <= window <= 128
+    const float* qrow = qs + q * kHeadDim;
+    float s0 = -INFINITY, s1 = -INFINITY;
+    const int r0 = lo + lane, r1 = lo + lane + kWave;
+    if (lane < n) {
+      float acc = 0.f;
+      const float* krow = ks + r0 * kKPitch;
+#pragma unroll 16
+      for (int d = 0; d < kHeadDim; ++d) acc += qrow[d] * krow[d];
+      s0 = acc * p.scale;
+    }
+    if (lane + kWave < n) {
+      float acc = 0.f;
+      const float* krow = ks + r1 * kKPitch;
+#pragma unroll 16
+      for (int d = 0; d < kHeadDim; ++d) acc += qrow[d] * krow[d];
+      s1 = acc * p.scale;
+    }
+    const float m = wave_max(fmaxf(s0, s1));
+    const float e0 = lane < n ? __expf(s0 - m) : 0.f;
+    const float e1 = lane + kWave < n ? __expf(s1 - m) : 0.f;
+    const float sum = wave_sum(e0 + e1);
+    float o = 0.f;
+    for (int j = 0; j < n; ++j) {
+      const float pj = __shfl(j < kWave ? e0 : e1, j & (kWave - 1), kWave);
+      o += pj * vs[(lo + j) * kHeadDim + lane];
+    }
+    p.out[(b * p.frames + t0 + q) * p.out_stride + head * kHeadDim + lane] =
+        float_to_bits_bf16(o / sum);
+  }
+}
+
+// ------------------------------------------------------------------------------ SwiGLU
+
+struct SiluMulParams {
+  const u16* gate_up;
+  int64_t rows;
+  int64_t inter;
+  int64_t in_stride;
+  u16* out;
+  int64_t out_stride;
+};
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(SiluMulParams p) {
+  const int64_t per_row = p.inter / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= p.rows * per_row) return;
+  const int64_t row = idx / per_row;
+  const int64_t c = (idx - row * per_row) * 8;
+  float g[8], u[8], o[8];
+  load_bf16x8(p.gate_up + row * p.in_stride + c, g);
+  load_bf16x8(p.gate_up + row * p.in_stride + p.inter + c, u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = g[i] / (1.f + __expf(-g[i])) * u[i];
+  store_bf16x8(p.out + row * p.out_stride + c, o);
+}
+
+// ------------------------------------------------------------------------------ ConvNeXt
+
+constexpr int kDwTaps = 7;
+constexpr int kDwHistory = kDwTaps - 1;
+
+struct DwParams {
+  const float* x;  // [B][L][C] float32, rows x_stride_b apart
+  int64_t x_stride_b;
+  int64_t length;
+  int channels;
+  int groups;
+  const float* weight;  // [7][C]
+  const float* bias;
+  const float* ln_weight;
+  const float* ln_bias;
+  float eps;
+  float* hist;  // [slots][2][6][C] float32 (nullable)
+  int64_t hist_slot_stride;
+  const int64_t* slot_index;
+  const int64_t* slot_parity;
+  int64_t num_slots;
+  int cold;
+  u16* out;  // [B][L][C] bf16, rows out_stride_b apart
+  int64_t out_stride_b;
+  int pos_blocks;  // workgroups of positions per batch row (one more writes the new history)
+};
+
+__global__ __launch_bounds__(256) void dwconv_layernorm_kernel(DwParams p) {
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int C = p.channels;
+  int64_t slot = -1;
+  if (p.hist && p.slot_index) {
+    slot = p.slot_index[b];
+    if (slot < 0 || slot >= p.num_slots) slot = -1;
+  }
+  const int parity = slot >= 0 ? (int)(p.slot_parity[slot] & 1) : 0;
+  const float* hread =
+      (slot >= 0 && !p.cold) ? p.hist + slot * p.hist_slot_stride + parity * kDwHistory * C
+                             : nullptr;
+  const float* xb = p.x + b * p.x_stride_b;
+  if ((int)blockIdx.x == p.pos_blocks) {
+    // the new history: the last 6 samples of (old history ++ this call's samples)
+    if (slot < 0) return;
+    float* hw = p.hist + slot * p.hist_slot_stride + (1 - parity) * kDwHistory * C;
+    for (int e = threadIdx.x; e < kDwHistory * C; e += blockDim.x) {
+      const int s = e / C;
+      const int c = e - s * C;
+      const int64_t q = p.length + s;  // index into (history ++ samples)
+      float v;
+      if (q >= kDwHistory) v = xb[(q - kDwHistory) * C + c];
+      else v = hread ? hread[q * C + c] : 0.f;
+      hw[s * C + c] = v;
+    }
+    return;
+  }
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= p.length) return;
+  float v[kMaxGroups][4];
+  float sum = 0.f;
+#pragma unroll
+  for (int g = 0; g < kMaxGroups; ++g) {
+    if (g < p.groups) {
+      const int c = (g * kWave + lane) * 4;
+      const float4 bias = *reinterpret_cast<const float4*>(p.bias + c);
+      float a[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+      for (int j = 0; j < kDwTaps; ++j) {
+        const int64_t pos = t - kDwHistory + j;
+        float4 x;
+        if (pos >= 0) x = *reinterpret_cast<const float4*>(xb + pos * C + c);
+        else if (hread) x = *reinterpret_cast<const float4*>(hread + (kDwHistory + pos) * C + c);
+        else x = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 w = *reinterpret_cast<const float4*>(p.weight + j * C + c);
+        a[0] += w.x * x.x;
+        a[1] += w.y * x.y;
+        a[2] += w.z * x.z;
+        a[3] += w.w * x.w;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[g][k] = a[k];
+        sum += a[k];
+      }
+    }
+  }
+  const float mean = wave_sum(sum) / (float)C;
+  float var = 0.f;
+#pragma unroll
+  for (int g = 0; g < kMaxGroups; ++g)
+    if (g < p.groups)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float d = v[g][k] - mean;
+        var += d * d;
+      }
+  const float inv = rsqrtf(wave_sum(var) / (float)C + p.eps);
+  u16* ob = p.out + b * p.out_stride_b + t * C;
+#pragma unroll
+  for (int g = 0; g < kMaxGroups; ++g) {
+    if (g < p.groups) {
+      const int c = (g * kWave + lane) * 4;
+      const float4 w = *reinterpret_cast<const float4*>(p.ln_weight + c);
+      const float4 bb = *reinterpret_cast<const float4*>(p.ln_bias + c);
+      const float o[4] = {(v[g][0] - mean) * inv * w.x + bb.x, (v[g][1] - mean) * inv * w.y + bb.y,
+                          (v[g][2] - mean) * inv * w.z + bb.z, (v[g][3] - mean) * inv * w.w + bb.w};
+      store_bf16x4(ob + c, o);
+    }
+  }
+}
+
+struct BiasGeluParams {
+  u16* y;
+  int64_t rows, cols, stride;
+  const float* bias;
+};
+
+__global__ __launch_bounds__(256) void bias_gelu_kernel(BiasGeluParams p) {
+  const int64_t per_row = p.cols / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= p.rows * per_row) return;
+  const int64_t row = idx / per_row;
+  const int64_t c = (idx - row * per_row) * 8;
+  u16* ptr = p.y + row * p.stride + c;
+  float v[8];
+  load_bf16x8(ptr, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float x = v[i] + p.bias[c + i];
+    v[i] = 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+  }
+  store_bf16x8(ptr, v);
+}
+
+struct ScaleResidualParams {
+  float* r;  // [rows][channels] float32, contiguous
+  int64_t rows;
+  int64_t channels;
+  const u16* y;
+  int64_t y_stride;
+  const float* bias;
+  const float* gamma;
+  u16* out;  // bf16 copy of the new r (nullable)
+  int64_t out_stride;
+};
+
+__global__ __launch_bounds__(256) void bias_scale_residual_kernel(ScaleResidualParams p) {
+  const int64_t per_row = p.channels / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= p.rows * per_row) return;
+  const int64_t row = idx / per_row;
+  const int64_t c = (idx - row * per_row) * 4;
+  float* rp = p.r + row * p.channels + c;
+  float4 r = *reinterpret_cast<float4*>(rp);
+  float y[4];
+  load_bf16x4(p.y + row * p.y_stride + c, y);
+  const float4 b = *reinterpret_cast<const float4*>(p.bias + c);
+  const float4 g = *reinterpret_cast<const float4*>(p.gamma + c);
+  r.x += g.x * (y[0] + b.x);
+  r.y += g.y * (y[1] + b.y);
+  r.z += g.z * (y[2] + b.z);
+  r.w += g.w * (y[3] + b.w);
+  *reinterpret_cast<float4*>(rp) = r;
+  if (p.out) {
+    const float o[4] = {r.x, r.y, r.z, r.w};
+    store_bf16x4(p.out + row * p.out_stride + c, o);
+  }
+}
+
+__global__ void advance_positions_kernel(int64_t* positions, int64_t num_slots,
+                                         const int64_t* slot_index, int64_t rows,
+                                         int64_t new_frames, int cold) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t slot = slot_index[r];
+  if (slot < 0 || slot >= num_slots) return;
+  positions[slot] = (cold ? 0 : positions[slot]) + new_frames;
+}
+
+bool aligned(const void* ptr, int bytes) {
+  return (reinterpret_cast<uintptr_t>(ptr) & (uintptr_t)(bytes - 1)) == 0;
+}
+
+unsigned blocks_for(int64_t items, int threads) { return (unsigned)((items + threads - 1) / threads); }
+
+}  // namespace
+
+extern "C" int omni_rms_norm_residual(float* h, int64_t rows, int64_t channels, const void* delta,
+                                      int64_t delta_stride, const float* scale,
+                                      const float* weight, float eps, void* normed,
+                                      int64_t normed_stride, omni_stream_t stream) {
+  if (!h || !weight || !normed || rows < 0) return OMNI_ERR_INVALID_ARG;
+  if (channels < 256 || channels % 256 || channels > 256 * kMaxGroups) return OMNI_ERR_UNSUPPORTED;
+  if (delta && (!scale || delta_stride < channels || delta_stride % 4)) return OMNI_ERR_INVALID_ARG;
+  if (normed_stride < channels || normed_stride % 4 || !(eps >= 0.f)) return OMNI_ERR_INVALID_ARG;
+  if (!aligned(h, 16) || !aligned(normed, 8) || (delta && !aligned(delta, 8)))
+    return OMNI_ERR_INVALID_ARG;
+  if (rows == 0) return OMNI_OK;
+  RmsParams p{h, rows, (int)channels, (int)(channels / 256), static_cast<const u16*>(delta),
+              delta_stride, scale, weight, eps, static_cast<u16*>(normed), normed_stride};
+  hipLaunchKernelGGL(rms_norm_residual_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_rope_kv_write(void* qkv, int64_t batch, int64_t frames, int64_t qkv_stride,
+                                  int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                  const float* inv_freq, const int64_t* slot_index,
+                                  const int64_t* positions, int cold, int64_t num_slots,
+                                  void* key_ring, void* value_ring, int64_t ring_frames,
+                                  omni_stream_t stream) {
+  if (!qkv || !inv_freq || batch < 0 || frames < 0) return OMNI_ERR_INVALID_ARG;
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 2 || head_dim % 2)
+    return OMNI_ERR_INVALID_ARG;
+  if (qkv_stride < (heads + 2 * kv_heads) * head_dim) return OMNI_ERR_INVALID_ARG;
+  if ((key_ring != nullptr) != (value_ring != nullptr)) return OMNI_ERR_INVALID_ARG;
+  if (key_ring && (!slot_index || ring_frames < 1)) return OMNI_ERR_INVALID_ARG;
+  if (!cold && (!slot_index || !positions)) return OMNI_ERR_INVALID_ARG;
+  if (batch * frames == 0) return OMNI_OK;
+  if (batch * frames > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
+  RopeParams p{static_cast<u16*>(qkv), frames, qkv_stride, (int)heads, (int)kv_heads,
+               (int)head_dim, inv_freq, slot_index, positions, cold, num_slots,
+               static_cast<u16*>(key_ring), static_cast<u16*>(value_ring), ring_frames};
+  hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)(batch * frames)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_window_attention(const void* qkv, int64_t batch, int64_t frames,
+                                     int64_t qkv_stride, int64_t heads, int64_t kv_heads,
+                                     int64_t head_dim, int64_t window, float scale,
+                                     const void* key_ring, const void* value_ring,
+                                     int64_t ring_frames, const int64_t* slot_index,
+                                     const int64_t* positions, int cold, int64_t num_slots,
+                                     void* out, int64_t out_stride, omni_stream_t stream) {
+  if (!qkv || !out || batch < 0 || frames < 0) return OMNI_ERR_INVALID_ARG;
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads) return OMNI_ERR_INVALID_ARG;
+  if (head_dim != kHeadDim) return OMNI_ERR_UNSUPPORTED;
+  if (window < 1 || window > 2 * kWave) return OMNI_ERR_UNSUPPORTED;
+  if (qkv_stride < (heads + 2 * kv_heads) * head_dim || qkv_stride % 8 ||
+      out_stride < heads * head_dim)
+    return OMNI_ERR_INVALID_ARG;
+  if (!aligned(qkv, 16)) return OMNI_ERR_INVALID_ARG;
+  if ((key_ring != nullptr) != (value_ring != nullptr)) return OMNI_ERR_INVALID_ARG;
+  if (key_ring) {
+    // the ring holds the window before the new frames and the frames themselves
+    if (!slot_index || ring_frames < window - 1 + frames) return OMNI_ERR_INVALID_ARG;
+    if (!aligned(key_ring, 16) || !aligned(value_ring, 16)) return OMNI_ERR_INVALID_ARG;
+    if (!cold && !positions) return OMNI_ERR_INVALID_ARG;
+  } else if (!cold) {
+    return OMNI_ERR_INVALID_ARG;  // without rings only a stream's first frames have their keys
+  }
+  if (batch * frames == 0) return OMNI_OK;
+  if (batch > 65535 || heads > 65535) return OMNI_ERR_UNSUPPORTED;
+  AttnParams p{static_cast<const u16*>(qkv), frames, qkv_stride, (int)heads, (int)kv_heads,
+               (int)window, scale, static_cast<const u16*>(key_ring),
+               static_cast<const u16*>(value_ring), ring_frames, slot_index, positions, cold,
+               num_slots, static_cast<u16*>(out), out_stride};
+  const size_t lds = attention_lds_bytes((int)window);
+  if (lds > 64 * 1024) return OMNI_ERR_UNSUPPORTED;
+  dim3 grid(blocks_for(frames, kQueries), (unsigned)heads, (unsigned)batch);
+  hipLaunchKernelGGL(window_attention_kernel, grid, dim3(256), lds,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_silu_mul(const void* gate_up, int64_t rows, int64_t inter, int64_t in_stride,
+                             void* out, int64_t out_stride, omni_stream_t stream) {
+  if (!gate_up || !out || rows < 0 || inter < 8 || inter % 8) return OMNI_ERR_INVALID_ARG;
+  if (in_stride < 2 * inter || in_stride % 8 || out_stride < inter || out_stride % 8)
+    return OMNI_ERR_INVALID_ARG;
+  if (!aligned(gate_up, 16) || !aligned(out, 16)) return OMNI_ERR_INVALID_ARG;
+  if (rows == 0) return OMNI_OK;
+  SiluMulParams p{static_cast<const u16*>(gate_up), rows, inter, in_stride,
+                  static_cast<u16*>(out), out_stride};
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks_for(rows * (inter / 8), 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_dwconv_layernorm(const float* x, int64_t batch, int64_t length,
+                                     int64_t channels, int64_t x_stride_b, const float* weight,
+                                     const float* bias, const float* ln_weight,
+                                     const float* ln_bias, float eps, float* hist_pool,
+                                     int64_t hist_slot_stride, const int64_t* slot_index,
+                                     const int64_t* slot_parity, int64_t num_slots, int cold,
+                                     void* out, int64_t out_stride_b, omni_stream_t stream) {
+  if (!x || !weight || !bias || !ln_weight || !ln_bias || !out) return OMNI_ERR_INVALID_ARG;
+  if (batch < 0 || length < 0) return OMNI_ERR_INVALID_ARG;
+  if (channels < 256 || channels % 256 || channels > 256 * kMaxGroups) return OMNI_ERR_UNSUPPORTED;
+  if (x_stride_b < length * channels || x_stride_b % 4 || out_stride_b < length * channels ||
+      out_stride_b % 4)
+    return OMNI_ERR_INVALID_ARG;
+  if (hist_pool && (!slot_index || !slot_parity || hist_slot_stride < 2 * kDwHistory * channels))
+    return OMNI_ERR_INVALID_ARG;
+  if (!aligned(x, 16) || !aligned(out, 8) || (hist_pool && !aligned(hist_pool, 16)))
+    return OMNI_ERR_INVALID_ARG;
+  if (batch == 0 || length == 0) return OMNI_OK;
+  if (batch > 65535) return OMNI_ERR_UNSUPPORTED;
+  DwParams p{};
+  p.x = x;
+  p.x_stride_b = x_stride_b;
+  p.length = length;
+  p.channels = (int)channels;
+  p.groups = (int)(channels / 256);
+  p.weight = weight;
+  p.bias = bias;
+  p.ln_weight = ln_weight;
+  p.ln_bias = ln_bias;
+  p.eps = eps;
+  p.hist = hist_pool;
+  p.hist_slot_stride = hist_slot_stride;
+  p.slot_index = slot_index;
+  p.slot_parity = slot_parity;
+  p.num_slots = num_slots;
+  p.cold = cold;
+  p.out = static_cast<u16*>(out);
+  p.out_stride_b = out_stride_b;
+  p.pos_blocks = (int)blocks_for(length, 4);
+  dim3 grid((unsigned)(p.pos_blocks + 1), (unsigned)batch);
+  hipLaunchKernelGGL(dwconv_layernorm_kernel, grid, dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_bias_gelu(void* y, int64_t rows, int64_t cols, int64_t stride,
+                              const float* bias, omni_stream_t stream) {
+  if (!y || !bias || rows < 0 || cols < 8 || cols % 8 || stride < cols || stride % 8)
+    return OMNI_ERR_INVALID_ARG;
+  if (!aligned(y, 16)) return OMNI_ERR_INVALID_ARG;
+  if (rows == 0) return OMNI_OK;
+  BiasGeluParams p{static_cast<u16*>(y), rows, cols, stride, bias};
+  hipLaunchKernelGGL(bias_gelu_kernel, dim3(blocks_for(rows * (cols / 8), 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_bias_scale_residual(float* r, int64_t rows, int64_t channels, const void* y,
+                                        int64_t y_stride, const float* bias, const float* gamma,
+                                        void* out, int64_t out_stride, omni_stream_t stream) {
+  if (!r || !y || !bias || !gamma || rows < 0 || channels < 4 || channels % 4)
+    return OMNI_ERR_INVALID_ARG;
+  if (y_stride < channels || y_stride % 4 || (out && (out_stride < channels || out_stride % 4)))
+    return OMNI_ERR_INVALID_ARG;
+  if (!aligned(r, 16) || !aligned(y, 8) || !aligned(bias, 16) || !aligned(gamma, 16) ||
+      (out && !aligned(out, 8)))
+    return OMNI_ERR_INVALID_ARG;
+  if (rows == 0) return OMNI_OK;
+  ScaleResidualParams p{r, rows, channels, static_cast<const u16*>(y), y_stride, bias, gamma,
+                        static_cast<u16*>(out), out_stride};
+  hipLaunchKernelGGL(bias_scale_residual_kernel, dim3(blocks_for(rows * (channels / 4), 256)),
+                     dim3(256), 0, reinterpret_cast<hipStream_t>(stream), p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_advance_positions(int64_t* positions, int64_t num_slots,
+                                      const int64_t* slot_index, int64_t rows,
+                                      int64_t new_frames, int cold, omni_stream_t stream) {
+  if (!positions || !slot_index || rows < 0 || new_frames < 0) return OMNI_ERR_INVALID_ARG;
+  if (rows == 0) return OMNI_OK;
+  hipLaunchKernelGGL(advance_positions_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), positions, num_slots, slot_index,
+                     rows, new_frames, cold);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}

@@ -190,6 +190,18 @@ SIGNATURES: dict[str, list] = {
     "omni_istft_tail": [_PTR, _I64, _I64, _I64, _I64, _PTR, _PTR, _I64, _I64, _I64,
                         ctypes.c_float, ctypes.c_float, _PTR, _I64, _PTR],
     "omni_waveform_egress": [_PTR, _I64, _I64, _I64, _PTR, _INT, _PTR, _I64, _PTR],
+    "omni_rms_norm_residual": [_PTR, _I64, _I64, _PTR, _I64, _PTR, _PTR, ctypes.c_float, _PTR,
+                               _I64, _PTR],
+    "omni_rope_kv_write": [_PTR, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _PTR, _PTR, _INT, _I64,
+                           _PTR, _PTR, _I64, _PTR],
+    "omni_window_attention": [_PTR, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                              _PTR, _PTR, _I64, _PTR, _PTR, _INT, _I64, _PTR, _I64, _PTR],
+    "omni_silu_mul": [_PTR, _I64, _I64, _I64, _PTR, _I64, _PTR],
+    "omni_dwconv_layernorm": [_PTR, _I64, _I64, _I64, _I64, _PTR, _PTR, _PTR, _PTR, ctypes.c_float,
+                              _PTR, _I64, _PTR, _PTR, _I64, _INT, _PTR, _I64, _PTR],
+    "omni_bias_gelu": [_PTR, _I64, _I64, _I64, _PTR, _PTR],
+    "omni_bias_scale_residual": [_PTR, _I64, _I64, _PTR, _I64, _PTR, _PTR, _PTR, _I64, _PTR],
+    "omni_advance_positions": [_PTR, _I64, _PTR, _I64, _I64, _INT, _PTR],
 }
 _RESTYPES = {"omni_codec_error_string": ctypes.c_char_p}
 

@@ -75,11 +75,66 @@ class HifiGanConfig:
         return int(math.prod(self.rates))
 
 
+@dataclass(frozen=True)
+class Qwen3Code2WavConfig:
+    """Qwen3-Omni code2wav (Qwen3OmniMoeCode2WavConfig's fields and defaults,
+    transformers configuration_qwen3_omni_moe.py): code embedding mean -> sliding-window
+    pre-transformer -> ConvNeXt upsamplers (x2, x2) -> causal decoder blocks of SnakeBeta ->
+    transposed conv (k = 2s, trimmed on both sides) -> residual units -> SnakeBeta -> conv to one
+    channel -> clamp."""
+
+    codebook_size: int = 2048
+    num_quantizers: int = 16
+    hidden_size: int = 1024
+    num_hidden_layers: int = 8
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 16
+    intermediate_size: int = 3072
+    sliding_window: int = 72
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    layer_scale_initial_scale: float = 0.01
+    decoder_dim: int = 1536
+    upsample_rates: tuple[int, ...] = (8, 5, 4, 3)
+    upsampling_ratios: tuple[int, ...] = (2, 2)
+    sample_rate: int = 24000
+    # the decoder's conv stack, in the vocabulary of DacDecoderConfig
+    kernel_size: int = 7
+    dilations: tuple[int, ...] = (1, 3, 9)
+    transconv_trim: str = "both"
+    final_activation: str = "clamp"
+    # random-init gains (no checkpoint here): kaiming fan_in gain for the decoder convs, and
+    # for the input conv, whose operand (the ConvNeXt output, RMS ~1) is ~12x the RVQ sum the
+    # DAC decoder's input conv sees
+    conv_gain: float = 0.85
+    input_conv_gain: float = 0.08
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    @property
+    def hop_length(self) -> int:
+        return int(math.prod(self.upsample_rates) * math.prod(self.upsampling_ratios))
+
+    @property
+    def channels(self) -> int:
+        return self.decoder_dim
+
+    @property
+    def rates(self) -> tuple[int, ...]:
+        return self.upsample_rates
+
+    def stage_channels(self) -> list[int]:
+        return [self.decoder_dim // 2**i for i in range(len(self.upsample_rates) + 1)]
+
+
 # The workloads' architectures.
 SINGLE_BLOCK = dict(n_codebooks=8, codebook_size=1024, latent_dim=256)  # RVQ + one conv block
 CODEC_24K = DacDecoderConfig()  # 16 x 2048 x 512 tables, 1536 ch, x1920 to 24 kHz
 CODEC_24K_LONG = DacDecoderConfig(n_codebooks=32, codebook_size=1024)  # fp8-weight long form
 HIFIGAN_24K = HifiGanConfig()
+QWEN3_CODE2WAV = Qwen3Code2WavConfig()
 
 
 def _kaiming(shape: tuple[int, ...], fan_in: int, gain: float, gen: torch.Generator) -> torch.Tensor:
@@ -142,6 +197,111 @@ def make_dac_weights(config: DacDecoderConfig, seed: int = 0) -> dict[str, Any]:
         "conv": _conv(1, chans[-1], config.kernel_size, g, gen),
     }
     return weights
+
+
+def make_qwen3_code2wav_weights(config: Qwen3Code2WavConfig, seed: int = 0, *,
+                                branch_scale: float | None = None,
+                                activation_spread: float = 0.0) -> dict[str, torch.Tensor]:
+    """Seeded float32 weights under ``Qwen3OmniMoeCode2Wav.state_dict()`` names (a checkpoint's
+    code2wav weights load the same way). Linear and conv weights kaiming-normal (fan_in), biases
+    zero, norms one. ``branch_scale`` replaces the layer scales (default 0.01) and ConvNeXt
+    gammas (default 1e-6) so the transformer and ConvNeXt branches matter to the output;
+    ``activation_spread`` draws the SnakeBeta log-parameters from N(0, spread) instead of 0."""
+    gen = torch.Generator().manual_seed(seed)
+    c, inter = config.hidden_size, config.intermediate_size
+    kv = config.num_key_value_heads * config.head_dim
+
+    def lin(out_f: int, in_f: int, gain: float = 1.0) -> torch.Tensor:
+        return _kaiming((out_f, in_f), in_f, gain, gen)
+
+    layer_scale = config.layer_scale_initial_scale if branch_scale is None else branch_scale
+    gamma = 1e-6 if branch_scale is None else branch_scale
+    w: dict[str, torch.Tensor] = {
+        "code_embedding.weight": torch.randn(config.num_quantizers * config.codebook_size, c,
+                                             generator=gen),
+    }
+    for i in range(config.num_hidden_layers):
+        p = f"pre_transformer.layers.{i}"
+        w[f"{p}.self_attn.q_proj.weight"] = lin(c, c)
+        w[f"{p}.self_attn.k_proj.weight"] = lin(kv, c)
+        w[f"{p}.self_attn.v_proj.weight"] = lin(kv, c)
+        w[f"{p}.self_attn.o_proj.weight"] = lin(c, c)
+        w[f"{p}.mlp.gate_proj.weight"] = lin(inter, c)
+        w[f"{p}.mlp.up_proj.weight"] = lin(inter, c)
+        w[f"{p}.mlp.down_proj.weight"] = lin(c, inter)
+        w[f"{p}.input_layernorm.weight"] = torch.ones(c)
+        w[f"{p}.post_attention_layernorm.weight"] = torch.ones(c)
+        w[f"{p}.self_attn_layer_scale.scale"] = torch.full((c,), layer_scale)
+        w[f"{p}.mlp_layer_scale.scale"] = torch.full((c,), layer_scale)
+    w["pre_transformer.norm.weight"] = torch.ones(c)
+    for i, factor in enumerate(config.upsampling_ratios):
+        w[f"upsample.{i}.0.conv.weight"] = _kaiming((c, c, factor), c * factor, 1.0, gen)
+        w[f"upsample.{i}.0.conv.bias"] = torch.zeros(c)
+        p = f"upsample.{i}.1"
+        w[f"{p}.dwconv.conv.weight"] = _kaiming((c, 1, 7), 7, 1.0, gen)
+        w[f"{p}.dwconv.conv.bias"] = torch.zeros(c)
+        w[f"{p}.norm.weight"] = torch.ones(c)
+        w[f"{p}.norm.bias"] = torch.zeros(c)
+        w[f"{p}.pwconv1.weight"] = lin(4 * c, c)
+        w[f"{p}.pwconv1.bias"] = torch.zeros(4 * c)
+        w[f"{p}.pwconv2.weight"] = lin(c, 4 * c)
+        w[f"{p}.pwconv2.bias"] = torch.zeros(c)
+        w[f"{p}.gamma"] = torch.full((c,), gamma)
+
+    def snake(prefix: str, ch: int) -> None:
+        for name in ("alpha", "beta"):
+            w[f"{prefix}.{name}"] = (torch.randn(ch, generator=gen) * activation_spread
+                                     if activation_spread else torch.zeros(ch))
+
+    g = config.conv_gain
+    chans = config.stage_channels()
+    k = config.kernel_size
+    w["decoder.0.conv.weight"] = _kaiming((chans[0], c, k), c * k, config.input_conv_gain, gen)
+    w["decoder.0.conv.bias"] = torch.zeros(chans[0])
+    for bi, rate in enumerate(config.upsample_rates, start=1):
+        p = f"decoder.{bi}.block"
+        c_in, c_out = chans[bi - 1], chans[bi]
+        snake(f"{p}.0", c_in)
+        w[f"{p}.1.conv.weight"] = _kaiming((c_in, c_out, 2 * rate), c_out * 2 * rate, g, gen)
+        w[f"{p}.1.conv.bias"] = torch.zeros(c_out)
+        for u in range(len(config.dilations)):
+            q = f"{p}.{u + 2}"
+            snake(f"{q}.act1", c_out)
+            w[f"{q}.conv1.conv.weight"] = _kaiming((c_out, c_out, k), c_out * k, g, gen)
+            w[f"{q}.conv1.conv.bias"] = torch.zeros(c_out)
+            snake(f"{q}.act2", c_out)
+            w[f"{q}.conv2.conv.weight"] = _kaiming((c_out, c_out, 1), c_out, g, gen)
+            w[f"{q}.conv2.conv.bias"] = torch.zeros(c_out)
+    n = len(config.upsample_rates)
+    snake(f"decoder.{n + 1}", chans[-1])
+    w[f"decoder.{n + 2}.conv.weight"] = _kaiming((1, chans[-1], k), chans[-1] * k, g, gen)
+    w[f"decoder.{n + 2}.conv.bias"] = torch.zeros(1)
+    return w
+
+
+def qwen3_code2wav_macs_per_frame(config: Qwen3Code2WavConfig) -> int:
+    """Multiply-accumulates per code frame: the pre-transformer's projections and attention
+    (at most a full window of keys per query), the ConvNeXt upsamplers and the decoder convs."""
+    c, inter, hd = config.hidden_size, config.intermediate_size, config.head_dim
+    kv = config.num_key_value_heads * hd
+    per_token = c * (c + 2 * kv) + c * c + 3 * c * inter
+    per_token += 2 * config.num_attention_heads * hd * config.sliding_window
+    macs = config.num_hidden_layers * per_token
+    positions = 1
+    for factor in config.upsampling_ratios:
+        macs += positions * c * c * factor  # transposed conv k = s
+        positions *= factor
+        macs += positions * (7 * c + 2 * 4 * c * c)
+    chans = config.stage_channels()
+    k = config.kernel_size
+    macs += positions * chans[0] * c * k
+    for i, s in enumerate(config.upsample_rates):
+        c_in, c_out = chans[i], chans[i + 1]
+        macs += positions * c_in * c_out * 2 * s
+        positions *= s
+        macs += positions * len(config.dilations) * (c_out * c_out * k + c_out * c_out)
+    macs += positions * chans[-1] * k
+    return macs
 
 
 def make_hifigan_weights(config: HifiGanConfig, seed: int = 0) -> dict[str, Any]:

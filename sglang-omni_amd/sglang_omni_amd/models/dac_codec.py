@@ -97,7 +97,15 @@ FUSED_UNIT_CHANNELS_BF16 = (96,)
 STACK_CHANNELS = (96,)
 
 
-def _snake_coefficients(alpha: torch.Tensor, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+def _snake_coefficients(alpha: torch.Tensor | dict[str, torch.Tensor],
+                        device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """The epilogues' (a, b) of v + b * sin(a * v)^2: Snake1d's alpha gives (alpha, 1 / (alpha +
+    1e-9)); a SnakeBeta's {"alpha", "beta"} (log scale, modeling_qwen3_omni_moe.py:3566-3581)
+    gives (exp(alpha), 1 / (exp(beta) + 1e-9))."""
+    if isinstance(alpha, dict):
+        a = torch.exp(alpha["alpha"].detach().float().reshape(-1))
+        inv_b = (torch.exp(alpha["beta"].detach().float().reshape(-1)) + 1e-9).reciprocal()
+        return a.to(device).contiguous(), inv_b.to(device).contiguous()
     a = alpha.detach().float().reshape(-1)
     return a.to(device).contiguous(), (a + 1e-9).reciprocal().to(device).contiguous()
 
@@ -149,13 +157,14 @@ class CodecStatePool:
 
 @dataclass
 class _Workspace:
-    z: torch.Tensor
+    z: torch.Tensor | None
     x: torch.Tensor  # the float32 residual stream (updated in place by each residual unit)
     u: list[torch.Tensor]  # the bf16 operand of the next conv, two buffers (read while written)
     h: torch.Tensor  # bf16 activation between the two convs of an unfused residual unit
     # blocks whose residual units the fused kernel has no tile for at this shape (short rows with a
     # wide halo): they run as two launches
     unfused_blocks: set[int] = field(default_factory=set)
+    front: dict[str, torch.Tensor] = field(default_factory=dict)  # a front's own buffers
 
 
 class DacCodecDecoder:
@@ -179,7 +188,17 @@ class DacCodecDecoder:
         self.frame_length = config.hop_length
         self.delay = 0
         dev = self.device
-        self.codebooks = ref["codebooks"].to(torch.bfloat16).to(dev).contiguous()
+        # "right": a transposed conv (k = 2s) emits s samples per input (modded_dac.py:583-600);
+        # "both": the whole decode and a stream's first decode also drop its first s samples
+        # (Qwen3OmniMoeCausalTransConvNet, modeling_qwen3_omni_moe.py:3216-3228)
+        self.trim_first = getattr(config, "transconv_trim", "right") == "both"
+        self.final_activation = (N.ACT_CLAMP if getattr(config, "final_activation", "tanh") == "clamp"
+                                 else N.ACT_TANH)
+        # conv-stack positions per code frame at the input conv
+        self.front_upsample = 1
+        self.codebooks = (ref["codebooks"].to(torch.bfloat16).to(dev).contiguous()
+                          if "codebooks" in ref else None)
+        self.num_codebooks = None if self.codebooks is None else self.codebooks.shape[0]
 
         def conv1d(src: dict, rsrc: dict, dilation: int = 1) -> PackedConv:
             w = src["weight"] if fp8 else rsrc["weight"]
@@ -259,14 +278,15 @@ class DacCodecDecoder:
         ws = self._workspaces.get(key)
         if ws is None:
             dev = self.device
-            length = frames
-            largest = frames * self.in_conv.conv.n_cols
+            length = frames * self.front_upsample
+            largest = length * self.in_conv.conv.n_cols
             for blk in self.blocks:
                 length *= blk.stride
                 largest = max(largest, length * blk.c_out)
             ws = _Workspace(
-                z=torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16,
-                              device=dev),
+                z=None if self.codebooks is None else
+                torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16,
+                            device=dev),
                 x=torch.empty(batch * largest, dtype=torch.float32, device=dev),
                 u=[torch.empty(batch * largest, dtype=torch.bfloat16, device=dev) for _ in range(2)],
                 h=torch.empty(batch * largest, dtype=torch.bfloat16, device=dev),
@@ -300,17 +320,15 @@ class DacCodecDecoder:
 
         timer = self.timer
         snake = N.ACT_SNAKE
-
-        k_books, _, dim = self.codebooks.shape
-        rvq_bytes = batch * frames * (k_books * dim * 2 + dim * 2 + k_books * codes.element_size())
-        with timer.launch("rvq", rvq_bytes):
-            rvq_gather_sum(codes, self.codebooks, out=ws.z, clamp=True)
-        length = frames
+        z, length = self._front(codes, ws, state)
+        # the whole decode and a stream's first decode drop each transposed conv's first s
+        # samples when the decoder trims both sides
+        trim = self.trim_first and (state is None or state["cold"])
         cur = 0
         u = self._view(ws.u[cur], batch, length, self.in_conv.conv.n_cols)
         ic = self.in_conv
         with timer.launch("conv", 2.0 * batch * length * ic.conv.macs_per_position, ic.name):
-            fused_conv(ws.z, ic.conv, u, activation=snake, act_a=ic.out_a, act_b=ic.out_b,
+            fused_conv(z, ic.conv, u, activation=snake, act_a=ic.out_a, act_b=ic.out_b,
                        **hist(ic.name))
         for bi, blk in enumerate(self.blocks):
             up = blk.up
@@ -325,6 +343,12 @@ class DacCodecDecoder:
                            None if blk.stack else u_next.view(batch, length, up.conv.n_cols),
                            sum_out=x.view(batch, length, up.conv.n_cols), activation=snake,
                            act_a=up.out_a, act_b=up.out_b, **hist(up.name))
+            if trim:
+                # the first input sample's s outputs leave the stream: every later op reads the
+                # views that start after them
+                x = x[:, blk.stride:]
+                u_next = u_next[:, blk.stride:]
+                out_len -= blk.stride
             cur = 1 - cur
             u = u_next
             length = out_len
@@ -342,7 +366,7 @@ class DacCodecDecoder:
                 last = blk.units[-1]
                 if bi + 1 == len(self.blocks) and self.final_in_stack:
                     # the last block: the final conv runs inside the stack launch
-                    final = FinalConv(self.final_weight, self.final_bias, N.ACT_TANH,
+                    final = FinalConv(self.final_weight, self.final_bias, self.final_activation,
                                       torch.empty(batch, 1, length, dtype=torch.float32,
                                                   device=self.device),
                                       hist("final").get("history"))
@@ -392,9 +416,19 @@ class DacCodecDecoder:
         wave = torch.empty(batch, 1, length, dtype=torch.float32, device=self.device)
         with timer.launch("final", 2.0 * batch * length * self.final_taps * self.final_channels):
             single_output_conv(u, self.final_weight, self.final_bias, wave,
-                               activation=N.ACT_TANH, left_pad=self.final_taps - 1,
+                               activation=self.final_activation, left_pad=self.final_taps - 1,
                                **hist("final"))
         return self._finish_step(wave, state, batch)
+
+    def _front(self, codes: torch.Tensor, ws: _Workspace,
+               state: dict | None) -> tuple[torch.Tensor, int]:
+        """The input conv's operand [B, L, C] bf16 and L: the RVQ gather-sum of the codes."""
+        batch, _, frames = codes.shape
+        k_books, _, dim = self.codebooks.shape
+        rvq_bytes = batch * frames * (k_books * dim * 2 + dim * 2 + k_books * codes.element_size())
+        with self.timer.launch("rvq", rvq_bytes):
+            rvq_gather_sum(codes, self.codebooks, out=ws.z, clamp=True)
+        return ws.z, frames
 
     def _finish_step(self, wave: torch.Tensor, state: dict | None, batch: int) -> torch.Tensor:
         """End of a decode step: flip the slot parity of the step's rows (streaming)."""
@@ -413,7 +447,7 @@ class DacCodecDecoder:
     def frames_per_call(self, batch: int) -> int:
         """Frames one decode call takes for ``batch`` rows: longer inputs are decoded in chunks of
         this many frames through per-row slot state, which gives the same bits."""
-        per_frame, samples = 0, 1
+        per_frame, samples = 0, self.front_upsample
         for blk in self.blocks:
             samples *= blk.stride
             per_frame = max(per_frame, samples * blk.c_out * 4)

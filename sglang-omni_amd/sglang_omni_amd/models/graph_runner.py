@@ -86,7 +86,7 @@ class CodecGraphRunner:
         dec = self.decoder
         dev = dec.device
         first = key.decode == "first"
-        n_books = dec.codebooks.shape[0]
+        n_books = dec.num_codebooks
         codes = torch.zeros(key.batch_size, n_books, key.frames, dtype=torch.long, device=dev)
         index = self._scratch_index(key.batch_size)
 

@@ -1,0 +1,345 @@
+"""The Qwen3-Omni code2wav decoder on HIP kernels: ``forward`` / ``from_indices`` and streaming
+slot decodes.
+
+Drop-in for ``Qwen3OmniCode2Wav`` and ``Qwen3OmniIncrementalCodec.decode_slots``
+(sglang_omni/models/qwen3_omni/components/code2wav.py:107-460) with a slot pool shaped as the
+reference's ``CodecStatePool`` (codec_state_pool.py:26-145: conv histories, per-layer K/V rings
+indexed ``slot * ring_frames + position % ring_frames``, frame positions). Weights are read by
+``Qwen3OmniMoeCode2Wav.state_dict()`` names.
+
+A decode step on channels-last activations:
+
+    rvq_gather_sum (mean form)            codes -> h (float32 residual stream)
+    per layer (8):
+      rms_norm_residual                   h -> normed (bf16)
+      GEMM qkv (hipBLASLt)                normed -> qkv
+      rope_kv_write                       rotary on q, k in place; new K / V into the rings
+      window_attention                    q over the 72-frame window -> attn
+      GEMM o                              attn -> o
+      rms_norm_residual                   h += scale * o; normed = RMSNorm(h)
+      GEMM gate_up, silu_mul, GEMM down   normed -> d
+      rms_norm_residual                   h += scale * d; normed = RMSNorm(h) (next layer / final)
+    per upsampler (x2, x2):
+      conv_dma (transposed, k = s)        normed -> r (float32, bias included)
+      dwconv_layernorm                    r -> n (bf16; depthwise causal k7 with slot history)
+      GEMM pwconv1, bias_gelu, GEMM pwconv2, bias_scale_residual
+                                          r += gamma * (...); the next operand (bf16)
+    the causal conv stack of ``DacCodecDecoder`` with SnakeBeta coefficients, transposed convs
+    trimmed on both sides and the final clamp.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from .. import _native as N
+from ..kernels import code2wav_front as F
+from ..kernels.conv import fused_conv, pack_conv_transpose1d
+from ..kernels.rvq import rvq_gather_sum
+from .configs import Qwen3Code2WavConfig
+from .dac_codec import CodecStatePool, DacCodecDecoder, _Workspace
+
+LN_EPS = 1e-6  # Qwen3OmniMoeConvNeXtBlock's LayerNorm
+
+
+def conv_stack_tree(state: dict[str, torch.Tensor], config: Qwen3Code2WavConfig) -> dict[str, Any]:
+    """The decoder convs of a code2wav state dict as ``DacCodecDecoder``'s weight tree, each
+    SnakeBeta as its {"alpha", "beta"} log-parameters."""
+
+    def conv(prefix: str) -> dict[str, torch.Tensor]:
+        return {"weight": state[f"{prefix}.weight"].float(), "bias": state[f"{prefix}.bias"].float()}
+
+    def snake(prefix: str) -> dict[str, torch.Tensor]:
+        return {"alpha": state[f"{prefix}.alpha"].float(), "beta": state[f"{prefix}.beta"].float()}
+
+    tree: dict[str, Any] = {"in_conv": conv("decoder.0.conv"), "blocks": []}
+    for bi, rate in enumerate(config.upsample_rates, start=1):
+        p = f"decoder.{bi}.block"
+        tree["blocks"].append({
+            "stride": rate,
+            "alpha": snake(f"{p}.0"),
+            "up": conv(f"{p}.1.conv"),
+            "units": [{"dilation": d, "alpha1": snake(f"{p}.{u + 2}.act1"),
+                       "conv1": conv(f"{p}.{u + 2}.conv1.conv"),
+                       "alpha2": snake(f"{p}.{u + 2}.act2"),
+                       "conv2": conv(f"{p}.{u + 2}.conv2.conv")}
+                      for u, d in enumerate(config.dilations)],
+        })
+    n = len(config.upsample_rates)
+    tree["final"] = {"alpha": snake(f"decoder.{n + 1}"), "conv": conv(f"decoder.{n + 2}.conv")}
+    return tree
+
+
+class Code2WavStatePool(CodecStatePool):
+    """The conv stack's per-slot histories (``CodecStatePool``), plus what the front streams:
+    per-layer K / V rings [slots * ring_frames, kv_heads * head_dim] bf16, the slots' frame
+    positions, and the ConvNeXt depthwise convs' float32 histories [slots, 2, 6, C]."""
+
+    def __init__(self, layout: list[tuple[str, int, int]], *, num_slots: int, capture_slots: int,
+                 device: torch.device, num_layers: int, kv_width: int, ring_frames: int,
+                 retained_frames: int, dw_names: list[str], channels: int):
+        super().__init__(layout, num_slots=num_slots, capture_slots=capture_slots, device=device)
+        if ring_frames <= retained_frames:
+            raise ValueError("a ring holds the window and the new frames")
+        total = num_slots + capture_slots
+        self.ring_frames = ring_frames
+        self.retained_frames = retained_frames
+        self.keys = [torch.zeros(total * ring_frames, kv_width, dtype=torch.bfloat16, device=device)
+                     for _ in range(num_layers)]
+        self.values = [torch.zeros_like(ring) for ring in self.keys]
+        self.frame_positions = torch.zeros(total, dtype=torch.int64, device=device)
+        self.dw_histories = {name: torch.zeros(total, 2, 6, channels, dtype=torch.float32,
+                                               device=device) for name in dw_names}
+        self.bytes_per_slot += (2 * num_layers * ring_frames * kv_width * 2
+                                + len(dw_names) * 2 * 6 * channels * 4 + 8)
+
+    def zero_slots(self, slots: torch.Tensor) -> None:
+        super().zero_slots(slots)
+        for ring in (*self.keys, *self.values):
+            ring.view(-1, self.ring_frames, ring.shape[1]).index_fill_(0, slots, 0)
+        for pool in self.dw_histories.values():
+            pool.index_fill_(0, slots, 0)
+        self.frame_positions.index_fill_(0, slots, 0)
+
+
+class Qwen3Code2WavDecoder(DacCodecDecoder):
+    """Qwen3-Omni code2wav, every op but the transformer's and ConvNeXt's plain GEMMs on gfx950
+    HIP kernels (the GEMMs are hipBLASLt through torch.mm, on the same stream). ``state`` is a
+    ``Qwen3OmniMoeCode2Wav.state_dict()``-named float32 dict (``configs.make_qwen3_code2wav_
+    weights``); conv weights are bf16 (``weight_format`` "fp8" quantizes the decoder convs)."""
+
+    DEFAULT_RING_EXTRA = 64  # frames one decode may add to a pool built with the default ring
+
+    def __init__(self, state: dict[str, torch.Tensor], config: Qwen3Code2WavConfig, *,
+                 device: torch.device | str = "cuda", weight_format: str = "bf16",
+                 residual_stacks: bool = True):
+        super().__init__(conv_stack_tree(state, config), config, device=device,
+                         weight_format=weight_format, residual_stacks=residual_stacks)
+        cfg = config
+        dev = self.device
+        if cfg.head_dim != 64:
+            raise ValueError("the attention kernel takes head_dim 64")
+        self.front_upsample = int(math.prod(cfg.upsampling_ratios))
+        self.num_codebooks = cfg.num_quantizers
+        c = cfg.hidden_size
+        self.hidden = c
+        self.kv_width = cfg.num_key_value_heads * cfg.head_dim
+
+        def bf16(t: torch.Tensor) -> torch.Tensor:
+            return t.float().to(torch.bfloat16).to(dev).contiguous()
+
+        def f32(t: torch.Tensor) -> torch.Tensor:
+            return t.float().to(dev).contiguous()
+
+        self.code_tables = bf16(state["code_embedding.weight"].view(cfg.num_quantizers,
+                                                                    cfg.codebook_size, c))
+        self.layers = []
+        for i in range(cfg.num_hidden_layers):
+            p = f"pre_transformer.layers.{i}"
+            qkv = torch.cat([state[f"{p}.self_attn.{n}_proj.weight"] for n in "qkv"], dim=0)
+            gate_up = torch.cat([state[f"{p}.mlp.gate_proj.weight"],
+                                 state[f"{p}.mlp.up_proj.weight"]], dim=0)
+            # GEMM operands as [in, out] row-major: x @ W with no transposed views
+            self.layers.append({
+                "in_norm": f32(state[f"{p}.input_layernorm.weight"]),
+                "qkv": bf16(qkv.t()),
+                "o": bf16(state[f"{p}.self_attn.o_proj.weight"].t()),
+                "attn_scale": f32(state[f"{p}.self_attn_layer_scale.scale"]),
+                "post_norm": f32(state[f"{p}.post_attention_layernorm.weight"]),
+                "gate_up": bf16(gate_up.t()),
+                "down": bf16(state[f"{p}.mlp.down_proj.weight"].t()),
+                "mlp_scale": f32(state[f"{p}.mlp_layer_scale.scale"]),
+            })
+        self.final_norm = f32(state["pre_transformer.norm.weight"])
+        # inv_freq as the rotary module computes it, in float32
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2,
+                                                                dtype=torch.float32)
+                                                   / cfg.head_dim))).to(dev).contiguous()
+        self.upsamplers = []
+        for i, factor in enumerate(cfg.upsampling_ratios):
+            p = f"upsample.{i}.1"
+            self.upsamplers.append({
+                "name": f"upsample.{i}.convnext.dwconv",
+                "factor": factor,
+                "up": pack_conv_transpose1d(state[f"upsample.{i}.0.conv.weight"].float(),
+                                            state[f"upsample.{i}.0.conv.bias"].float(),
+                                            stride=factor).to(dev),
+                "dw_weight": f32(state[f"{p}.dwconv.conv.weight"][:, 0, :].t()),  # [7, C]
+                "dw_bias": f32(state[f"{p}.dwconv.conv.bias"]),
+                "ln_weight": f32(state[f"{p}.norm.weight"]),
+                "ln_bias": f32(state[f"{p}.norm.bias"]),
+                "w1": bf16(state[f"{p}.pwconv1.weight"].t()),
+                "b1": f32(state[f"{p}.pwconv1.bias"]),
+                "w2": bf16(state[f"{p}.pwconv2.weight"].t()),
+                "b2": f32(state[f"{p}.pwconv2.bias"]),
+                "gamma": f32(state[f"{p}.gamma"]),
+            })
+            if self.upsamplers[-1]["up"].taps != 1:
+                raise ValueError("the upsamplers' transposed convs have k = s")
+
+    # ---------------------------------------------------------------- state pool
+
+    def new_state_pool(self, num_slots: int, capture_slots: int = 0,
+                       ring_frames: int | None = None) -> Code2WavStatePool:
+        """A pool whose rings hold the window and up to ``ring_frames - (sliding_window - 1)``
+        new frames per decode (default: 64)."""
+        retained = self.config.sliding_window - 1
+        if ring_frames is None:
+            ring_frames = retained + self.DEFAULT_RING_EXTRA
+        return Code2WavStatePool(
+            self.state_layout(), num_slots=num_slots, capture_slots=capture_slots,
+            device=self.device, num_layers=self.config.num_hidden_layers,
+            kv_width=self.kv_width, ring_frames=ring_frames, retained_frames=retained,
+            dw_names=[u["name"] for u in self.upsamplers], channels=self.hidden)
+
+    # ---------------------------------------------------------------- front
+
+    def _front_buffers(self, ws: _Workspace, batch: int, frames: int) -> dict[str, torch.Tensor]:
+        if ws.front:
+            return ws.front
+        dev, c, cfg = self.device, self.hidden, self.config
+        m = batch * frames
+        bf = torch.bfloat16
+        width = c + 2 * self.kv_width
+        big = max(m * 2 * cfg.intermediate_size, m * width)
+        buf = {
+            "h": torch.empty(m, c, dtype=torch.float32, device=dev),
+            "normed": torch.empty(m, c, dtype=bf, device=dev),
+            "qkv": torch.empty(m, width, dtype=bf, device=dev),
+            "attn": torch.empty(m, c, dtype=bf, device=dev),
+            "proj": torch.empty(m, c, dtype=bf, device=dev),
+            "wide": torch.empty(big, dtype=bf, device=dev),
+            "act": torch.empty(m, cfg.intermediate_size, dtype=bf, device=dev),
+        }
+        length = frames
+        for i, up in enumerate(self.upsamplers):
+            length *= up["factor"]
+            buf[f"r{i}"] = torch.empty(batch, length, c, dtype=torch.float32, device=dev)
+            buf[f"n{i}"] = torch.empty(batch, length, c, dtype=bf, device=dev)
+            buf[f"p1_{i}"] = torch.empty(batch * length, 4 * c, dtype=bf, device=dev)
+            buf[f"p2_{i}"] = torch.empty(batch * length, c, dtype=bf, device=dev)
+            buf[f"z{i}"] = torch.empty(batch, length, c, dtype=bf, device=dev)
+        ws.front.update(buf)
+        return ws.front
+
+    def _front(self, codes: torch.Tensor, ws: _Workspace,
+               state: dict | None) -> tuple[torch.Tensor, int]:
+        cfg = self.config
+        batch, books, frames = codes.shape
+        if books != cfg.num_quantizers:
+            raise ValueError(f"Expected {cfg.num_quantizers} layer of codes, got {books}")
+        buf = self._front_buffers(ws, batch, frames)
+        timer = self.timer
+        c, m = self.hidden, batch * frames
+        pool = None if state is None else state["pool"]
+        cold = True if state is None else bool(state["cold"])
+        slots = None if state is None else state["slot_index"]
+        if state is not None:
+            state["new_frames"] = frames
+            if not cold and frames > pool.ring_frames - pool.retained_frames:
+                raise ValueError(f"{frames} new frames overflow the pool's {pool.ring_frames}-frame "
+                                 f"rings (window {pool.retained_frames} + new frames)")
+        h, normed, qkv = buf["h"], buf["normed"], buf["qkv"]
+        attn, proj, act = buf["attn"], buf["proj"], buf["act"]
+        gate_up = buf["wide"][: m * 2 * cfg.intermediate_size].view(m, 2 * cfg.intermediate_size)
+        k_books, _, dim = self.code_tables.shape
+        with timer.launch("rvq", m * (k_books * dim * 2 + dim * 4 + k_books * codes.element_size())):
+            rvq_gather_sum(codes, self.code_tables, out=h.view(batch, frames, c), mean=True,
+                           clamp=True)
+        heads, kv_heads, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        eps = cfg.rms_norm_eps
+        with timer.launch("front_elementwise", 0.0):
+            F.rms_norm_residual(h, self.layers[0]["in_norm"], eps, normed)
+        for i, layer in enumerate(self.layers):
+            ring = {}
+            if pool is not None:
+                ring = {"slot_index": slots, "positions": pool.frame_positions,
+                        "key_ring": pool.keys[i], "value_ring": pool.values[i],
+                        "ring_frames": pool.ring_frames}
+            with timer.launch("front_gemm", 2.0 * m * c * qkv.shape[1]):
+                torch.mm(normed, layer["qkv"], out=qkv)
+            with timer.launch("front_elementwise", 0.0):
+                F.rope_kv_write(qkv, batch, heads, kv_heads, hd, self.inv_freq, cold=cold, **ring)
+            # a first decode attends to its own frames: the keys are in qkv already
+            attend_ring = {} if cold else ring
+            with timer.launch("front_attention", 4.0 * m * heads * hd * cfg.sliding_window):
+                F.window_attention(qkv, batch, heads, kv_heads, hd, cfg.sliding_window,
+                                   hd ** -0.5, attn, cold=cold, **attend_ring)
+            with timer.launch("front_gemm", 2.0 * m * c * c):
+                torch.mm(attn, layer["o"], out=proj)
+            with timer.launch("front_elementwise", 0.0):
+                F.rms_norm_residual(h, layer["post_norm"], eps, normed, delta=proj,
+                                    scale=layer["attn_scale"])
+            with timer.launch("front_gemm", 2.0 * m * c * gate_up.shape[1]):
+                torch.mm(normed, layer["gate_up"], out=gate_up)
+            with timer.launch("front_elementwise", 0.0):
+                F.silu_mul(gate_up, act)
+            with timer.launch("front_gemm", 2.0 * m * act.shape[1] * c):
+                torch.mm(act, layer["down"], out=proj)
+            nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
+            with timer.launch("front_elementwise", 0.0):
+                F.rms_norm_residual(h, nxt, eps, normed, delta=proj, scale=layer["mlp_scale"])
+        x = normed.view(batch, frames, c)
+        length = frames
+        for i, up in enumerate(self.upsamplers):
+            factor = up["factor"]
+            r = buf[f"r{i}"]
+            with timer.launch("conv", 2.0 * batch * length * up["up"].macs_per_position,
+                              f"upsample.{i}.up"):
+                fused_conv(x, up["up"], None, sum_out=r.view(batch, length, factor * c))
+            length *= factor
+            hist = {}
+            if pool is not None:
+                hist = {"history": pool.dw_histories[up["name"]], "slot_index": slots,
+                        "slot_parity": pool.parity, "history_cold": cold}
+            n = buf[f"n{i}"]
+            with timer.launch("front_elementwise", 0.0):
+                F.dwconv_layernorm(r, up["dw_weight"], up["dw_bias"], up["ln_weight"],
+                                   up["ln_bias"], LN_EPS, n, **hist)
+            rows = batch * length
+            p1, p2 = buf[f"p1_{i}"], buf[f"p2_{i}"]
+            with timer.launch("front_gemm", 2.0 * rows * c * 4 * c):
+                torch.mm(n.view(rows, c), up["w1"], out=p1)
+            with timer.launch("front_elementwise", 0.0):
+                F.bias_gelu(p1, up["b1"])
+            with timer.launch("front_gemm", 2.0 * rows * 4 * c * c):
+                torch.mm(p1, up["w2"], out=p2)
+            z = buf[f"z{i}"]
+            with timer.launch("front_elementwise", 0.0):
+                F.bias_scale_residual(r.view(rows, c), p2, up["b2"], up["gamma"],
+                                      out=z.view(rows, c))
+            x = z
+        return x, length
+
+    def _finish_step(self, wave: torch.Tensor, state: dict | None, batch: int) -> torch.Tensor:
+        if state is not None:
+            F.advance_positions(state["pool"].frame_positions, state["slot_index"],
+                                state["new_frames"], bool(state["cold"]))
+        return super()._finish_step(wave, state, batch)
+
+    # ---------------------------------------------------------------- API
+
+    @torch.no_grad()
+    def from_indices(self, indices: torch.Tensor) -> torch.Tensor:
+        """Qwen3OmniMoeCode2Wav.forward: [B, Q, T] codes -> [B, 1, samples] float32 (the whole
+        decode drops each decoder transposed conv's first and last s samples). Long inputs
+        decode in chunks through a temporary slot pool, which gives the same samples."""
+        if indices.dim() != 3:
+            raise ValueError(f"codes must be [B, Q, T], got {tuple(indices.shape)}")
+        batch, _, frames = indices.shape
+        step = self.frames_per_call(batch)
+        if frames <= step:
+            return self._decode(indices, None)
+        pool = self.new_state_pool(num_slots=batch,
+                                   ring_frames=self.config.sliding_window - 1 + step)
+        rows = torch.arange(batch, device=self.device)
+        parts = [self._decode(indices[..., s:s + step],
+                              {"pool": pool, "slot_index": rows, "cold": s == 0})
+                 for s in range(0, frames, step)]
+        return torch.cat(parts, dim=-1)
+
+    __call__ = from_indices
+    forward = from_indices
