@@ -435,7 +435,7 @@ int omni_waveform_egress(const float* wave, int64_t rows, int64_t samples,
  *   positions p with 0 <= P - p < window (P the query's position) of scale * q . k, times v;
  *   keys / values from the rings (which must hold the window before the new frames, ring_frames >=
  *   window - 1 + frames) or, for a first decode (cold, rings NULL), from qkv itself
- *   (code2wav.py:227-256,295-316). head_dim 64, window <= 104 (the window's keys sit in LDS).
+ *   (code2wav.py:227-256,295-316). head_dim 64, window <= 113 (the window and 16 queries' keys sit in LDS).
  * omni_silu_mul: out[row, i] = silu(gate_up[row, i]) * gate_up[row, inter + i], bf16.
  * omni_dwconv_layernorm: ConvNeXt's depthwise causal conv (7 taps, weight [7][channels]
  *   float32, tap 6 on the current sample) over x [batch][length][channels] float32 with slot

@@ -8,8 +8,8 @@
 //                              rows' absolute positions, and the new K / V into the slots' rings
 //                              (apply_rope_inplace_with_kvcache, code2wav.py:216-226)
 //   window_attention_kernel    causal sliding-window softmax attention of the new frames over
-//                              their window: the rows' rings or, for a stream's first decode, the
-//                              qkv buffer itself (code2wav.py:227-256,295-316)
+//                              their window (rows' rings or, for a stream's first decode, the
+//                              qkv buffer itself) on MFMA (code2wav.py:227-256,295-316)
 //   silu_mul_kernel            silu(gate) * up of the merged gate / up GEMM (code2wav.py:353)
 //   dwconv_layernorm_kernel    ConvNeXt's depthwise causal conv (k = 7) over the float32
 //                              residual stream with per-slot history, then LayerNorm, as the
@@ -206,10 +206,21 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeParams p) {
 }
 
 // ------------------------------------------------------------------------------ attention
+//
+// One wave per (batch row, head, tile of 16 queries), both products on v_mfma_f32_16x16x32_bf16:
+//   S^T = K Q^T   (M = 16 keys per tile, N = 16 queries, K = 64 dims in two steps)
+//   O^T = V^T P^T (M = 16 dims per tile, N = 16 queries, K = 32 keys per step)
+// Lane l = 16 g + n holds S^T[key 4 g + e][query n] of each key tile (e < 4). The softmax of
+// query n reduces over the lane's registers and the 4 lanes n, n + 16, n + 32, n + 48. For the
+// second product the lane's probabilities go in as they lie: K-step s takes, in lane (g, n), the
+// keys 32 s + 4 g + (0..3) of tile 2 s and 32 s + 16 + 4 g + (0..3) of tile 2 s + 1, and V^T is
+// read from LDS in that same key order, so the keys' order in the sum is a fixed permutation and
+// no probability crosses lanes. P is rounded to bf16 for the product; everything else is float32.
 
-constexpr int kQueries = 16;  // queries per workgroup, 4 per wave
-constexpr int kHeadDim = 64;  // one dimension per lane in the P . V product
-constexpr int kKPitch = kHeadDim + 1;  // float pitch of a K row in LDS (conflict-free reads)
+constexpr int kQueries = 16;     // queries per wave
+constexpr int kHeadDim = 64;
+constexpr int kMaxKeyTiles = 8;  // 16-key tiles: window - 1 + 16 <= 128 keys
+constexpr int kKRow = kHeadDim + 8;  // bf16 pitch of a K row in LDS (16-byte reads spread banks)
 
 struct AttnParams {
   const u16* qkv;
@@ -217,7 +228,7 @@ struct AttnParams {
   int64_t qkv_stride;
   int heads, kv_heads;
   int window;
-  float scale;
+  float scale_log2;  // softmax scale times log2(e): p = 2^(s * scale_log2 - max)
   const u16* key_ring;  // null: keys and values come from qkv (a first decode)
   const u16* value_ring;
   int64_t ring_frames;
@@ -227,103 +238,152 @@ struct AttnParams {
   int64_t num_slots;
   u16* out;
   int64_t out_stride;
+  int key_slots;  // keys staged per wave: a multiple of 32 >= window - 1 + 16
 };
 
-size_t attention_lds_bytes(int window) {
-  const int keys = window - 1 + kQueries;
-  return sizeof(float) * ((size_t)keys * kKPitch + (size_t)keys * kHeadDim + kQueries * kHeadDim);
+size_t attention_lds_bytes(int key_slots) {
+  // K [key_slots][kKRow] and V^T [64][key_slots + 8], bf16
+  return 2 * ((size_t)key_slots * kKRow + (size_t)kHeadDim * (key_slots + 8));
 }
 
-__global__ __launch_bounds__(256) void window_attention_kernel(AttnParams p) {
-  extern __shared__ float lds[];
+__global__ __launch_bounds__(64) void window_attention_kernel(AttnParams p) {
+  extern __shared__ u16 alds[];
   const int64_t b = blockIdx.z;
   const int head = blockIdx.y;
   const int64_t t0 = (int64_t)blockIdx.x * kQueries;
   const int kvh = head / (p.heads / p.kv_heads);
-  const int max_keys = p.window - 1 + kQueries;
-  float* ks = lds;                                  // [max_keys][kKPitch]
-  float* vs = ks + (size_t)max_keys * kKPitch;       // [max_keys][kHeadDim]
-  float* qs = vs + (size_t)max_keys * kHeadDim;      // [kQueries][kHeadDim]
+  const int lane = threadIdx.x;
+  const int ks_n = p.key_slots;
+  const int vpitch = ks_n + 8;
+  u16* ks = alds;                              // [ks_n][kKRow]
+  u16* vt = alds + (size_t)ks_n * kKRow;       // [64][vpitch]
   int64_t slot;
   const int64_t start = row_start(p.slot_index, p.positions, p.cold, p.num_slots, b, &slot);
   const bool ring = p.key_ring != nullptr;
   const int64_t p0 = start + t0;
   const int64_t last_t = min(t0 + kQueries, p.frames) - 1;
   const int64_t kp0 = max(p0 - (p.window - 1), (int64_t)0);
-  const int64_t kp1 = start + last_t;
-  const int nk = (int)(kp1 - kp0 + 1);  // <= max_keys
+  const int nk = (int)(start + last_t - kp0 + 1);  // <= window - 1 + 16 <= ks_n
   const int kv_width = p.kv_heads * kHeadDim;
-  // stage K and V of positions kp0..kp1 and the block's queries, 8 bf16 per thread and step
-  const int chunks = nk * (kHeadDim / 8);
-  for (int e = threadIdx.x; e < chunks; e += blockDim.x) {
-    const int r = e / (kHeadDim / 8);
-    const int c8 = (e - r * (kHeadDim / 8)) * 8;
-    const int64_t kpos = kp0 + r;
-    const u16* ksrc;
-    const u16* vsrc;
-    if (ring) {
-      const int64_t rr = (slot < 0 ? 0 : slot) * p.ring_frames + kpos % p.ring_frames;
-      ksrc = p.key_ring + rr * kv_width + kvh * kHeadDim + c8;
-      vsrc = p.value_ring + rr * kv_width + kvh * kHeadDim + c8;
-    } else {
-      const u16* tok = p.qkv + (b * p.frames + (kpos - start)) * p.qkv_stride;
-      ksrc = tok + (p.heads + kvh) * kHeadDim + c8;
-      vsrc = tok + (p.heads + p.kv_heads + kvh) * kHeadDim + c8;
+  // stage K (row-major) and V (transposed), 8 bf16 per lane and step; rows >= nk are zeros
+  for (int e = lane; e < ks_n * (kHeadDim / 8); e += kWave) {
+    const int r = e >> 3;
+    const int c8 = (e & 7) * 8;
+    uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+    if (r < nk) {
+      const int64_t kpos = kp0 + r;
+      const u16* ksrc;
+      const u16* vsrc;
+      if (ring) {
+        const int64_t rr = (slot < 0 ? 0 : slot) * p.ring_frames + kpos % p.ring_frames;
+        ksrc = p.key_ring + rr * kv_width + kvh * kHeadDim + c8;
+        vsrc = p.value_ring + rr * kv_width + kvh * kHeadDim + c8;
+      } else {
+        const u16* tok = p.qkv + (b * p.frames + (kpos - start)) * p.qkv_stride;
+        ksrc = tok + (p.heads + kvh) * kHeadDim + c8;
+        vsrc = tok + (p.heads + p.kv_heads + kvh) * kHeadDim + c8;
+      }
+      kw = *reinterpret_cast<const uint4*>(ksrc);
+      vw = *reinterpret_cast<const uint4*>(vsrc);
     }
-    float kv[8];
-    load_bf16x8(ksrc, kv);
+    *reinterpret_cast<uint4*>(ks + r * kKRow + c8) = kw;
+    const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ks[r * kKPitch + c8 + i] = kv[i];
-    load_bf16x8(vsrc, kv);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vs[r * kHeadDim + c8 + i] = kv[i];
+    for (int i = 0; i < 4; ++i) {
+      vt[(c8 + 2 * i) * vpitch + r] = (u16)(vv[i] & 0xffff);
+      vt[(c8 + 2 * i + 1) * vpitch + r] = (u16)(vv[i] >> 16);
+    }
   }
+  // this lane's query row n (zeros past the last query) as the B operand, dims 8 g .. 8 g + 7
+  // and 32 + 8 g ..
+  const int n = lane & 15;
+  const int g = lane >> 4;
   const int nq = (int)(last_t - t0 + 1);
-  for (int e = threadIdx.x; e < nq * (kHeadDim / 8); e += blockDim.x) {
-    const int q = e / (kHeadDim / 8);
-    const int c8 = (e - q * (kHeadDim / 8)) * 8;
-    float qv[8];
-    load_bf16x8(p.qkv + (b * p.frames + t0 + q) * p.qkv_stride + head * kHeadDim + c8, qv);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qs[q * kHeadDim + c8 + i] = qv[i];
+  bf16x8 qv[2];
+  {
+    uint4 w0 = make_uint4(0, 0, 0, 0), w1 = w0;
+    if (n < nq) {
+      const u16* q = p.qkv + (b * p.frames + t0 + n) * p.qkv_stride + head * kHeadDim + 8 * g;
+      w0 = *reinterpret_cast<const uint4*>(q);
+      w1 = *reinterpret_cast<const uint4*>(q + 32);
+    }
+    qv[0] = *reinterpret_cast<const bf16x8*>(&w0);
+    qv[1] = *reinterpret_cast<const bf16x8*>(&w1);
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int qi = 0; qi < kQueries / 4; ++qi) {
-    const int q = wave * (kQueries / 4) + qi;
-    if (q >= nq) break;
-    const int64_t pos = p0 + q;
-    const int lo = (int)(max(pos - (p.window - 1), (int64_t)0) - kp0);
-    const int n = (int)(pos - kp0) - lo + 1;  // keys of this query, <= window <= 128
-    const float* qrow = qs + q * kHeadDim;
-    float s0 = -INFINITY, s1 = -INFINITY;
-    const int r0 = lo + lane, r1 = lo + lane + kWave;
-    if (lane < n) {
-      float acc = 0.f;
-      const float* krow = ks + r0 * kKPitch;
-#pragma unroll 16
-      for (int d = 0; d < kHeadDim; ++d) acc += qrow[d] * krow[d];
-      s0 = acc * p.scale;
+  const int tiles = (nk + 15) / 16;
+  f32x4 st[kMaxKeyTiles];
+  const int64_t qpos = p0 + n;
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < kMaxKeyTiles; ++t) {
+    if (t < tiles) {
+      const u16* krow = ks + (16 * t + n) * kKRow + 8 * g;  // A: key row (lane & 15)
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(krow),
+                                                    qv[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(krow + 32),
+                                                    qv[1], acc, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = 16 * t + 4 * g + e;
+        const int64_t d = qpos - (kp0 + key);
+        const bool ok = key < nk && d >= 0 && d < p.window;
+        acc[e] = ok ? acc[e] * p.scale_log2 : -INFINITY;
+        m = fmaxf(m, acc[e]);
+      }
+      st[t] = acc;
+    } else {
+      st[t] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
-    if (lane + kWave < n) {
-      float acc = 0.f;
-      const float* krow = ks + r1 * kKPitch;
-#pragma unroll 16
-      for (int d = 0; d < kHeadDim; ++d) acc += qrow[d] * krow[d];
-      s1 = acc * p.scale;
+  }
+  m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  if (m == -INFINITY) m = 0.f;  // a padding query (no stored output)
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < kMaxKeyTiles; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pe = t < tiles ? __builtin_amdgcn_exp2f(st[t][e] - m) : 0.f;
+      st[t][e] = pe;
+      sum += pe;
     }
-    const float m = wave_max(fmaxf(s0, s1));
-    const float e0 = lane < n ? __expf(s0 - m) : 0.f;
-    const float e1 = lane + kWave < n ? __expf(s1 - m) : 0.f;
-    const float sum = wave_sum(e0 + e1);
-    float o = 0.f;
-    for (int j = 0; j < n; ++j) {
-      const float pj = __shfl(j < kWave ? e0 : e1, j & (kWave - 1), kWave);
-      o += pj * vs[(lo + j) * kHeadDim + lane];
+  sum += __shfl_xor(sum, 16, kWave);
+  sum += __shfl_xor(sum, 32, kWave);
+  // O^T = V^T P^T over K-steps of 32 keys
+  f32x4 o[kHeadDim / 16];
+#pragma unroll
+  for (int dt = 0; dt < kHeadDim / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < kMaxKeyTiles / 2; ++s2) {
+    if (2 * s2 < tiles) {
+      bf16x8 pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pb[e] = to_bf16(st[2 * s2][e]);
+        pb[4 + e] = to_bf16(st[2 * s2 + 1][e]);
+      }
+      const int k0 = 32 * s2 + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+        const u16* vrow = vt + (16 * dt + n) * vpitch;  // A: dim row (lane & 15)
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + k0);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + k0 + 16);
+        const uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(&w), pb,
+                                                        o[dt], 0, 0, 0);
+      }
     }
-    p.out[(b * p.frames + t0 + q) * p.out_stride + head * kHeadDim + lane] =
-        float_to_bits_bf16(o / sum);
+  }
+  if (n < nq) {
+    const float inv = 1.f / sum;
+    u16* dst = p.out + (b * p.frames + t0 + n) * p.out_stride + head * kHeadDim + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+      const float v[4] = {o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv};
+      store_bf16x4(dst + 16 * dt, v);
+    }
   }
 }
 
@@ -592,11 +652,11 @@ extern "C" int omni_window_attention(const void* qkv, int64_t batch, int64_t fra
   if (!qkv || !out || batch < 0 || frames < 0) return OMNI_ERR_INVALID_ARG;
   if (heads < 1 || kv_heads < 1 || heads % kv_heads) return OMNI_ERR_INVALID_ARG;
   if (head_dim != kHeadDim) return OMNI_ERR_UNSUPPORTED;
-  if (window < 1 || window > 2 * kWave) return OMNI_ERR_UNSUPPORTED;
+  if (window < 1) return OMNI_ERR_INVALID_ARG;
   if (qkv_stride < (heads + 2 * kv_heads) * head_dim || qkv_stride % 8 ||
-      out_stride < heads * head_dim)
+      out_stride < heads * head_dim || out_stride % 4)
     return OMNI_ERR_INVALID_ARG;
-  if (!aligned(qkv, 16)) return OMNI_ERR_INVALID_ARG;
+  if (!aligned(qkv, 16) || !aligned(out, 8)) return OMNI_ERR_INVALID_ARG;
   if ((key_ring != nullptr) != (value_ring != nullptr)) return OMNI_ERR_INVALID_ARG;
   if (key_ring) {
     // the ring holds the window before the new frames and the frames themselves
@@ -608,14 +668,15 @@ extern "C" int omni_window_attention(const void* qkv, int64_t batch, int64_t fra
   }
   if (batch * frames == 0) return OMNI_OK;
   if (batch > 65535 || heads > 65535) return OMNI_ERR_UNSUPPORTED;
+  const int key_slots = (int)((window - 1 + kQueries + 31) / 32 * 32);
+  if (key_slots > 16 * kMaxKeyTiles) return OMNI_ERR_UNSUPPORTED;
   AttnParams p{static_cast<const u16*>(qkv), frames, qkv_stride, (int)heads, (int)kv_heads,
-               (int)window, scale, static_cast<const u16*>(key_ring),
+               (int)window, scale * 1.4426950408889634f, static_cast<const u16*>(key_ring),
                static_cast<const u16*>(value_ring), ring_frames, slot_index, positions, cold,
-               num_slots, static_cast<u16*>(out), out_stride};
-  const size_t lds = attention_lds_bytes((int)window);
-  if (lds > 64 * 1024) return OMNI_ERR_UNSUPPORTED;
+               num_slots, static_cast<u16*>(out), out_stride, key_slots};
+  const size_t lds = attention_lds_bytes(key_slots);
   dim3 grid(blocks_for(frames, kQueries), (unsigned)heads, (unsigned)batch);
-  hipLaunchKernelGGL(window_attention_kernel, grid, dim3(256), lds,
+  hipLaunchKernelGGL(window_attention_kernel, grid, dim3(kWave), lds,
                      reinterpret_cast<hipStream_t>(stream), p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
