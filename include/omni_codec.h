@@ -421,7 +421,7 @@ int omni_waveform_egress(const float* wave, int64_t rows, int64_t samples,
  * plain GEMMs. Activations are bf16 rows (GEMM operands / outputs) and float32 residual streams.
  *
  * omni_rms_norm_residual: per row of h [rows][channels] float32 (contiguous): if delta, h +=
- *   scale[c] * delta[row, c] (the layer-scaled residual add, code2wav.py:338-356's addcmul);
+ *   scale[c] * delta[row, c] (the layer-scaled residual add, code2wav.py:300-324's addcmul);
  *   then normed[row, c] = weight[c] * h[row, c] / sqrt(mean_c(h^2) + eps) as bf16 (rmsnorm).
  *   channels a multiple of 256, at most 4096.
  * omni_rope_kv_write: qkv [batch * frames][qkv_stride] bf16 holds q (heads * head_dim), k, v
@@ -430,12 +430,12 @@ int omni_waveform_egress(const float* wave, int64_t rows, int64_t samples,
  *   positions[slot_index[b]]); with key_ring / value_ring ([slots * ring_frames][kv_heads *
  *   head_dim] bf16) the rotated k and the v of each frame also go to ring row
  *   slot * ring_frames + position % ring_frames (apply_rope_inplace_with_kvcache,
- *   code2wav.py:216-226).
+ *   code2wav.py:205-215).
  * omni_window_attention: out[b * frames + t, h * 64 + d] (bf16) = softmax over the keys at
  *   positions p with 0 <= P - p < window (P the query's position) of scale * q . k, times v;
  *   keys / values from the rings (which must hold the window before the new frames, ring_frames >=
  *   window - 1 + frames) or, for a first decode (cold, rings NULL), from qkv itself
- *   (code2wav.py:227-256,295-316). head_dim 64, window <= 113 (the window and 16 queries' keys sit in LDS).
+ *   (code2wav.py:227-246,278-298). head_dim 64, window <= 113 (the window and 16 queries' keys sit in LDS).
  * omni_silu_mul: out[row, i] = silu(gate_up[row, i]) * gate_up[row, inter + i], bf16.
  * omni_dwconv_layernorm: ConvNeXt's depthwise causal conv (7 taps, weight [7][channels]
  *   float32, tap 6 on the current sample) over x [batch][length][channels] float32 with slot

@@ -65,7 +65,7 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: 
                      scale: float, q_offset: int = 0) -> torch.Tensor:
     """Causal sliding-window softmax attention of q [B, H, Tq, d] over k / v [B, H, Tk, d]:
     query i (absolute position q_offset + i) sees keys j with 0 <= (q_offset + i) - j < window
-    (TF's sliding-window causal mask, the reference's window_mask at code2wav.py:170-177)."""
+    (TF's sliding-window causal mask, the reference's window_mask at code2wav.py:143-147,185-201)."""
     tq, tk = q.shape[2], k.shape[2]
     qpos = torch.arange(tq)[:, None] + q_offset
     kpos = torch.arange(tk)[None, :]

@@ -3,14 +3,14 @@
 //
 //   rms_norm_residual_kernel   h += scale * delta (layer scale + residual, float32 h), then
 //                              normed = RMSNorm(h) * weight as the next GEMM's bf16 operand
-//                              (code2wav.py:338-356's addcmul + rmsnorm; the layer's input norm)
+//                              (code2wav.py:300-324's addcmul + rmsnorm; the layer's input norm)
 //   rope_kv_kernel             neox rotary on q and k in the qkv GEMM output, in place, at the
 //                              rows' absolute positions, and the new K / V into the slots' rings
-//                              (apply_rope_inplace_with_kvcache, code2wav.py:216-226)
+//                              (apply_rope_inplace_with_kvcache, code2wav.py:205-215)
 //   window_attention_kernel    causal sliding-window softmax attention of the new frames over
 //                              their window (rows' rings or, for a stream's first decode, the
-//                              qkv buffer itself) on MFMA (code2wav.py:227-256,295-316)
-//   silu_mul_kernel            silu(gate) * up of the merged gate / up GEMM (code2wav.py:353)
+//                              qkv buffer itself) on MFMA (code2wav.py:227-246,278-298)
+//   silu_mul_kernel            silu(gate) * up of the merged gate / up GEMM (code2wav.py:318)
 //   dwconv_layernorm_kernel    ConvNeXt's depthwise causal conv (k = 7) over the float32
 //                              residual stream with per-slot history, then LayerNorm, as the
 //                              first MLP GEMM's bf16 operand (incremental_codec.py:160-175)

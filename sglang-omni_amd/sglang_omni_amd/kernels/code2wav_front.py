@@ -1,5 +1,5 @@
 """The Qwen3-Omni code2wav front's HIP kernels: the ops around the pre-transformer's and the
-ConvNeXt upsamplers' GEMMs (sglang_omni/models/qwen3_omni/components/code2wav.py:107-356 runs
+ConvNeXt upsamplers' GEMMs (sglang_omni/models/qwen3_omni/components/code2wav.py:107-324 runs
 them as rmsnorm / rope / attention / silu_and_mul / addcmul kernels; incremental_codec.py:137-175
 the ConvNeXt blocks). Every wrapper launches on the current stream and validates before launch.
 """
