@@ -23,6 +23,7 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
                 the staging of the step through a pinned slot to host arrays (PCIe-inclusive);
   calibration   the box's practical peaks: a 1 GiB copy and a bf16 8192^3 GEMM.
 
+--only qwen3_code2wav runs the Qwen3-Omni code2wav leg alone (its kernel-trace profile).
 --only stack96 / --only copy run one kernel alone for hardware-counter profiles: the roofline
 kernel (the 96-channel residual stack of the same decoder, x [64, 23040, 96]) or a plain 1 GiB
 device copy (the calibration of the FETCH_SIZE / WRITE_SIZE counters), --launches times each.
@@ -453,8 +454,9 @@ def main() -> None:
     parser.add_argument("--workload", default="streaming64")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-rvq-large", action="store_true")
-    parser.add_argument("--only", choices=["stack96", "copy"],
-                        help="run one kernel alone (hardware-counter profiles); prints no JSON")
+    parser.add_argument("--only", choices=["stack96", "copy", "qwen3_code2wav"],
+                        help="run one kernel alone (hardware-counter profiles; prints no JSON), "
+                             "or only the Qwen3-Omni code2wav leg (prints its JSON)")
     parser.add_argument("--launches", type=int, default=2)
     parser.add_argument("--no-other-configs", action="store_true",
                         help="skip the xRT of the other configurations and the peak calibration")
@@ -469,6 +471,9 @@ def main() -> None:
         sys.exit(1)
     device = torch.device("cuda", 0)
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.only == "qwen3_code2wav":
+        print(json.dumps(bench_qwen3_code2wav(device)), flush=True)
+        return
     if args.only:
         run_only(args, device)
         return
