@@ -252,7 +252,7 @@ def run_only(args, device) -> None:
         final = FinalConv(decoder.final_weight, decoder.final_bias, N.ACT_TANH, wave)
         last = blk.units[-1]
         fn = lambda: residual_stack(x, blk.stack, None, last.next_a, last.next_b,  # noqa: E731
-                                    final=final)
+                                    final=final, coef_table=blk.stack_coef)
         what = "residual stack + final conv, 96 channels, x [64, 23040, 96]"
     for _ in range(2):
         fn()

@@ -96,7 +96,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 4: omni_residual_stack's fused final conv */
+int omni_codec_abi_version(void); /* 5: omni_residual_stack's coefficient table */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -277,7 +277,18 @@ typedef struct omni_residual_stack_args {
   int64_t final_hist_slot_stride;
   float* final_out; /* float32, element (b, i) at b * final_out_stride_b + i */
   int64_t final_out_stride_b;
+  /* ABI version 5: the per-channel coefficient rows the launch would otherwise compute in every
+     workgroup, precomputed by omni_residual_stack_coefficients for these units (16-byte
+     aligned), or NULL */
+  const float* coef_table;
 } omni_residual_stack_args;
+
+/* Fills table[(num_units * 8 + 2) * channels] (float32, device, 16-byte aligned) with the
+   coefficient rows of a's units and output Snake (a's weights, activations and scales; its
+   activations / histories / outputs are not read). Call once per set of weights; pass the table
+   as coef_table to every omni_residual_stack call with those weights. */
+int omni_residual_stack_coefficients(const omni_residual_stack_args* a, float* table,
+                                     int64_t table_floats, omni_stream_t stream);
 
 int omni_residual_stack(const omni_residual_stack_args* args, omni_stream_t stream);
 

@@ -83,6 +83,7 @@ struct StackParams {
   uint32_t fin_hist_bytes;
   float* fin_out;
   int64_t fin_o_sb;
+  const float* coef_table;  // the coefficient rows below, precomputed (stack_coef), or NULL
   int H;              // staged rows ahead of each segment (sum of the unit halos and the
                       // final conv's taps - 1)
   int seg_len;        // long rows: output positions per tile; short rows: the row length
@@ -94,6 +95,38 @@ struct StackParams {
 template <int UROWS>
 __device__ __forceinline__ int uaddr(int kc, int row, int slot) {
   return (kc * UROWS + row) * kChunk + ((slot ^ ((row >> 2) & 3)) << 3);
+}
+
+// The per-launch coefficient rows in LDS order: per unit kCoefRows rows of C (scale1, bias1,
+// mid Snake a in revolutions, b, scale2, bias2, the next operand's Snake a in revolutions, b),
+// then unit 0's input Snake (a in revolutions, b). Entry e of the table.
+enum { kS1, kB1, kMA, kMB, kS2, kB2, kNA, kNB };
+
+__device__ __forceinline__ float stack_coef(const StackParams& p, int e, int C) {
+  const int k = e / C;
+  const int n = e - k * C;
+  if (k >= p.nunits * kCoefRows)
+    return k == p.nunits * kCoefRows ? p.unit[0].in_a[n] * kInvTwoPi : p.unit[0].in_b[n];
+  const int unit = k / kCoefRows;
+  const int row = k - unit * kCoefRows;
+  const StackUnit& U = p.unit[unit];
+  const bool last = unit + 1 == p.nunits;
+  switch (row) {
+    case kS1: return U.w1_scale ? U.w1_scale[n] : 1.f;
+    case kB1: return U.b1 ? U.b1[n] : 0.f;
+    case kMA: return U.mid_a[n] * kInvTwoPi;
+    case kMB: return U.mid_b[n];
+    case kS2: return U.w2_scale ? U.w2_scale[n] : 1.f;
+    case kB2: return U.b2 ? U.b2[n] : 0.f;
+    case kNA: return (last ? p.out_a[n] : p.unit[unit + 1].in_a[n]) * kInvTwoPi;
+    default: return last ? p.out_b[n] : p.unit[unit + 1].in_b[n];
+  }
+}
+
+template <int C>
+__global__ void stack_coef_kernel(const StackParams p, float* table) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < (p.nunits * kCoefRows + 2) * C) table[e] = stack_coef(p, e, C);
 }
 
 template <int C, int WCO, int WP, int TP, bool DMA = false>
@@ -140,10 +173,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   u16* us = lds;                        // operand / h tile
   u16* ws = lds + CH * UROWS * kChunk;  // weights
   float* coef = reinterpret_cast<float*>(ws + Tile::W_ELEMS);
-  // per unit: scale1, bias1, mid Snake (a in revolutions, b), scale2, bias2, the next operand's
-  // Snake (a in revolutions, b)
-  enum { kS1, kB1, kMA, kMB, kS2, kB2, kNA, kNB };
-  float* in0 = coef + kMaxUnits * kCoefRows * C;  // unit 0's input Snake a, b
+  float* in0 = coef + p.nunits * kCoefRows * C;  // unit 0's input Snake a, b
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -198,30 +228,13 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       }
     }
   }
-  for (int e = tid; e < (p.nunits * kCoefRows + 2) * C; e += NT) {
-    const int k = e / C;
-    const int n = e - k * C;
-    float v;
-    if (k >= p.nunits * kCoefRows) {
-      v = k == p.nunits * kCoefRows ? p.unit[0].in_a[n] * kInvTwoPi : p.unit[0].in_b[n];
-      in0[(k - p.nunits * kCoefRows) * C + n] = v;
-      continue;
-    }
-    const int unit = k / kCoefRows;
-    const int row = k - unit * kCoefRows;
-    const StackUnit& U = p.unit[unit];
-    const bool last = unit + 1 == p.nunits;
-    switch (row) {
-      case kS1: v = U.w1_scale ? U.w1_scale[n] : 1.f; break;
-      case kB1: v = U.b1 ? U.b1[n] : 0.f; break;
-      case kMA: v = U.mid_a[n] * kInvTwoPi; break;
-      case kMB: v = U.mid_b[n]; break;
-      case kS2: v = U.w2_scale ? U.w2_scale[n] : 1.f; break;
-      case kB2: v = U.b2 ? U.b2[n] : 0.f; break;
-      case kNA: v = (last ? p.out_a[n] : p.unit[unit + 1].in_a[n]) * kInvTwoPi; break;
-      default: v = last ? p.out_b[n] : p.unit[unit + 1].in_b[n]; break;
-    }
-    coef[unit * kCoefRows * C + row * C + n] = v;
+  const int ncoef = (p.nunits * kCoefRows + 2) * C;
+  if (p.coef_table != nullptr) {
+    // a straight copy of the precomputed rows: independent 16-byte loads, in flight with x's
+    for (int e = tid * 4; e < ncoef; e += NT * 4)
+      *reinterpret_cast<f32x4*>(coef + e) = *reinterpret_cast<const f32x4*>(p.coef_table + e);
+  } else {
+    for (int e = tid; e < ncoef; e += NT) coef[e] = stack_coef(p, e, C);
   }
   for (int e = tid; e < CH * kGuard * 4; e += NT) {
     const int kc = e / (kGuard * 4);

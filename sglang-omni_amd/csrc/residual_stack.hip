@@ -5,7 +5,50 @@ namespace {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
+// The arrays the coefficient rows come from (omni_stack::stack_coef).
+void coef_sources(const omni_residual_stack_args* a, bool fp8, omni_stack::StackParams& p) {
+  p.nunits = a->num_units;
+  for (int k = 0; k < a->num_units; ++k) {
+    const omni_residual_unit& u = a->units[k];
+    omni_stack::StackUnit& s = p.unit[k];
+    s.w1_scale = fp8 ? u.weight1_scale : nullptr;
+    s.b1 = u.bias1;
+    s.in_a = u.in_act_a;
+    s.in_b = u.in_act_b;
+    s.mid_a = u.mid_act_a;
+    s.mid_b = u.mid_act_b;
+    s.w2_scale = fp8 ? u.weight2_scale : nullptr;
+    s.b2 = u.bias2;
+  }
+  p.out_a = a->out_act_a;
+  p.out_b = a->out_act_b;
+}
+
 }  // namespace
+
+extern "C" int omni_residual_stack_coefficients(const omni_residual_stack_args* a, float* table,
+                                                int64_t table_floats, omni_stream_t stream) {
+  using namespace omni_stack;
+  if (!a || !table || !a->out_act_a || !a->out_act_b) return OMNI_ERR_INVALID_ARG;
+  if (a->num_units < 1 || a->num_units > kMaxUnits) return OMNI_ERR_INVALID_ARG;
+  if (a->channels != 96) return OMNI_ERR_UNSUPPORTED;
+  if (a->weight_dtype != OMNI_DTYPE_BF16 && a->weight_dtype != OMNI_DTYPE_FP8_E4M3)
+    return OMNI_ERR_INVALID_ARG;
+  const bool fp8 = a->weight_dtype == OMNI_DTYPE_FP8_E4M3;
+  for (int k = 0; k < a->num_units; ++k) {
+    const omni_residual_unit& u = a->units[k];
+    if (!u.in_act_a || !u.in_act_b || !u.mid_act_a || !u.mid_act_b) return OMNI_ERR_INVALID_ARG;
+    if (fp8 && (!u.weight1_scale || !u.weight2_scale)) return OMNI_ERR_INVALID_ARG;
+  }
+  const int n = (a->num_units * kCoefRows + 2) * 96;
+  if (table_floats != n || !aligned16(table)) return OMNI_ERR_INVALID_ARG;
+  StackParams p{};
+  coef_sources(a, fp8, p);
+  hipLaunchKernelGGL(stack_coef_kernel<96>, dim3((n + 255) / 256), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p, table);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
 
 extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_stream_t stream) {
   using namespace omni_stack;
@@ -37,6 +80,7 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
          a->final_hist_slot_stride < 2 * (a->final_taps - 1) * C || a->final_hist_slot_stride % 8))
       return OMNI_ERR_INVALID_ARG;
   }
+  if (a->coef_table && !aligned16(a->coef_table)) return OMNI_ERR_INVALID_ARG;
   if (a->x_out && (!aligned16(a->x_out) || a->x_out_stride_t < C || a->x_out_stride_t % 4 ||
                    a->x_out_stride_b % 4))
     return OMNI_ERR_INVALID_ARG;
@@ -131,6 +175,7 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   p.o_bytes = (uint32_t)o_bytes;
   p.xo_bytes = (uint32_t)xo_bytes;
   p.H = (int)H;
+  p.coef_table = a->coef_table;
   if (fin) {
     p.fin_w = a->final_weight;
     p.fin_b = a->final_bias;

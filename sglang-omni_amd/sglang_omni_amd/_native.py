@@ -155,6 +155,7 @@ class ResidualStackArgs(ctypes.Structure):
         ("final_hist_slot_stride", ctypes.c_int64),
         ("final_out", ctypes.c_void_p),
         ("final_out_stride_b", ctypes.c_int64),
+        ("coef_table", ctypes.c_void_p),
     ]
 
 
@@ -172,6 +173,7 @@ SIGNATURES: dict[str, list] = {
                             _PTR, _INT, _I64, _I64, _I64, _INT, _PTR],
     "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
     "omni_residual_stack": [ctypes.POINTER(ResidualStackArgs), _PTR],
+    "omni_residual_stack_coefficients": [ctypes.POINTER(ResidualStackArgs), _PTR, _I64, _PTR],
     "omni_single_output_conv": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _PTR, _PTR,
                                 _PTR, _PTR, _I64, _I64, _PTR, _PTR, _PTR, _I64, _I64, _INT, _INT,
                                 _PTR, _INT, _I64, _PTR],

@@ -305,6 +305,7 @@ def residual_stack(
     slot_parity: torch.Tensor | None = None,
     history_cold: bool = False,
     final: FinalConv | None = None,
+    coef_table: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Launch ``omni_residual_stack``: every unit in turn over x [B, L, C] float32, then
     out = Snake(out_a, out_b)(x_last) as bf16 [B, L, C] (and x_last into x_out, float32).
@@ -393,7 +394,39 @@ def residual_stack(
     if x_out is not None:
         args.x_out = x_out.data_ptr()
         args.x_out_stride_b, args.x_out_stride_t = x_out.stride(0), x_out.stride(1)
+    if coef_table is not None:
+        if coef_table.dtype != torch.float32 or coef_table.numel() != (8 * len(units) + 2) * channels:
+            raise ValueError("coef_table must be stack_coefficients(...) of these units")
+        args.coef_table = coef_table.data_ptr()
     lib = N.load_library()
     N.check(lib.omni_residual_stack(ctypes.byref(args), N.stream_handle(x.device)),
             "omni_residual_stack")
     return final.out if final is not None else out
+
+
+def stack_coefficients(units: list[ResidualUnitWeights], out_a: torch.Tensor,
+                       out_b: torch.Tensor) -> torch.Tensor:
+    """The coefficient rows ``residual_stack`` launches over these units and output Snake read
+    (``omni_residual_stack_coefficients``): computed once, passed as ``coef_table`` to every
+    launch with the same weights."""
+    channels = units[0].conv1.c_out
+    N.require_device(out_a, out_b)
+    args = N.ResidualStackArgs()
+    args.channels = channels
+    args.weight_dtype = N.omni_dtype(units[0].conv1.weight.dtype)
+    args.num_units = len(units)
+    for k, u in enumerate(units):
+        a = args.units[k]
+        a.weight1_scale = N.ptr(u.conv1.scale)
+        a.bias1 = N.ptr(u.conv1.bias)
+        a.in_act_a, a.in_act_b = u.in_a.data_ptr(), u.in_b.data_ptr()
+        a.mid_act_a, a.mid_act_b = u.mid_a.data_ptr(), u.mid_b.data_ptr()
+        a.weight2_scale = N.ptr(u.conv2.scale)
+        a.bias2 = N.ptr(u.conv2.bias)
+    args.out_act_a, args.out_act_b = out_a.data_ptr(), out_b.data_ptr()
+    table = torch.empty((8 * len(units) + 2) * channels, dtype=torch.float32, device=out_a.device)
+    lib = N.load_library()
+    N.check(lib.omni_residual_stack_coefficients(ctypes.byref(args), table.data_ptr(),
+                                                 table.numel(), N.stream_handle(out_a.device)),
+            "omni_residual_stack_coefficients")
+    return table

@@ -50,6 +50,7 @@ from ..kernels.conv import (
     pack_conv1d,
     pack_conv_transpose1d,
     residual_stack,
+    stack_coefficients,
 )
 from ..kernels.rvq import rvq_gather_sum
 from ..kernels.single_output_conv import single_output_conv
@@ -84,6 +85,7 @@ class _Block:
     stride: int
     c_out: int
     stack: list[ResidualUnitWeights] | None = None  # the units as one residual-stack launch
+    stack_coef: torch.Tensor | None = None  # their coefficient rows (computed once)
 
 
 # channel counts the fused residual-unit kernel handles (one column tile holds every channel)
@@ -239,6 +241,9 @@ class DacCodecDecoder:
                 ins = [(up.out_a, up.out_b)] + [(u.next_a, u.next_b) for u in units[:-1]]
                 blk.stack = [ResidualUnitWeights(u.conv1.conv, u.conv2, a, b, u.mid_a, u.mid_b)
                              for u, (a, b) in zip(units, ins)]
+                if self.device.type == "cuda":
+                    blk.stack_coef = stack_coefficients(blk.stack, units[-1].next_a,
+                                                        units[-1].next_b)
             self.blocks.append(blk)
         fw = ref["final"]["conv"]["weight"]  # [1, C, k]
         self.final_weight = fw[0].t().contiguous().float().to(dev)  # [k, C]
@@ -373,10 +378,11 @@ class DacCodecDecoder:
                     flops += 2.0 * batch * length * self.final_taps * self.final_channels
                     with timer.launch(f"stack{c}", flops, f"blocks.{bi}.units+final"):
                         wave = residual_stack(x, blk.stack, None, last.next_a, last.next_b,
-                                              final=final, **h)
+                                              final=final, coef_table=blk.stack_coef, **h)
                     return self._finish_step(wave, state, batch)
                 with timer.launch(f"stack{c}", flops, f"blocks.{bi}.units"):
-                    residual_stack(x, blk.stack, u_next, last.next_a, last.next_b, **h)
+                    residual_stack(x, blk.stack, u_next, last.next_a, last.next_b,
+                                   coef_table=blk.stack_coef, **h)
                 cur = 1 - cur
                 u = u_next
                 continue

@@ -18,6 +18,7 @@ from sglang_omni_amd.kernels.conv import (
     fused_conv,
     pack_conv1d,
     residual_stack,
+    stack_coefficients,
 )
 from sglang_omni_amd.kernels.single_output_conv import single_output_conv
 
@@ -192,3 +193,25 @@ def test_residual_stack_final_conv_streams_through_its_slot_history(gpu, splits)
         parts.append(wave)
         start += size
     assert torch.equal(torch.cat(parts, dim=-1), whole)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("dilations", [(1, 3, 9), (4,)])
+def test_residual_stack_precomputed_coefficients_give_the_same_bits(gpu, fp8, dilations):
+    """The coefficient rows computed once (omni_residual_stack_coefficients) and passed as
+    coef_table give exactly the launch that computes them per workgroup."""
+    units, out_a, out_b = make_units(dilations, gpu, fp8=fp8, seed=11)
+    table = stack_coefficients(units, out_a, out_b)
+    assert table.numel() == (8 * len(units) + 2) * C
+    gen = torch.Generator().manual_seed(5)
+    x = (torch.randn(3, 700, C, generator=gen) * 0.5).to(gpu)
+    outs = []
+    for coef in (None, table):
+        out = torch.empty(3, 700, C, dtype=torch.bfloat16, device=gpu)
+        x_out = torch.empty_like(x)
+        residual_stack(x, units, out, out_a, out_b, x_out=x_out, coef_table=coef)
+        outs.append((out, x_out))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    with pytest.raises(ValueError):
+        residual_stack(x, units, torch.empty_like(outs[0][0]), out_a, out_b,
+                       coef_table=table[:-1])
