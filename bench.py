@@ -19,6 +19,8 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
   hift_transforms  HiFT's source spectrum and fused iSTFT tail at the HiFiGAN size, in HBM GB/s;
   qwen3_code2wav the Qwen3-Omni code2wav (pre-transformer + ConvNeXt + decoder) streaming 64
                 streams x 12-frame chunks, eager and HIP-graph replayed, per-kind kernel times;
+  qwen3_tts_codec the Qwen3-TTS tokenizer decoder through decode(codes, state), 64 rows x 12
+                frames per decode;
   egress        one step's waveform leaving the device: the PCM16 egress kernel (HBM GB/s) and
                 the staging of the step through a pinned slot to host arrays (PCIe-inclusive);
   calibration   the box's practical peaks: a 1 GiB copy and a bf16 8192^3 GEMM.
@@ -367,6 +369,37 @@ def bench_qwen3_code2wav(device, steps: int = 20, warmup: int = 3) -> dict:
     return out
 
 
+def bench_qwen3_tts(device, steps: int = 20, warmup: int = 3) -> dict:
+    """The Qwen3-TTS tokenizer decoder (512-hidden 8-layer transformer with 16 x 64 attention,
+    1024 latent, 1536-channel decoder, x1920; seeded random weights) through its incremental
+    API: one state of 64 rows, each decode 12 fresh frames of every row."""
+    from sglang_omni_amd.models import Qwen3TTSCodecDecoder, make_qwen3_code2wav_weights
+    from sglang_omni_amd.models.configs import QWEN3_TTS_CODEC, qwen3_code2wav_macs_per_frame
+
+    cfg = QWEN3_TTS_CODEC
+    dec = Qwen3TTSCodecDecoder(make_qwen3_code2wav_weights(cfg, seed=0), cfg, device=device)
+    codes = torch.randint(0, cfg.codebook_size,
+                          (STREAMS, cfg.num_quantizers, CHUNK_FRAMES * CHUNKS_PER_STREAM),
+                          generator=torch.Generator().manual_seed(1))
+    chunks = [codes[..., c * CHUNK_FRAMES:(c + 1) * CHUNK_FRAMES].contiguous().to(device)
+              for c in range(CHUNKS_PER_STREAM)]
+    state = {"s": dec.init_state(STREAMS)}
+
+    def step(i: int) -> None:
+        c = i % CHUNKS_PER_STREAM
+        if c == 0:
+            state["s"] = dec.init_state(STREAMS)
+        dec.decode(chunks[c], state["s"])
+
+    dt = timed_steps(step, steps, warmup) / steps
+    audio_per_step = STREAMS * CHUNK_FRAMES * cfg.hop_length / cfg.sample_rate
+    flops = 2.0 * qwen3_code2wav_macs_per_frame(cfg) * STREAMS * CHUNK_FRAMES
+    return {"workload": f"Qwen3-TTS tokenizer decoder, decode(codes, state) of {STREAMS} rows x "
+                        f"{CHUNK_FRAMES} frames, bf16",
+            "ms_per_step": round(dt * 1e3, 3), "xRT": round(audio_per_step / dt, 1),
+            "TFLOPs": round(flops / dt / 1e12, 1)}
+
+
 def bench_hift_transforms(device) -> dict:
     """HiFT's transforms at the HiFiGAN configuration's size (16 rows x 10 s at 24 kHz, n_fft 16,
     hop 4): the source spectrum (240 000 samples -> 18 x 60 001) and the fused iSTFT tail
@@ -507,6 +540,7 @@ def main() -> None:
         line["hift_transforms"] = bench_hift_transforms(device)
         line["egress"] = bench_egress(device)
         line["qwen3_code2wav"] = bench_qwen3_code2wav(device)
+        line["qwen3_tts_codec"] = bench_qwen3_tts(device)
         line["calibration"] = calibrate(device)
     print(json.dumps(line), flush=True)
 

@@ -21,6 +21,11 @@ Parity pins (``tests/test_qwen3_code2wav_oracle.py``):
   full causal attention when the window covers the input;
 * ``apply_rope`` against the complex-rotation form of rotary embeddings (pairs (i, i + d/2));
 * ``first_decode_samples`` against the length of the transformers module's output.
+* ``qwen3_tts_decode`` (the Qwen3-TTS tokenizer decoder; its module, ``qwen_tts``, is not
+  installed, so the composition is parity unpinned beyond its pieces): its transformer with
+  identity input / output projections equals ``code2wav_transformer``; ``split_rvq_decode``
+  against a per-frame loop; right-trimmed transposed convs against the reference test's own
+  module form (tests/unit_test/qwen3_tts/test_incremental_codec.py:93-110); T * hop samples.
 
 The reference's streaming semantics (sglang_omni/models/qwen3_omni/components/
 incremental_codec.py:109-200: a stream decoded in any split of chunks gives the whole decode's
@@ -83,7 +88,7 @@ def transformer_layer(h: torch.Tensor, w: dict[str, torch.Tensor], prefix: str, 
     b, t, c = h.shape
     heads = cfg.num_attention_heads
     kv_heads = cfg.num_key_value_heads
-    hd = c // heads
+    hd = getattr(cfg, "head_dim", c // heads)
     eps = cfg.rms_norm_eps
     x = rms_norm(h, w[f"{prefix}.input_layernorm.weight"], eps)
     q = F.linear(x, w[f"{prefix}.self_attn.q_proj.weight"].float()).view(b, t, heads, hd)
@@ -96,7 +101,8 @@ def transformer_layer(h: torch.Tensor, w: dict[str, torch.Tensor], prefix: str, 
         k = k.repeat_interleave(heads // kv_heads, dim=1)
         v = v.repeat_interleave(heads // kv_heads, dim=1)
     a = window_attention(q, k, v, cfg.sliding_window, hd ** -0.5)
-    a = F.linear(a.transpose(1, 2).reshape(b, t, c), w[f"{prefix}.self_attn.o_proj.weight"].float())
+    a = F.linear(a.transpose(1, 2).reshape(b, t, heads * hd),
+                 w[f"{prefix}.self_attn.o_proj.weight"].float())
     h = h + w[f"{prefix}.self_attn_layer_scale.scale"].float() * a
     x = rms_norm(h, w[f"{prefix}.post_attention_layernorm.weight"], eps)
     gate = F.linear(x, w[f"{prefix}.mlp.gate_proj.weight"].float())
@@ -107,7 +113,7 @@ def transformer_layer(h: torch.Tensor, w: dict[str, torch.Tensor], prefix: str, 
 
 def code2wav_transformer(h: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
     """The pre-transformer on inputs_embeds [B, T, C] at positions 0..T-1 (TF :3484-3539)."""
-    hd = cfg.hidden_size // cfg.num_attention_heads
+    hd = getattr(cfg, "head_dim", cfg.hidden_size // cfg.num_attention_heads)
     cos, sin = rope_cos_sin(torch.arange(h.shape[1]), hd, cfg.rope_theta)
     for i in range(cfg.num_hidden_layers):
         h = transformer_layer(h, w, f"pre_transformer.layers.{i}", cfg, cos, sin)
@@ -125,11 +131,14 @@ def causal_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None
 
 
 def causal_trans_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
-                      stride: int) -> torch.Tensor:
+                      stride: int, trim: str = "both") -> torch.Tensor:
     """Qwen3OmniMoeCausalTransConvNet (TF :3216-3228): ConvTranspose1d, then k - s samples
-    trimmed on both sides."""
+    trimmed on both sides; with trim "right" the Qwen3-TTS tokenizer's form, k - s trimmed on the
+    right only (right_pad, qwen3_tts/incremental_codec.py:191-237 emits T * s samples)."""
     y = F.conv_transpose1d(x.float(), weight.float(), bias.float(), stride=stride)
     pad = weight.shape[-1] - stride
+    if trim == "right":
+        return y[..., :y.shape[-1] - pad]
     return y[..., pad:y.shape[-1] - pad]
 
 
@@ -160,16 +169,17 @@ def code2wav_conv_stack(h: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -
     upsamplers, the decoder blocks (SnakeBeta -> causal transposed conv -> residual units of
     SnakeBeta -> conv k7 dilation 1/3/9 -> SnakeBeta -> conv k1, + input), the final SnakeBeta
     -> conv to one channel, clamp to [-1, 1]. Returns [B, 1, samples]."""
+    trim = getattr(cfg, "transconv_trim", "both")
     x = h.float().transpose(1, 2)
     for i, factor in enumerate(cfg.upsampling_ratios):
         x = causal_trans_conv(x, w[f"upsample.{i}.0.conv.weight"], w[f"upsample.{i}.0.conv.bias"],
-                              factor)
+                              factor, trim)
         x = convnext_block(x, w, f"upsample.{i}.1")
     x = causal_conv(x, w["decoder.0.conv.weight"], w["decoder.0.conv.bias"])
     for bi, rate in enumerate(cfg.upsample_rates, start=1):
         p = f"decoder.{bi}.block"
         x = snake_beta(x, w[f"{p}.0.alpha"], w[f"{p}.0.beta"])
-        x = causal_trans_conv(x, w[f"{p}.1.conv.weight"], w[f"{p}.1.conv.bias"], rate)
+        x = causal_trans_conv(x, w[f"{p}.1.conv.weight"], w[f"{p}.1.conv.bias"], rate, trim)
         for u, d in enumerate((1, 3, 9)):
             q = f"{p}.{u + 2}"
             y = snake_beta(x, w[f"{q}.act1.alpha"], w[f"{q}.act1.beta"])
@@ -194,6 +204,40 @@ def qwen3_code2wav(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) ->
     if codes.shape[1] != cfg.num_quantizers:
         raise ValueError(f"Expected {cfg.num_quantizers} layer of codes, got {codes.shape[1]}")
     h = code2wav_transformer(code_embedding_mean(codes, w, cfg), w, cfg)
+    return code2wav_conv_stack(h, w, cfg)
+
+
+def split_rvq_decode(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
+    """The Qwen3-TTS split quantizer's dequantize as this build lays it out: the semantic
+    codebooks' embeddings summed and projected, plus the acoustic codebooks' summed and
+    projected (each group W_g sum_k E_k[code_k]). [B, Q, T] -> [B, T, latent], float64."""
+    books = w["quantizer.codebooks"].double()
+    s = cfg.semantic_quantizers
+    groups = ((range(0, s), w["quantizer.semantic_proj.weight"]),
+              (range(s, cfg.num_quantizers), w["quantizer.acoustic_proj.weight"]))
+    out = 0
+    for ks, proj in groups:
+        summed = sum(books[k][codes[:, k].clamp(max=cfg.codebook_size - 1)] for k in ks)
+        out = out + summed @ proj.double().t()
+    return out
+
+
+def qwen3_tts_decode(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
+    """The Qwen3-TTS tokenizer decoder's whole-stream decode as the reference's incremental
+    decoder composes it (qwen3_tts/incremental_codec.py:1136-1276): split RVQ -> causal pre_conv
+    -> input_proj -> pre-transformer layers -> RMSNorm -> output_proj -> the conv stack with
+    right-trimmed transposed convs -> clamp. [B, Q, T] -> [B, 1, T * hop]."""
+    z = split_rvq_decode(codes, w, cfg).float().transpose(1, 2)
+    z = causal_conv(z, w["pre_conv.conv.weight"], w["pre_conv.conv.bias"]).transpose(1, 2)
+    h = F.linear(z, w["pre_transformer.input_proj.weight"].float(),
+                 w["pre_transformer.input_proj.bias"].float())
+    hd = cfg.head_dim
+    cos, sin = rope_cos_sin(torch.arange(h.shape[1]), hd, cfg.rope_theta)
+    for i in range(cfg.num_hidden_layers):
+        h = transformer_layer(h, w, f"pre_transformer.layers.{i}", cfg, cos, sin)
+    h = rms_norm(h, w["pre_transformer.norm.weight"], cfg.rms_norm_eps)
+    h = F.linear(h, w["pre_transformer.output_proj.weight"].float(),
+                 w["pre_transformer.output_proj.bias"].float())
     return code2wav_conv_stack(h, w, cfg)
 
 

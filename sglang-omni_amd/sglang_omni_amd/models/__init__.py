@@ -5,9 +5,11 @@ from .configs import (
     CODEC_24K_LONG,
     HIFIGAN_24K,
     QWEN3_CODE2WAV,
+    QWEN3_TTS_CODEC,
     DacDecoderConfig,
     HifiGanConfig,
     Qwen3Code2WavConfig,
+    Qwen3TTSCodecConfig,
     make_dac_weights,
     make_hifigan_weights,
     make_qwen3_code2wav_weights,
@@ -15,13 +17,19 @@ from .configs import (
 from .dac_codec import CodecStatePool, DacCodecDecoder
 from .graph_runner import CodecGraphRunner, GraphKey
 from .hifigan import HifiGanVocoder
-from .qwen3_code2wav import Code2WavStatePool, Qwen3Code2WavDecoder
+from .qwen3_code2wav import (
+    Code2WavStatePool,
+    Qwen3Code2WavDecoder,
+    Qwen3TTSCodecDecoder,
+    Qwen3TTSCodecState,
+)
 
 __all__ = [
     "CODEC_24K",
     "CODEC_24K_LONG",
     "HIFIGAN_24K",
     "QWEN3_CODE2WAV",
+    "QWEN3_TTS_CODEC",
     "Code2WavStatePool",
     "CodecGraphRunner",
     "CodecStatePool",
@@ -32,6 +40,9 @@ __all__ = [
     "HifiGanVocoder",
     "Qwen3Code2WavConfig",
     "Qwen3Code2WavDecoder",
+    "Qwen3TTSCodecConfig",
+    "Qwen3TTSCodecDecoder",
+    "Qwen3TTSCodecState",
     "make_dac_weights",
     "make_hifigan_weights",
     "make_qwen3_code2wav_weights",

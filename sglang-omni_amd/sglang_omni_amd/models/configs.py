@@ -129,12 +129,69 @@ class Qwen3Code2WavConfig:
         return [self.decoder_dim // 2**i for i in range(len(self.upsample_rates) + 1)]
 
 
+@dataclass(frozen=True)
+class Qwen3TTSCodecConfig:
+    """Qwen3-TTS tokenizer (12 Hz) decoder, as the reference's Qwen3TTSIncrementalDecoder walks
+    it (sglang_omni/models/qwen3_tts/incremental_codec.py:771-1276): split RVQ dequantize
+    (semantic codebooks and acoustic codebooks, each group summed and projected to latent_dim)
+    -> causal pre_conv -> input_proj -> sliding-window pre-transformer (heads * head_dim wide
+    attention) -> RMSNorm -> output_proj -> ConvNeXt upsamplers (x2, x2) at latent_dim -> the
+    causal decoder blocks of Qwen3-Omni's code2wav with transposed convs trimmed on the right
+    only (every decode emits frames * 1920 samples) -> SnakeBeta -> conv to one channel ->
+    clamp. The transformer sizes are those of the reference's own test of the decoder
+    transformer (tests/unit_test/qwen3_tts/test_incremental_codec.py:461-469); the quantizer's
+    codebook_dim and the layer count are this build's defaults."""
+
+    codebook_size: int = 2048
+    num_quantizers: int = 16
+    semantic_quantizers: int = 1
+    codebook_dim: int = 512
+    latent_dim: int = 1024
+    hidden_size: int = 512
+    num_hidden_layers: int = 8
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 16
+    head_dim: int = 64
+    intermediate_size: int = 1024
+    sliding_window: int = 72
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    layer_scale_initial_scale: float = 0.01
+    pre_conv_kernel: int = 3
+    decoder_dim: int = 1536
+    upsample_rates: tuple[int, ...] = (8, 5, 4, 3)
+    upsampling_ratios: tuple[int, ...] = (2, 2)
+    sample_rate: int = 24000
+    kernel_size: int = 7
+    dilations: tuple[int, ...] = (1, 3, 9)
+    transconv_trim: str = "right"
+    final_activation: str = "clamp"
+    conv_gain: float = 0.85
+    input_conv_gain: float = 0.08
+
+    @property
+    def hop_length(self) -> int:
+        return int(math.prod(self.upsample_rates) * math.prod(self.upsampling_ratios))
+
+    @property
+    def channels(self) -> int:
+        return self.decoder_dim
+
+    @property
+    def rates(self) -> tuple[int, ...]:
+        return self.upsample_rates
+
+    def stage_channels(self) -> list[int]:
+        return [self.decoder_dim // 2**i for i in range(len(self.upsample_rates) + 1)]
+
+
 # The workloads' architectures.
 SINGLE_BLOCK = dict(n_codebooks=8, codebook_size=1024, latent_dim=256)  # RVQ + one conv block
 CODEC_24K = DacDecoderConfig()  # 16 x 2048 x 512 tables, 1536 ch, x1920 to 24 kHz
 CODEC_24K_LONG = DacDecoderConfig(n_codebooks=32, codebook_size=1024)  # fp8-weight long form
 HIFIGAN_24K = HifiGanConfig()
 QWEN3_CODE2WAV = Qwen3Code2WavConfig()
+QWEN3_TTS_CODEC = Qwen3TTSCodecConfig()
 
 
 def _kaiming(shape: tuple[int, ...], fan_in: int, gain: float, gen: torch.Generator) -> torch.Tensor:
@@ -199,33 +256,53 @@ def make_dac_weights(config: DacDecoderConfig, seed: int = 0) -> dict[str, Any]:
     return weights
 
 
-def make_qwen3_code2wav_weights(config: Qwen3Code2WavConfig, seed: int = 0, *,
+def make_qwen3_code2wav_weights(config: Qwen3Code2WavConfig | Qwen3TTSCodecConfig,
+                                seed: int = 0, *,
                                 branch_scale: float | None = None,
                                 activation_spread: float = 0.0) -> dict[str, torch.Tensor]:
     """Seeded float32 weights under ``Qwen3OmniMoeCode2Wav.state_dict()`` names (a checkpoint's
-    code2wav weights load the same way). Linear and conv weights kaiming-normal (fan_in), biases
+    code2wav weights load the same way); for a Qwen3TTSCodecConfig also the split quantizer
+    (``quantizer.codebooks`` [K, V, codebook_dim], ``quantizer.semantic_proj`` /
+    ``acoustic_proj`` [latent, codebook_dim]), ``pre_conv`` and the transformer's
+    ``input_proj`` / ``output_proj``. Linear and conv weights kaiming-normal (fan_in), biases
     zero, norms one. ``branch_scale`` replaces the layer scales (default 0.01) and ConvNeXt
     gammas (default 1e-6) so the transformer and ConvNeXt branches matter to the output;
     ``activation_spread`` draws the SnakeBeta log-parameters from N(0, spread) instead of 0."""
     gen = torch.Generator().manual_seed(seed)
     c, inter = config.hidden_size, config.intermediate_size
     kv = config.num_key_value_heads * config.head_dim
+    qw = config.num_attention_heads * config.head_dim
+    latent = getattr(config, "latent_dim", c)
+    tts = hasattr(config, "semantic_quantizers")
 
     def lin(out_f: int, in_f: int, gain: float = 1.0) -> torch.Tensor:
         return _kaiming((out_f, in_f), in_f, gain, gen)
 
     layer_scale = config.layer_scale_initial_scale if branch_scale is None else branch_scale
     gamma = 1e-6 if branch_scale is None else branch_scale
-    w: dict[str, torch.Tensor] = {
-        "code_embedding.weight": torch.randn(config.num_quantizers * config.codebook_size, c,
-                                             generator=gen),
-    }
+    w: dict[str, torch.Tensor] = {}
+    if tts:
+        dq = config.codebook_dim
+        w["quantizer.codebooks"] = torch.randn(config.num_quantizers, config.codebook_size, dq,
+                                               generator=gen)
+        w["quantizer.semantic_proj.weight"] = lin(latent, dq)
+        w["quantizer.acoustic_proj.weight"] = lin(latent, dq)
+        k = config.pre_conv_kernel
+        w["pre_conv.conv.weight"] = _kaiming((latent, latent, k), latent * k, 1.0, gen)
+        w["pre_conv.conv.bias"] = torch.zeros(latent)
+        w["pre_transformer.input_proj.weight"] = lin(c, latent)
+        w["pre_transformer.input_proj.bias"] = torch.zeros(c)
+        w["pre_transformer.output_proj.weight"] = lin(latent, c)
+        w["pre_transformer.output_proj.bias"] = torch.zeros(latent)
+    else:
+        w["code_embedding.weight"] = torch.randn(config.num_quantizers * config.codebook_size, c,
+                                                 generator=gen)
     for i in range(config.num_hidden_layers):
         p = f"pre_transformer.layers.{i}"
-        w[f"{p}.self_attn.q_proj.weight"] = lin(c, c)
+        w[f"{p}.self_attn.q_proj.weight"] = lin(qw, c)
         w[f"{p}.self_attn.k_proj.weight"] = lin(kv, c)
         w[f"{p}.self_attn.v_proj.weight"] = lin(kv, c)
-        w[f"{p}.self_attn.o_proj.weight"] = lin(c, c)
+        w[f"{p}.self_attn.o_proj.weight"] = lin(c, qw)
         w[f"{p}.mlp.gate_proj.weight"] = lin(inter, c)
         w[f"{p}.mlp.up_proj.weight"] = lin(inter, c)
         w[f"{p}.mlp.down_proj.weight"] = lin(c, inter)
@@ -234,19 +311,20 @@ def make_qwen3_code2wav_weights(config: Qwen3Code2WavConfig, seed: int = 0, *,
         w[f"{p}.self_attn_layer_scale.scale"] = torch.full((c,), layer_scale)
         w[f"{p}.mlp_layer_scale.scale"] = torch.full((c,), layer_scale)
     w["pre_transformer.norm.weight"] = torch.ones(c)
+    u = latent  # the upsamplers run at the transformer's output width
     for i, factor in enumerate(config.upsampling_ratios):
-        w[f"upsample.{i}.0.conv.weight"] = _kaiming((c, c, factor), c * factor, 1.0, gen)
-        w[f"upsample.{i}.0.conv.bias"] = torch.zeros(c)
+        w[f"upsample.{i}.0.conv.weight"] = _kaiming((u, u, factor), u * factor, 1.0, gen)
+        w[f"upsample.{i}.0.conv.bias"] = torch.zeros(u)
         p = f"upsample.{i}.1"
-        w[f"{p}.dwconv.conv.weight"] = _kaiming((c, 1, 7), 7, 1.0, gen)
-        w[f"{p}.dwconv.conv.bias"] = torch.zeros(c)
-        w[f"{p}.norm.weight"] = torch.ones(c)
-        w[f"{p}.norm.bias"] = torch.zeros(c)
-        w[f"{p}.pwconv1.weight"] = lin(4 * c, c)
-        w[f"{p}.pwconv1.bias"] = torch.zeros(4 * c)
-        w[f"{p}.pwconv2.weight"] = lin(c, 4 * c)
-        w[f"{p}.pwconv2.bias"] = torch.zeros(c)
-        w[f"{p}.gamma"] = torch.full((c,), gamma)
+        w[f"{p}.dwconv.conv.weight"] = _kaiming((u, 1, 7), 7, 1.0, gen)
+        w[f"{p}.dwconv.conv.bias"] = torch.zeros(u)
+        w[f"{p}.norm.weight"] = torch.ones(u)
+        w[f"{p}.norm.bias"] = torch.zeros(u)
+        w[f"{p}.pwconv1.weight"] = lin(4 * u, u)
+        w[f"{p}.pwconv1.bias"] = torch.zeros(4 * u)
+        w[f"{p}.pwconv2.weight"] = lin(u, 4 * u)
+        w[f"{p}.pwconv2.bias"] = torch.zeros(u)
+        w[f"{p}.gamma"] = torch.full((u,), gamma)
 
     def snake(prefix: str, ch: int) -> None:
         for name in ("alpha", "beta"):
@@ -256,7 +334,7 @@ def make_qwen3_code2wav_weights(config: Qwen3Code2WavConfig, seed: int = 0, *,
     g = config.conv_gain
     chans = config.stage_channels()
     k = config.kernel_size
-    w["decoder.0.conv.weight"] = _kaiming((chans[0], c, k), c * k, config.input_conv_gain, gen)
+    w["decoder.0.conv.weight"] = _kaiming((chans[0], u, k), u * k, config.input_conv_gain, gen)
     w["decoder.0.conv.bias"] = torch.zeros(chans[0])
     for bi, rate in enumerate(config.upsample_rates, start=1):
         p = f"decoder.{bi}.block"
@@ -279,22 +357,26 @@ def make_qwen3_code2wav_weights(config: Qwen3Code2WavConfig, seed: int = 0, *,
     return w
 
 
-def qwen3_code2wav_macs_per_frame(config: Qwen3Code2WavConfig) -> int:
+def qwen3_code2wav_macs_per_frame(config: Qwen3Code2WavConfig | Qwen3TTSCodecConfig) -> int:
     """Multiply-accumulates per code frame: the pre-transformer's projections and attention
     (at most a full window of keys per query), the ConvNeXt upsamplers and the decoder convs."""
     c, inter, hd = config.hidden_size, config.intermediate_size, config.head_dim
     kv = config.num_key_value_heads * hd
-    per_token = c * (c + 2 * kv) + c * c + 3 * c * inter
-    per_token += 2 * config.num_attention_heads * hd * config.sliding_window
+    qw = config.num_attention_heads * hd
+    u = getattr(config, "latent_dim", c)
+    per_token = c * (qw + 2 * kv) + qw * c + 3 * c * inter
+    per_token += 2 * qw * config.sliding_window
     macs = config.num_hidden_layers * per_token
+    if hasattr(config, "semantic_quantizers"):  # pre_conv, input_proj, output_proj
+        macs += u * u * config.pre_conv_kernel + 2 * u * c
     positions = 1
     for factor in config.upsampling_ratios:
-        macs += positions * c * c * factor  # transposed conv k = s
+        macs += positions * u * u * factor  # transposed conv k = s
         positions *= factor
-        macs += positions * (7 * c + 2 * 4 * c * c)
+        macs += positions * (7 * u + 2 * 4 * u * u)
     chans = config.stage_channels()
     k = config.kernel_size
-    macs += positions * chans[0] * c * k
+    macs += positions * chans[0] * u * k
     for i, s in enumerate(config.upsample_rates):
         c_in, c_out = chans[i], chans[i + 1]
         macs += positions * c_in * c_out * 2 * s

@@ -37,9 +37,9 @@ import torch
 
 from .. import _native as N
 from ..kernels import code2wav_front as F
-from ..kernels.conv import fused_conv, pack_conv_transpose1d
+from ..kernels.conv import fused_conv, pack_conv1d, pack_conv_transpose1d
 from ..kernels.rvq import rvq_gather_sum
-from .configs import Qwen3Code2WavConfig
+from .configs import Qwen3Code2WavConfig, Qwen3TTSCodecConfig
 from .dac_codec import CodecStatePool, DacCodecDecoder, _Workspace
 
 LN_EPS = 1e-6  # Qwen3OmniMoeConvNeXtBlock's LayerNorm
@@ -126,7 +126,11 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
         self.num_codebooks = cfg.num_quantizers
         c = cfg.hidden_size
         self.hidden = c
+        # the transformer's input / output width (Qwen3-TTS projects from / to latent_dim)
+        self.latent = getattr(cfg, "latent_dim", c)
+        self.q_width = cfg.num_attention_heads * cfg.head_dim
         self.kv_width = cfg.num_key_value_heads * cfg.head_dim
+        self.split_rvq = hasattr(cfg, "semantic_quantizers")
 
         def bf16(t: torch.Tensor) -> torch.Tensor:
             return t.float().to(torch.bfloat16).to(dev).contiguous()
@@ -134,8 +138,27 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
         def f32(t: torch.Tensor) -> torch.Tensor:
             return t.float().to(dev).contiguous()
 
-        self.code_tables = bf16(state["code_embedding.weight"].view(cfg.num_quantizers,
-                                                                    cfg.codebook_size, c))
+        self.pre_conv = self.input_proj = self.output_proj = None
+        if self.split_rvq:
+            # each codebook's entries projected by its group's output projection once, so the
+            # dequantize is one gather-sum: sum_k (W_g(k) E_k)[code_k]
+            books = state["quantizer.codebooks"].double()
+            sem = state["quantizer.semantic_proj.weight"].double()
+            aco = state["quantizer.acoustic_proj.weight"].double()
+            proj = [books[k] @ (sem if k < cfg.semantic_quantizers else aco).t()
+                    for k in range(cfg.num_quantizers)]
+            self.code_tables = torch.stack(proj).float().to(dev).contiguous()
+            self.pre_conv = pack_conv1d(state["pre_conv.conv.weight"].float(),
+                                        state["pre_conv.conv.bias"].float()).to(dev)
+            self.input_proj = pack_conv1d(
+                state["pre_transformer.input_proj.weight"].float()[..., None],
+                state["pre_transformer.input_proj.bias"].float()).to(dev)
+            self.output_proj = pack_conv1d(
+                state["pre_transformer.output_proj.weight"].float()[..., None],
+                state["pre_transformer.output_proj.bias"].float()).to(dev)
+        else:
+            self.code_tables = bf16(state["code_embedding.weight"].view(cfg.num_quantizers,
+                                                                        cfg.codebook_size, c))
         self.layers = []
         for i in range(cfg.num_hidden_layers):
             p = f"pre_transformer.layers.{i}"
@@ -182,6 +205,12 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
 
     # ---------------------------------------------------------------- state pool
 
+    def state_layout(self) -> list[tuple[str, int, int]]:
+        layout = super().state_layout()
+        if self.pre_conv is not None:
+            layout.insert(0, ("pre_conv", self.latent, self.pre_conv.left_pad))
+        return layout
+
     def new_state_pool(self, num_slots: int, capture_slots: int = 0,
                        ring_frames: int | None = None) -> Code2WavStatePool:
         """A pool whose rings hold the window and up to ``ring_frames - (sliding_window - 1)``
@@ -193,7 +222,7 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             self.state_layout(), num_slots=num_slots, capture_slots=capture_slots,
             device=self.device, num_layers=self.config.num_hidden_layers,
             kv_width=self.kv_width, ring_frames=ring_frames, retained_frames=retained,
-            dw_names=[u["name"] for u in self.upsamplers], channels=self.hidden)
+            dw_names=[u["name"] for u in self.upsamplers], channels=self.latent)
 
     # ---------------------------------------------------------------- front
 
@@ -201,27 +230,32 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
         if ws.front:
             return ws.front
         dev, c, cfg = self.device, self.hidden, self.config
+        u = self.latent
         m = batch * frames
         bf = torch.bfloat16
-        width = c + 2 * self.kv_width
+        width = self.q_width + 2 * self.kv_width
         big = max(m * 2 * cfg.intermediate_size, m * width)
         buf = {
             "h": torch.empty(m, c, dtype=torch.float32, device=dev),
             "normed": torch.empty(m, c, dtype=bf, device=dev),
             "qkv": torch.empty(m, width, dtype=bf, device=dev),
-            "attn": torch.empty(m, c, dtype=bf, device=dev),
+            "attn": torch.empty(m, self.q_width, dtype=bf, device=dev),
             "proj": torch.empty(m, c, dtype=bf, device=dev),
             "wide": torch.empty(big, dtype=bf, device=dev),
             "act": torch.empty(m, cfg.intermediate_size, dtype=bf, device=dev),
         }
+        if self.split_rvq:
+            buf["quantized"] = torch.empty(batch, frames, u, dtype=bf, device=dev)
+            buf["pre"] = torch.empty(batch, frames, u, dtype=bf, device=dev)
+            buf["latent"] = torch.empty(batch, frames, u, dtype=bf, device=dev)
         length = frames
         for i, up in enumerate(self.upsamplers):
             length *= up["factor"]
-            buf[f"r{i}"] = torch.empty(batch, length, c, dtype=torch.float32, device=dev)
-            buf[f"n{i}"] = torch.empty(batch, length, c, dtype=bf, device=dev)
-            buf[f"p1_{i}"] = torch.empty(batch * length, 4 * c, dtype=bf, device=dev)
-            buf[f"p2_{i}"] = torch.empty(batch * length, c, dtype=bf, device=dev)
-            buf[f"z{i}"] = torch.empty(batch, length, c, dtype=bf, device=dev)
+            buf[f"r{i}"] = torch.empty(batch, length, u, dtype=torch.float32, device=dev)
+            buf[f"n{i}"] = torch.empty(batch, length, u, dtype=bf, device=dev)
+            buf[f"p1_{i}"] = torch.empty(batch * length, 4 * u, dtype=bf, device=dev)
+            buf[f"p2_{i}"] = torch.empty(batch * length, u, dtype=bf, device=dev)
+            buf[f"z{i}"] = torch.empty(batch, length, u, dtype=bf, device=dev)
         ws.front.update(buf)
         return ws.front
 
@@ -246,9 +280,26 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
         attn, proj, act = buf["attn"], buf["proj"], buf["act"]
         gate_up = buf["wide"][: m * 2 * cfg.intermediate_size].view(m, 2 * cfg.intermediate_size)
         k_books, _, dim = self.code_tables.shape
-        with timer.launch("rvq", m * (k_books * dim * 2 + dim * 4 + k_books * codes.element_size())):
-            rvq_gather_sum(codes, self.code_tables, out=h.view(batch, frames, c), mean=True,
-                           clamp=True)
+        tab = self.code_tables.element_size()
+        with timer.launch("rvq", m * (k_books * dim * tab + dim * 4 + k_books * codes.element_size())):
+            if self.split_rvq:
+                rvq_gather_sum(codes, self.code_tables, out=buf["quantized"], clamp=True)
+            else:
+                rvq_gather_sum(codes, self.code_tables, out=h.view(batch, frames, c), mean=True,
+                               clamp=True)
+        if self.split_rvq:
+            # causal pre_conv (its context from the slot history), then input_proj (+ bias)
+            # into the float32 residual stream
+            pc = self.pre_conv
+            hist = {}
+            if pool is not None:
+                hist = {"history": pool.histories.get("pre_conv"), "slot_index": slots,
+                        "slot_parity": pool.parity, "history_cold": cold}
+            with timer.launch("conv", 2.0 * m * pc.macs_per_position, "pre_conv"):
+                fused_conv(buf["quantized"], pc, buf["pre"], **hist)
+            ip = self.input_proj
+            with timer.launch("conv", 2.0 * m * ip.macs_per_position, "input_proj"):
+                fused_conv(buf["pre"], ip, None, sum_out=h.view(batch, frames, c))
         heads, kv_heads, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         eps = cfg.rms_norm_eps
         with timer.launch("front_elementwise", 0.0):
@@ -268,7 +319,7 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             with timer.launch("front_attention", 4.0 * m * heads * hd * cfg.sliding_window):
                 F.window_attention(qkv, batch, heads, kv_heads, hd, cfg.sliding_window,
                                    hd ** -0.5, attn, cold=cold, **attend_ring)
-            with timer.launch("front_gemm", 2.0 * m * c * c):
+            with timer.launch("front_gemm", 2.0 * m * self.q_width * c):
                 torch.mm(attn, layer["o"], out=proj)
             with timer.launch("front_elementwise", 0.0):
                 F.rms_norm_residual(h, layer["post_norm"], eps, normed, delta=proj,
@@ -283,13 +334,19 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             with timer.launch("front_elementwise", 0.0):
                 F.rms_norm_residual(h, nxt, eps, normed, delta=proj, scale=layer["mlp_scale"])
         x = normed.view(batch, frames, c)
+        if self.output_proj is not None:
+            op = self.output_proj
+            with timer.launch("conv", 2.0 * m * op.macs_per_position, "output_proj"):
+                fused_conv(x, op, buf["latent"])
+            x = buf["latent"]
         length = frames
         for i, up in enumerate(self.upsamplers):
             factor = up["factor"]
             r = buf[f"r{i}"]
             with timer.launch("conv", 2.0 * batch * length * up["up"].macs_per_position,
                               f"upsample.{i}.up"):
-                fused_conv(x, up["up"], None, sum_out=r.view(batch, length, factor * c))
+                fused_conv(x, up["up"], None,
+                           sum_out=r.view(batch, length, factor * self.latent))
             length *= factor
             hist = {}
             if pool is not None:
@@ -300,17 +357,18 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                 F.dwconv_layernorm(r, up["dw_weight"], up["dw_bias"], up["ln_weight"],
                                    up["ln_bias"], LN_EPS, n, **hist)
             rows = batch * length
+            u = self.latent
             p1, p2 = buf[f"p1_{i}"], buf[f"p2_{i}"]
-            with timer.launch("front_gemm", 2.0 * rows * c * 4 * c):
-                torch.mm(n.view(rows, c), up["w1"], out=p1)
+            with timer.launch("front_gemm", 2.0 * rows * u * 4 * u):
+                torch.mm(n.view(rows, u), up["w1"], out=p1)
             with timer.launch("front_elementwise", 0.0):
                 F.bias_gelu(p1, up["b1"])
-            with timer.launch("front_gemm", 2.0 * rows * 4 * c * c):
+            with timer.launch("front_gemm", 2.0 * rows * 4 * u * u):
                 torch.mm(p1, up["w2"], out=p2)
             z = buf[f"z{i}"]
             with timer.launch("front_elementwise", 0.0):
-                F.bias_scale_residual(r.view(rows, c), p2, up["b2"], up["gamma"],
-                                      out=z.view(rows, c))
+                F.bias_scale_residual(r.view(rows, u), p2, up["b2"], up["gamma"],
+                                      out=z.view(rows, u))
             x = z
         return x, length
 
@@ -343,3 +401,84 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
 
     __call__ = from_indices
     forward = from_indices
+
+
+class Qwen3TTSCodecState:
+    """One cohort of streams' decoder state for ``Qwen3TTSCodecDecoder.decode``: a slot pool with
+    one slot per row (conv histories, transposed-conv contexts, K / V rings, frame positions)
+    and the frames the rows have decoded (``frame_position``), as the reference's
+    ``Qwen3TTSIncrementalCodecState`` (qwen3_tts/incremental_codec.py:74-133) carries them."""
+
+    def __init__(self, pool: Code2WavStatePool, batch_size: int, device: torch.device):
+        self.pool = pool
+        self.batch_size = batch_size
+        self.slot_index = torch.arange(batch_size, dtype=torch.int64, device=device)
+        self.frame_position = 0
+
+    @property
+    def frame_positions(self) -> torch.Tensor:
+        """The rows' absolute frame positions (on the device)."""
+        return self.pool.frame_positions[self.slot_index]
+
+    def advance(self, fresh_frames: int) -> None:
+        self.frame_position += fresh_frames
+
+
+class Qwen3TTSCodecDecoder(Qwen3Code2WavDecoder):
+    """The Qwen3-TTS tokenizer's decoder with the reference's incremental API
+    (``Qwen3TTSIncrementalDecoder``, qwen3_tts/incremental_codec.py:771-1083): ``init_state``
+    and ``decode(codes, state)``, every decode of T fresh frames emitting T * total_upsample
+    samples and advancing the state in place; the rows of a state decode together."""
+
+    def __init__(self, state: dict[str, torch.Tensor], config: Qwen3TTSCodecConfig, *,
+                 device: torch.device | str = "cuda", weight_format: str = "bf16",
+                 residual_stacks: bool = True):
+        if getattr(config, "transconv_trim", "right") != "right":
+            raise ValueError("the Qwen3-TTS decoder trims its transposed convs on the right")
+        super().__init__(state, config, device=device, weight_format=weight_format,
+                         residual_stacks=residual_stacks)
+        self.total_upsample = config.hop_length
+        self.compiled_shapes: set[tuple[int, int]] = set()
+
+    def init_state(self, batch_size: int, *, device: torch.device | None = None,
+                   max_fresh_frames: int | None = None) -> Qwen3TTSCodecState:
+        """A zeroed state for ``batch_size`` rows whose decodes take at most
+        ``max_fresh_frames`` frames (default 64)."""
+        if batch_size < 1:
+            raise ValueError("a state holds at least one row")
+        retained = self.config.sliding_window - 1
+        extra = self.DEFAULT_RING_EXTRA if max_fresh_frames is None else max_fresh_frames
+        pool = self.new_state_pool(num_slots=batch_size, ring_frames=retained + extra)
+        return Qwen3TTSCodecState(pool, batch_size, device or self.device)
+
+    def decode(self, codes: torch.Tensor, state: Qwen3TTSCodecState, *,
+               compiled: bool = False) -> torch.Tensor:
+        """(B, Q, T) codes after the frames ``state`` holds -> (B, 1, T * total_upsample)
+        waveform; ``state`` advances by T frames."""
+        if codes.ndim != 3:
+            raise ValueError("Qwen3-TTS incremental codec decoding requires codes shaped [B, Q, T]")
+        if int(codes.shape[0]) < 1:
+            raise ValueError("Qwen3-TTS incremental codec decoding requires at least one row")
+        fresh_frames = int(codes.shape[-1])
+        if fresh_frames <= 0:
+            raise ValueError("Qwen3-TTS incremental codec decoding requires fresh frames")
+        shape = (int(codes.shape[0]), fresh_frames)
+        if compiled and shape not in self.compiled_shapes:
+            raise RuntimeError(f"Qwen3-TTS incremental codec shape {shape} was not precompiled")
+        if int(codes.shape[0]) != state.batch_size:
+            raise ValueError(f"the state holds {state.batch_size} rows, the codes {codes.shape[0]}")
+        with torch.no_grad():
+            waveform = self._decode(codes, {"pool": state.pool, "slot_index": state.slot_index,
+                                            "cold": state.frame_position == 0})
+        if int(waveform.shape[-1]) != fresh_frames * self.total_upsample:
+            raise RuntimeError("Qwen3-TTS incremental codec decoder returned the wrong sample count")
+        state.advance(fresh_frames)
+        return waveform
+
+    def precompile(self, codes: torch.Tensor, state: Qwen3TTSCodecState) -> None:
+        """Admit (B, T) for ``decode(..., compiled=True)``: the HIP path needs no tracing, so this
+        records the shape and, as the reference's precompile does, runs (and advances) one
+        decode."""
+        shape = (int(codes.shape[0]), int(codes.shape[-1]))
+        self.compiled_shapes.add(shape)
+        self.decode(codes, state)

@@ -25,9 +25,11 @@ from sglang_omni_amd.models import (
     GraphKey,
     Qwen3Code2WavConfig,
     Qwen3Code2WavDecoder,
+    Qwen3TTSCodecConfig,
+    Qwen3TTSCodecDecoder,
     make_qwen3_code2wav_weights,
 )
-from sglang_omni_amd.models.configs import QWEN3_CODE2WAV
+from sglang_omni_amd.models.configs import QWEN3_CODE2WAV, QWEN3_TTS_CODEC
 
 pytestmark = pytest.mark.gpu
 
@@ -48,7 +50,9 @@ def effective_weights(state: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]
     bf16 (but the depthwise conv's, which stays float32), decoder conv biases rounded to bf16."""
     out = {}
     for name, t in state.items():
-        if t.dim() >= 2 and "dwconv" not in name:
+        if name.startswith("quantizer."):
+            out[name] = t.float()  # the split quantizer's projected tables stay float32
+        elif t.dim() >= 2 and "dwconv" not in name:
             out[name] = bf16r(t)
         elif name.startswith("decoder.") and name.endswith("conv.bias"):
             out[name] = bf16r(t)
@@ -341,4 +345,88 @@ def test_full_size_decoder_matches_oracle(gpu):
         plain = Q.qwen3_code2wav(codes, {k: (torch.zeros_like(v) if k.endswith(
             ("layer_scale.scale", ".gamma")) else v) for k, v in w.items()}, cfg)
     assert (ref - plain).abs().max() > 20 * 2e-3  # the branches matter
+    check_waveform(got, ref)
+
+
+# ------------------------------------------------------------------------------ Qwen3-TTS
+
+# hidden 256 with 8 heads of 64 (attention twice as wide as the residual stream), latent 512
+TTS_SMALL = Qwen3TTSCodecConfig(codebook_size=64, num_quantizers=4, codebook_dim=32,
+                                latent_dim=512, hidden_size=256, num_hidden_layers=2,
+                                num_attention_heads=8, num_key_value_heads=2, intermediate_size=512,
+                                sliding_window=8, decoder_dim=384, upsample_rates=(2, 3),
+                                input_conv_gain=0.04)
+
+
+@pytest.fixture(scope="module")
+def tts_small(gpu):
+    state = make_qwen3_code2wav_weights(TTS_SMALL, seed=2, branch_scale=0.5,
+                                        activation_spread=0.1)
+    return state, Qwen3TTSCodecDecoder(state, TTS_SMALL, device=gpu)
+
+
+def test_tts_decoder_matches_oracle(tts_small, gpu):
+    state, dec = tts_small
+    codes = _codes(TTS_SMALL, 2, 17, 3)
+    st = dec.init_state(2)
+    got = dec.decode(codes.to(gpu), st)
+    assert got.shape == (2, 1, 17 * TTS_SMALL.hop_length) and st.frame_position == 17
+    with torch.no_grad():
+        ref = Q.qwen3_tts_decode(codes, effective_weights(state), TTS_SMALL)
+    check_waveform(got, ref)
+
+
+def test_tts_decoder_chunks_equal_the_whole_decode(tts_small, gpu):
+    """A stream decoded in chunks of 1..12 frames gives the whole decode's samples, both within
+    the oracle bounds. Unlike the code2wav decoder the two are not bit-identical: the chunks'
+    transformer GEMMs run at 3..36 rows, where hipBLASLt picks other kernels (other summation
+    orders) than at 75 rows, and the bf16 roundings that differ propagate."""
+    state, dec = tts_small
+    codes_cpu = _codes(TTS_SMALL, 3, 25, 4)
+    codes = codes_cpu.to(gpu)
+    whole = dec.decode(codes, dec.init_state(3)).cpu()
+    st = dec.init_state(3)
+    parts, s = [], 0
+    for n in (1, 6, 12, 6):
+        parts.append(dec.decode(codes[..., s:s + n], st).cpu())
+        s += n
+    streamed = torch.cat(parts, dim=-1)
+    err = (streamed - whole).abs().max().item()
+    print(f"streamed vs whole max|err| {err:.3e}")
+    assert streamed.shape == whole.shape and err <= 2e-3
+    assert st.frame_position == 25 and st.frame_positions.tolist() == [25, 25, 25]
+    with torch.no_grad():
+        ref = Q.qwen3_tts_decode(codes_cpu, effective_weights(state), TTS_SMALL)
+    check_waveform(streamed, ref)
+
+
+def test_tts_decode_contract(tts_small, gpu):
+    _, dec = tts_small
+    st = dec.init_state(1)
+    codes = _codes(TTS_SMALL, 1, 4, 5).to(gpu)
+    with pytest.raises(ValueError, match="shaped"):
+        dec.decode(codes[0], st)
+    with pytest.raises(ValueError, match="at least one row"):
+        dec.decode(codes[:0], st)
+    with pytest.raises(ValueError, match="fresh frames"):
+        dec.decode(codes[..., :0], st)
+    with pytest.raises(RuntimeError, match="not precompiled"):
+        dec.decode(codes, st, compiled=True)
+    assert st.frame_position == 0
+    dec.precompile(codes, st)
+    assert st.frame_position == 4
+    out = dec.decode(codes, st, compiled=True)
+    assert out.shape == (1, 1, 4 * TTS_SMALL.hop_length) and st.frame_position == 8
+
+
+def test_tts_full_size_decoder_matches_oracle(gpu):
+    """The default Qwen3-TTS decoder shape (512 hidden, 16 x 64 attention, 1024 latent,
+    1536-channel decoder, x1920) on 1 row x 6 frames."""
+    cfg = QWEN3_TTS_CODEC
+    state = make_qwen3_code2wav_weights(cfg, seed=3, branch_scale=0.1, activation_spread=0.1)
+    dec = Qwen3TTSCodecDecoder(state, cfg, device=gpu)
+    codes = _codes(cfg, 1, 6, 6)
+    got = dec.decode(codes.to(gpu), dec.init_state(1))
+    with torch.no_grad():
+        ref = Q.qwen3_tts_decode(codes, effective_weights(state), cfg)
     check_waveform(got, ref)
