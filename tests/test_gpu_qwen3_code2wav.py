@@ -311,6 +311,53 @@ def test_small_decoder_streams_like_the_whole_decode(small, gpu):
     torch.testing.assert_close(again, parts[0][:1], rtol=0, atol=1e-3)
 
 
+def test_small_decoder_rows_at_different_positions_keep_their_streams(small, gpu):
+    """Two streams at different positions (12 and 20 frames in) continue in one decode: each
+    row reads its own slot's ring window and histories (code2wav.py:417-460 with per-slot frame
+    positions; the reference's test_code2wav.py:1262-1297)."""
+    _, dec = small
+    a = _codes(SMALL, 1, 18, 21).to(gpu)
+    b = _codes(SMALL, 1, 26, 22).to(gpu)
+    whole_a = dec.from_indices(a).cpu()
+    whole_b = dec.from_indices(b).cpu()
+    pool = dec.new_state_pool(num_slots=4)
+    ia = torch.tensor([3], dtype=torch.int64, device=gpu)
+    ib = torch.tensor([1], dtype=torch.int64, device=gpu)
+    head_a = dec.decode_slots(a[..., :12], pool, ia, first_decode=True).cpu()
+    head_b = dec.decode_slots(b[..., :20], pool, ib, first_decode=True).cpu()
+    both = dec.decode_slots(torch.cat([a[..., 12:], b[..., 20:]]), pool,
+                            torch.cat([ia, ib]), first_decode=False).cpu()
+    assert pool.frame_positions[[3, 1]].tolist() == [18, 26]
+    got_a = torch.cat([head_a, both[:1]], dim=-1)
+    got_b = torch.cat([head_b, both[1:]], dim=-1)
+    # the GEMMs run at other row counts than in the whole decodes: rounding-level differences
+    # (a row reading another slot's window or the wrong positions is off by ~1e-1)
+    for got, whole in ((got_a, whole_a), (got_b, whole_b)):
+        assert got.shape == whole.shape
+        assert (got - whole).abs().max().item() <= 2e-3
+        assert O.snr_db(whole, got) >= 40.0
+
+
+def test_small_decoder_reused_slot_equals_a_fresh_pool(small, gpu):
+    """A slot released by one stream and zeroed gives the next stream the decode a fresh pool
+    gives, bit for bit (the reference's test_code2wav.py:1242-1257)."""
+    _, dec = small
+    index = torch.tensor([2, 0], dtype=torch.int64, device=gpu)
+    pool = dec.new_state_pool(num_slots=3)
+    old = _codes(SMALL, 2, 16, 31).to(gpu)
+    dec.decode_slots(old[..., :9], pool, index, first_decode=True)
+    dec.decode_slots(old[..., 9:], pool, index, first_decode=False)
+    pool.zero_slots(index)
+    new = _codes(SMALL, 2, 10, 32).to(gpu)
+    reused = [dec.decode_slots(new[..., :4], pool, index, first_decode=True),
+              dec.decode_slots(new[..., 4:], pool, index, first_decode=False)]
+    fresh_pool = dec.new_state_pool(num_slots=3)
+    fresh = [dec.decode_slots(new[..., :4], fresh_pool, index, first_decode=True),
+             dec.decode_slots(new[..., 4:], fresh_pool, index, first_decode=False)]
+    for r, f in zip(reused, fresh):
+        assert torch.equal(r, f)
+
+
 def test_small_decoder_graph_replay(small, gpu):
     state, dec = small
     pool = dec.new_state_pool(num_slots=4, capture_slots=2)
