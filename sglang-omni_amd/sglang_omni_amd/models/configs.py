@@ -13,7 +13,7 @@ both the GPU decoder (which packs them) and any float32 reference.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import Any
 
 import torch

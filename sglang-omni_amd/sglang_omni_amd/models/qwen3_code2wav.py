@@ -35,7 +35,6 @@ from typing import Any
 
 import torch
 
-from .. import _native as N
 from ..kernels import code2wav_front as F
 from ..kernels.conv import fused_conv, pack_conv1d, pack_conv_transpose1d
 from ..kernels.rvq import rvq_gather_sum

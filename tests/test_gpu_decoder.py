@@ -19,7 +19,6 @@ from sglang_omni_amd.kernels.rvq import rvq_gather_sum
 from sglang_omni_amd.models import (
     DacCodecDecoder,
     DacDecoderConfig,
-    HifiGanConfig,
     HifiGanVocoder,
     make_dac_weights,
     make_hifigan_weights,

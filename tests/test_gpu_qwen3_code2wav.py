@@ -11,8 +11,6 @@ different hipBLASLt kernels at different row counts, so the two are not bit-iden
 
 from __future__ import annotations
 
-import math
-
 import pytest
 import torch
 

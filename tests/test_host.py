@@ -6,7 +6,6 @@ from __future__ import annotations
 
 import pytest
 import torch
-import torch.nn.functional as F
 
 from oracle import codec_oracle as O
 from sglang_omni_amd import _native as N

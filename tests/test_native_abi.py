@@ -9,8 +9,6 @@ import re
 import subprocess
 from pathlib import Path
 
-import pytest
-
 from sglang_omni_amd import _native as N
 
 REPO = Path(__file__).resolve().parents[1]
