@@ -96,6 +96,18 @@ OMNI_DEVICE float apply_act(int act, float v, float a, float b, float slope) {
   }
 }
 
+// Workgroup b of a grid of g runs on XCD b % 8 (round-robin dispatch). The logical tile that
+// gives XCD x the contiguous range [start(x), start(x + 1)) of tiles, ranges as even as g allows:
+// a bijection of [0, g).
+constexpr int kNumXcds = 8;
+OMNI_DEVICE int xcd_tile(int b, int g) {
+  const int xcd = b % kNumXcds;
+  const int local = b / kNumXcds;
+  const int per = g / kNumXcds;
+  const int rem = g % kNumXcds;  // the first rem XCDs take one tile more
+  return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
 #define OMNI_LAUNCH_CHECK()                                   \
   do {                                                        \
     hipError_t _e = hipGetLastError();                        \

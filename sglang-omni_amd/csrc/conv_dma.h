@@ -79,10 +79,12 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   const int wave_co = wave % WAVES_CO;
   const int wave_p = wave / WAVES_CO;
 
-  // blockIdx -> (position tile, column tile), column tile fastest so the workgroups that share
-  // an input tile run back to back.
-  const int n_tile = blockIdx.x % p.n_tiles;
-  const int p_tile = blockIdx.x / p.n_tiles;
+  // blockIdx -> (position tile, column tile). The hardware deals workgroups to the 8 XCDs
+  // round-robin (workgroup b to XCD b % 8), each XCD with its own L2: renumbered so that XCD x
+  // runs the contiguous range x of logical tiles, and with the column tile fastest in that order
+  // the workgroups sharing an input tile run on one XCD, back to back, and read it from its L2.
+  const int n_tile = xcd_tile(blockIdx.x, gridDim.x) % p.n_tiles;
+  const int p_tile = xcd_tile(blockIdx.x, gridDim.x) / p.n_tiles;
   const int n0 = n_tile * BCO;
 
   const int dil = p.dil;
