@@ -331,10 +331,10 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   const int wave_co = wave % WAVES_CO;
   const int wave_p = wave / WAVES_CO;
 
-  // blockIdx -> (position tile, column tile), column tile fastest so the workgroups that share
-  // an input tile run back to back.
-  const int n_tile = blockIdx.x % p.n_tiles;
-  const int p_tile = blockIdx.x / p.n_tiles;
+  // blockIdx -> (position tile, column tile), numbered per XCD (xcd_tile) with the column tile
+  // fastest, so the workgroups that share an input tile run back to back on one XCD.
+  const int n_tile = xcd_tile(blockIdx.x, gridDim.x) % p.n_tiles;
+  const int p_tile = xcd_tile(blockIdx.x, gridDim.x) / p.n_tiles;
   const int n0 = n_tile * BCO;
 
   const int taps = p.taps;
