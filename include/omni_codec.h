@@ -489,6 +489,21 @@ int omni_bias_scale_residual(float* r, int64_t rows, int64_t channels, const voi
 int omni_advance_positions(int64_t* positions, int64_t num_slots, const int64_t* slot_index,
                            int64_t rows, int64_t new_frames, int cold, omni_stream_t stream);
 
+/*
+ * omni_channel_embedding_sum: MOSS-TTS's fused multi-channel embedding
+ * (moss_tts/channel_embedding.py:13-50). out[r, :] = sum over c = 0 .. channels-1, in that
+ * order, of tables[c][ids[r, c], :], the running total rounded to `dtype` (bf16, f16 or f32)
+ * after every add; ids outside [0, vocab_sizes[c]) add nothing. ids (int32 or int64) at
+ * r * id_stride_row + c * id_stride_channel; tables a device array of the channels' table
+ * addresses ([vocab_sizes[c]][hidden] each, `dtype`, contiguous); vocab_sizes a device int64
+ * array; out [rows][hidden] contiguous. Any hidden width; 16-byte loads and stores are used
+ * where hidden % 8 == 0 and the table / output address is 16-byte aligned.
+ */
+int omni_channel_embedding_sum(const void* token_ids, int ids_dtype, int64_t rows,
+                               int64_t channels, int64_t id_stride_row, int64_t id_stride_channel,
+                               const uint64_t* tables, const int64_t* vocab_sizes, int dtype,
+                               int64_t hidden, void* out, omni_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

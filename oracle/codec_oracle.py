@@ -31,6 +31,9 @@ Parity pins (what fixes each function independently of this file's own formulas)
                             round trip istft(stft(x)) = x (Hann window at hop n_fft / 4 sums to a
                             constant); the DC and Nyquist bins of a constant / alternating signal;
                             ``hann_window`` against scipy's get_window.
+* ``channel_embedding_sum`` — one channel is a plain lookup; float32 tables give the
+                            sequential float32 sum of ``rvq_gather_sum`` bit for bit; a bf16
+                            two-channel sum is the rounded float32 sum; out-of-range ids add 0.
 * ``pcm16_encode``        — known answers of the clip / scale / truncate encoding (full scale,
                             half scale, just below one step, out-of-range and NaN samples) and
                             numpy's own float32 -> int16 cast of the same clipped product.
@@ -400,6 +403,22 @@ def hift_istft_tail(h: torch.Tensor, window: torch.Tensor, n_fft: int, hop: int,
     y = istft_reference(magnitude * torch.cos(phase), magnitude * torch.sin(phase), window,
                         n_fft, hop)
     return torch.clamp(y, -audio_limit, audio_limit)
+
+
+def channel_embedding_sum(token_ids: torch.Tensor, weights: list[torch.Tensor]) -> torch.Tensor:
+    """MOSS-TTS's multi-channel embedding (sglang_omni/models/moss_tts/channel_embedding.py:13-50):
+    sum over channels in order of weights[c][token_ids[:, c]], the running float32 total rounded
+    to the tables' dtype after every add; ids outside [0, len(weights[c])) add nothing."""
+    dtype = weights[0].dtype
+    rows, hidden = token_ids.shape[0], weights[0].shape[1]
+    total = torch.zeros(rows, hidden, dtype=torch.float32)
+    for c, table in enumerate(weights):
+        ids = token_ids[:, c].long()
+        ok = (ids >= 0) & (ids < table.shape[0])
+        values = torch.zeros(rows, hidden, dtype=torch.float32)
+        values[ok] = table[ids[ok]].float()
+        total = (total + values).to(dtype).float()
+    return total.to(dtype)
 
 
 # --------------------------------------------------------------------------------------------

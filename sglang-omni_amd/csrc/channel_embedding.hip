@@ -1,0 +1,166 @@
+// The MOSS-TTS multi-channel embedding sum: out[row, :] = sum over channels c, in channel order,
+// of tables[c][token_ids[row, c], :], the running total rounded to the output dtype after every
+// add (the eager ordered sum's bits), ids outside [0, vocab_sizes[c]) adding nothing
+// (moss_tts/channel_embedding.py:13-50).
+//
+// One thread owns 8 consecutive columns of a row (one 16-byte load per channel for bf16 / f16,
+// two for float32, when the widths and addresses allow; element loads otherwise); a row's token
+// ids are wave-uniform loads. Tables are separate allocations, reached through a device array of
+// their addresses, with their own vocabulary sizes.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kCols = 8;  // columns per thread
+
+struct ChannelEmbeddingParams {
+  const void* ids;
+  int ids_dtype;  // OMNI_DTYPE_I32 or OMNI_DTYPE_I64
+  int64_t id_stride_row, id_stride_channel;
+  int channels;
+  const uint64_t* tables;  // [channels] device addresses of [vocab_c][hidden] tables
+  const int64_t* vocab_sizes;
+  int64_t hidden;
+  void* out;  // [rows][hidden]
+  int64_t col_blocks;  // workgroups per row
+  int out_aligned;  // out is 16-byte aligned
+};
+
+template <int DT>
+OMNI_DEVICE float round_to(float v) {
+  if constexpr (DT == OMNI_DTYPE_BF16) return bits_to_float_bf16(float_to_bits_bf16(v));
+  else if constexpr (DT == OMNI_DTYPE_F16) return bits_to_float_f16(float_to_bits_f16(v));
+  else return v;
+}
+
+template <int DT>
+OMNI_DEVICE void load8(const void* table, int64_t off, float v[kCols]) {
+  if constexpr (DT == OMNI_DTYPE_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(table) + off);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(table) + off + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const u16*>(table) + off);
+    const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u16 lo = (u16)(q[i] & 0xffff), hi = (u16)(q[i] >> 16);
+      if constexpr (DT == OMNI_DTYPE_BF16) {
+        v[2 * i] = bits_to_float_bf16(lo);
+        v[2 * i + 1] = bits_to_float_bf16(hi);
+      } else {
+        v[2 * i] = bits_to_float_f16(lo);
+        v[2 * i + 1] = bits_to_float_f16(hi);
+      }
+    }
+  }
+}
+
+template <int DT>
+OMNI_DEVICE void store8(void* out, int64_t off, const float v[kCols]) {
+  if constexpr (DT == OMNI_DTYPE_F32) {
+    float* o = static_cast<float*>(out) + off;
+    *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u16 lo, hi;
+      if constexpr (DT == OMNI_DTYPE_BF16) {
+        lo = float_to_bits_bf16(v[2 * i]);
+        hi = float_to_bits_bf16(v[2 * i + 1]);
+      } else {
+        lo = float_to_bits_f16(v[2 * i]);
+        hi = float_to_bits_f16(v[2 * i + 1]);
+      }
+      q[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    *reinterpret_cast<uint4*>(static_cast<u16*>(out) + off) = make_uint4(q[0], q[1], q[2], q[3]);
+  }
+}
+
+template <int DT>
+OMNI_DEVICE float load1(const void* table, int64_t off) {
+  if constexpr (DT == OMNI_DTYPE_F32) return static_cast<const float*>(table)[off];
+  else if constexpr (DT == OMNI_DTYPE_BF16) return bits_to_float_bf16(static_cast<const u16*>(table)[off]);
+  else return bits_to_float_f16(static_cast<const u16*>(table)[off]);
+}
+
+template <int DT>
+OMNI_DEVICE void store1(void* out, int64_t off, float v) {
+  if constexpr (DT == OMNI_DTYPE_F32) static_cast<float*>(out)[off] = v;
+  else if constexpr (DT == OMNI_DTYPE_BF16) static_cast<u16*>(out)[off] = float_to_bits_bf16(v);
+  else static_cast<u16*>(out)[off] = float_to_bits_f16(v);
+}
+
+// A thread's 8 columns are whole when hidden % 8 == 0; the 16-byte forms are taken when the
+// table (a wave-uniform address) or the output is also 16-byte aligned, element loads otherwise.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void channel_embedding_sum_kernel(ChannelEmbeddingParams p) {
+  const int64_t row = blockIdx.x / p.col_blocks;
+  const int64_t col = ((blockIdx.x - row * p.col_blocks) * kThreads + threadIdx.x) * kCols;
+  if (col >= p.hidden) return;
+  const bool whole = (p.hidden % kCols) == 0;
+  const int n = p.hidden - col < kCols ? (int)(p.hidden - col) : kCols;
+  float total[kCols];
+#pragma unroll
+  for (int i = 0; i < kCols; ++i) total[i] = 0.f;
+  for (int c = 0; c < p.channels; ++c) {
+    const int64_t id_off = row * p.id_stride_row + c * p.id_stride_channel;
+    const int64_t id = p.ids_dtype == OMNI_DTYPE_I64 ? static_cast<const int64_t*>(p.ids)[id_off]
+                                                     : static_cast<const int32_t*>(p.ids)[id_off];
+    float v[kCols];
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) v[i] = 0.f;
+    if (id >= 0 && id < p.vocab_sizes[c]) {
+      const uint64_t table = p.tables[c];
+      const int64_t off = id * p.hidden + col;
+      if (whole && (table & 15) == 0) {
+        load8<DT>(reinterpret_cast<const void*>(table), off, v);
+      } else {
+        for (int i = 0; i < n; ++i) v[i] = load1<DT>(reinterpret_cast<const void*>(table), off + i);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) total[i] = round_to<DT>(total[i] + v[i]);
+  }
+  if (whole && p.out_aligned) {
+    store8<DT>(p.out, row * p.hidden + col, total);
+  } else {
+    for (int i = 0; i < n; ++i) store1<DT>(p.out, row * p.hidden + col + i, total[i]);
+  }
+}
+
+}  // namespace
+
+extern "C" int omni_channel_embedding_sum(const void* token_ids, int ids_dtype, int64_t rows,
+                                          int64_t channels, int64_t id_stride_row,
+                                          int64_t id_stride_channel, const uint64_t* tables,
+                                          const int64_t* vocab_sizes, int dtype, int64_t hidden,
+                                          void* out, omni_stream_t stream) {
+  if (!token_ids || !tables || !vocab_sizes || !out) return OMNI_ERR_INVALID_ARG;
+  if (ids_dtype != OMNI_DTYPE_I32 && ids_dtype != OMNI_DTYPE_I64) return OMNI_ERR_INVALID_ARG;
+  if (dtype != OMNI_DTYPE_BF16 && dtype != OMNI_DTYPE_F16 && dtype != OMNI_DTYPE_F32)
+    return OMNI_ERR_INVALID_ARG;
+  if (rows < 0 || channels < 1 || hidden < 1) return OMNI_ERR_INVALID_ARG;
+  if (rows == 0) return OMNI_OK;
+  const int64_t per_block = (int64_t)kThreads * kCols;
+  const int64_t col_blocks = (hidden + per_block - 1) / per_block;
+  if (channels > 0x7fffffff || rows * col_blocks > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
+  ChannelEmbeddingParams p{token_ids, ids_dtype, id_stride_row, id_stride_channel, (int)channels,
+                           tables, vocab_sizes, hidden, out, col_blocks,
+                           (reinterpret_cast<uintptr_t>(out) & 15) == 0};
+  dim3 grid((unsigned)(rows * col_blocks));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == OMNI_DTYPE_BF16)
+    hipLaunchKernelGGL(channel_embedding_sum_kernel<OMNI_DTYPE_BF16>, grid, dim3(kThreads), 0, s, p);
+  else if (dtype == OMNI_DTYPE_F16)
+    hipLaunchKernelGGL(channel_embedding_sum_kernel<OMNI_DTYPE_F16>, grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(channel_embedding_sum_kernel<OMNI_DTYPE_F32>, grid, dim3(kThreads), 0, s, p);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}

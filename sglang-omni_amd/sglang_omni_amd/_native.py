@@ -204,6 +204,8 @@ SIGNATURES: dict[str, list] = {
     "omni_bias_gelu": [_PTR, _I64, _I64, _I64, _PTR, _PTR],
     "omni_bias_scale_residual": [_PTR, _I64, _I64, _PTR, _I64, _PTR, _PTR, _PTR, _I64, _PTR],
     "omni_advance_positions": [_PTR, _I64, _PTR, _I64, _I64, _INT, _PTR],
+    "omni_channel_embedding_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _PTR, _PTR, _INT, _I64, _PTR,
+                                   _PTR],
 }
 _RESTYPES = {"omni_codec_error_string": ctypes.c_char_p}
 

@@ -1,6 +1,7 @@
 """HIP kernels for the codec/vocoder decode path, with the reference kernels' Python API."""
 
 from .bias_snake_beta import SnakeBetaCoefficients, fused_bias_snake_beta
+from .channel_embedding import ChannelEmbeddingTables
 from .codec_state import history_exchange, overlap_exchange
 from .conv import (
     PackedConv,
@@ -14,6 +15,7 @@ from .rvq import rvq_gather_sum
 from .single_output_conv import clamped_single_output_conv, single_output_conv
 
 __all__ = [
+    "ChannelEmbeddingTables",
     "PackedConv",
     "ResidualUnitWeights",
     "SnakeBetaCoefficients",

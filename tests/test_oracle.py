@@ -601,3 +601,26 @@ def test_waveform_egress_reference_trims_rows():
     assert torch.equal(rows[1], wave[1, 0, :3])
     pcm = O.waveform_egress_reference(wave, None, format="pcm16")
     assert pcm[2].tolist() == [int(v / 32.0 * 32767) for v in range(16, 24)]
+
+
+# ------------------------------------------------------------------------------ MOSS channel sum
+
+
+def test_channel_embedding_sum_pins():
+    g = torch.Generator().manual_seed(9)
+    tables = [torch.randn(v, 16, generator=g) for v in (5, 7, 3)]
+    ids = torch.tensor([[0, 6, 2], [4, 0, 1], [-1, 7, 2], [2, 3, 99]])
+    # one channel: the lookup itself (out-of-range rows are zero)
+    one = O.channel_embedding_sum(ids[:, :1], tables[:1])
+    assert torch.equal(one[:2], tables[0][ids[:2, 0]]) and torch.equal(one[2], torch.zeros(16))
+    # float32 tables, ids in range: the ordered float32 sum of the RVQ gather-sum
+    inr = torch.tensor([[0, 6, 2], [4, 0, 1], [1, 1, 0]])
+    books = torch.stack([t[:3] for t in tables])  # equal-size tables for the RVQ form
+    ids3 = inr.clamp(max=2)
+    rvq = O.rvq_gather_sum(ids3.t()[None], books)[0].t()
+    assert torch.equal(O.channel_embedding_sum(ids3, [t[:3] for t in tables]), rvq)
+    # bf16, two channels: round(a + b) with a, b exact in bf16
+    bt = [t.to(torch.bfloat16) for t in tables[:2]]
+    got = O.channel_embedding_sum(inr[:, :2], bt)
+    ref = (bt[0][inr[:, 0]].float() + bt[1][inr[:, 1]].float()).to(torch.bfloat16)
+    assert torch.equal(got, ref)
