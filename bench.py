@@ -227,7 +227,7 @@ def bench_streaming(args, device) -> dict:
 # HBM bytes per launch of the roofline kernel, from two rocprofv3 --pmc runs of
 # `bench.py --only stack96` (FETCH_SIZE, then WRITE_SIZE), each scaled by the same counter's
 # reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB, WRITE_SIZE =
-# 1024 MiB: fetch x 2, write x 1); profiles/residual_stack96_pmc.md.
+# 1024 MiB: fetch x 2, write x 1).
 PMC_TRAFFIC_BYTES = {"stack96": (385682 * 2 + 5836) * 1024}
 
 
@@ -464,6 +464,39 @@ def bench_egress(device) -> dict:
     return line
 
 
+def bench_channel_embedding(device) -> dict:
+    """MOSS-TTS's multi-channel input embedding: 33 channels (a 151 936-row text table and 32
+    audio tables of 1 025 rows), hidden 2048, bf16, for a 64-row decode batch and a 4096-row
+    prefill. Bytes are algorithmic: every gathered table row, the output rows and the int64 ids
+    once (repeated audio rows may hit in cache)."""
+    from sglang_omni_amd.kernels.channel_embedding import ChannelEmbeddingTables
+    from sglang_omni_amd.utils.timing import LaunchTimer
+
+    hidden, vocab = 2048, [151936] + [1025] * 32
+    g = torch.Generator(device=device).manual_seed(0)
+    weights = [torch.randn(v, hidden, device=device, dtype=torch.bfloat16, generator=g)
+               for v in vocab]
+    tables = ChannelEmbeddingTables()
+    if not tables.refresh(weights):
+        raise RuntimeError("the MOSS-TTS tables could not be fused")
+    line = {}
+    for rows, reps in ((64, 200), (4096, 50)):
+        ids = torch.stack([torch.randint(0, v, (rows,), device=device, generator=g)
+                           for v in vocab], dim=1)
+        tables.embed(ids, weights)
+        timer = LaunchTimer()
+        with timer.launch("embed", 0.0):
+            for _ in range(reps):
+                tables.embed(ids, weights)
+        sync()
+        dt = timer.summary()["embed"]["ms"] / reps / 1e3
+        nbytes = rows * (len(vocab) * hidden * 2 + hidden * 2 + len(vocab) * 8)
+        line[f"rows_{rows}"] = {"us": round(dt * 1e6, 2), "bytes": nbytes,
+                                "achieved_GBps": round(nbytes / dt / 1e9, 1),
+                                "frac": round(nbytes / dt / 1e9 / PEAK_HBM_GBPS, 4)}
+    return line
+
+
 def calibrate(device) -> dict:
     """The box's practical peaks: a 1 GiB device copy (HBM) and a 8192^3 bf16 GEMM (torch's
     hipBLASLt, the MFMA reference point)."""
@@ -540,6 +573,7 @@ def main() -> None:
         line["other_configs"] = bench_other_configs(device)
         line["hift_transforms"] = bench_hift_transforms(device)
         line["egress"] = bench_egress(device)
+        line["channel_embedding"] = bench_channel_embedding(device)
         line["qwen3_code2wav"] = bench_qwen3_code2wav(device)
         line["qwen3_tts_codec"] = bench_qwen3_tts(device)
         line["calibration"] = calibrate(device)

@@ -94,3 +94,23 @@ def test_refuses_what_cannot_be_fused(gpu):
         tables.embed(torch.zeros(3, 2, dtype=torch.int64), w)  # ids on the host
     with pytest.raises(ValueError):
         tables.embed(torch.zeros(3, 3, dtype=torch.int64, device=gpu), w)
+
+
+@pytest.mark.parametrize("rows,hidden,channels,dtype", [
+    (600, 2056, 70, torch.bfloat16),   # 256-thread workgroups, two channel chunks
+    (5, 24, 65, torch.float32),        # 64-thread workgroups, a one-channel second chunk
+    (700, 2048, 33, torch.float16),    # the MOSS-TTS channel count at prefill size
+])
+def test_many_channels_and_both_workgroup_sizes(gpu, rows, hidden, channels, dtype):
+    g = torch.Generator().manual_seed(rows + channels)
+    vocab = [int(v) for v in torch.randint(1, 40, (channels,), generator=g)]
+    weights_cpu = [torch.randn(v, hidden, generator=g).to(dtype) for v in vocab]
+    ids = torch.stack([torch.randint(-1, v + 1, (rows,), generator=g) for v in vocab], dim=1)
+    ids32 = ids.to(torch.int32)
+    weights = [w.to(gpu) for w in weights_cpu]
+    tables = ChannelEmbeddingTables()
+    assert tables.refresh(weights)
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    expected = O.channel_embedding_sum(ids, weights_cpu).view(bits)
+    assert torch.equal(tables.embed(ids.to(gpu), weights).cpu().view(bits), expected)
+    assert torch.equal(tables.embed(ids32.to(gpu), weights).cpu().view(bits), expected)
