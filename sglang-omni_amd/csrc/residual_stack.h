@@ -511,7 +511,17 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         }
       }
     }
-    __syncthreads();  // the operand and the weights are no longer read
+    // every wave's reads of the operand tile (its rows are other waves' halo) and of the last
+    // tap half's weights are done before h overwrites the tile: with the DMA ring, the k = 1
+    // weights' stage barrier (its DMA ran during the last tap half) is that point
+    const u16* w2s = ws;
+    if constexpr (DMA) {
+      const int g = k * Tile::STAGES + 6;
+      stage_begin(g);
+      w2s = ws + (g & 1) * Tile::RING_ELEMS;
+    } else {
+      __syncthreads();
+    }
     // (d) h = Snake(acc * scale + bias) over the operand tile; the k = 1 weights
     const float* cf = coef + k * kCoefRows * C;
 #pragma unroll
@@ -531,13 +541,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    const u16* w2s = ws;
-    if constexpr (DMA) {
-      // the k = 1 weights' stage (its DMA ran during the last tap half); h is complete too
-      const int g = k * Tile::STAGES + 6;
-      stage_begin(g);
-      w2s = ws + (g & 1) * Tile::RING_ELEMS;
-    } else {
+    // (e) reads only the rows this wave wrote in (d), so no barrier is needed between them with
+    // the DMA ring (LDS operations of one wave complete in order)
+    if constexpr (!DMA) {
       store_w2();
       __syncthreads();
       if (k + 1 < p.nunits) load_w1(k + 1, 0);
@@ -558,7 +564,10 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
           acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
       }
     }
-    __syncthreads();  // h and the k = 1 weights are no longer read
+    // (f) overwrites only this wave's rows of the tile, which no other wave reads in (e); with the
+    // DMA ring the k = 1 weights' buffer is next written after the next unit's first stage
+    // barrier, so only the register-staged form (store_w1 of the next unit) needs one here
+    if constexpr (!DMA) __syncthreads();  // h and the k = 1 weights are no longer read
     // (f) x += acc * scale + bias; the next operand Snake(x) (the next unit's input Snake, or
     // the output Snake)
 #pragma unroll
