@@ -408,7 +408,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     u16* hist = p.unit[k].hist;
     const auto hr = buffer_rsrc(hist, p.unit[k].hist_bytes);
     const int hstride = p.unit[k].hist_stride;
-    __syncthreads();  // the operand tile is complete
+    // the operand tile is complete (every wave's (f) of the previous unit); with the DMA ring
+    // the first weight stage's barrier is that point: (a) and (b) below touch only rows that the
+    // dilated conv reads after it
+    if constexpr (DMA) stage_begin(k * Tile::STAGES);
+    else __syncthreads();
     // (a) operand rows left of position 0 (segments that start a stream row): the history copy
     // of the row's slot, or zeros
     if (i0 == 0 && h > 0) {
@@ -459,7 +463,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     if constexpr (DMA) {
       for (int r = 0; r < 6; ++r) {
         const int g = k * Tile::STAGES + r;
-        stage_begin(g);
+        if (r > 0) stage_begin(g);  // stage 0 began at the top of the unit
         const int kc = r >> 1;
         const int t0 = (r & 1) ? 4 : 0;
         const int nt = (r & 1) ? 3 : 4;
