@@ -84,3 +84,23 @@ def test_library_carries_gfx950_code_objects():
     blob = N.LIB_PATH.read_bytes()
     assert b"amdgcn-amd-amdhsa--gfx950" in blob
     assert b"gfx942" not in blob and b"gfx90a" not in blob
+
+
+def test_channel_embedding_tables_refuse_host_tables():
+    """The fused MOSS-TTS channel sum runs on the GPU only: host tables are refused (the caller
+    keeps its eager loop), and embed() before a successful refresh raises instead of computing."""
+    import torch
+
+    from sglang_omni_amd.kernels.channel_embedding import ChannelEmbeddingTables
+
+    tables = ChannelEmbeddingTables()
+    weights = [torch.zeros(4, 8, dtype=torch.bfloat16) for _ in range(3)]
+    assert not tables.refresh(weights)
+    assert tables.weight_pointer_tensor is None
+    try:
+        tables.embed(torch.zeros(2, 3, dtype=torch.int64), weights)
+    except N.OmniCodecError:
+        pass
+    else:
+        raise AssertionError("embed without a refreshed table set must raise")
+    assert tables.embed(torch.zeros(0, 3, dtype=torch.int64), weights).shape == (0, 8)
