@@ -530,7 +530,8 @@ def main() -> None:
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for "
-              f"--gpus {args.gpus}); streams shard across GPUs by process, see DESIGN.md.",
+              f"--gpus {args.gpus}); streams shard across GPUs by process (one decoder, "
+              "slot pool and stream set per GPU, no collective on the decode path).",
               file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -1,7 +1,7 @@
 """Decoder-level GPU parity: the HIP decode path against the float32 oracle of the reference's
 vocoder path on the same seeded inputs, and the streaming invariants of the reference's tests.
 
-Tolerances: waveform max|err| <= 2e-3 for bf16 weights (5e-3 for fp8
+Tolerances (the decode path's stated bounds): waveform max|err| <= 2e-3 for bf16 weights (5e-3 for fp8
 weights) and SNR >= 40 dB against the float32 oracle evaluated with the weights the decoder
 multiplies by (bf16-rounded, or fp8-dequantized). Output RMS is asserted non-trivial so the
 tolerance is not vacuous.
