@@ -529,7 +529,7 @@ def main() -> None:
                         help="skip the xRT of the other configurations and the peak calibration")
     args = parser.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for "
+        print(f"bench.py runs on one GPU: this library has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); streams shard across GPUs by process (one decoder, "
               "slot pool and stream set per GPU, no collective on the decode path).",
               file=sys.stderr)

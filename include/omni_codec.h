@@ -65,7 +65,7 @@ typedef struct ihipStream_t* omni_stream_t;
 enum {
   OMNI_OK = 0,
   OMNI_ERR_INVALID_ARG = 1, /* a shape, stride, pointer or flag outside the documented contract */
-  OMNI_ERR_UNSUPPORTED = 2, /* a valid request this build has no kernel for */
+  OMNI_ERR_UNSUPPORTED = 2, /* a valid request the library has no kernel for */
   OMNI_ERR_LAUNCH = 3,      /* the HIP runtime refused the launch */
   OMNI_ERR_DEVICE = 4       /* a HIP device query failed */
 };

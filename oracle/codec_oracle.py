@@ -1,8 +1,8 @@
 """CPU oracle for the codec/vocoder decode path: a float32 PyTorch restatement of the reference.
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` may import this module, and only as the checker (or, for the CPU baseline,
-as the timed CPU port of the reference path). The product path never routes through it.
+leg of ``bench.py`` may import this module, and only to check results against it (or, for the CPU
+baseline, as the timed CPU port of the reference path). The product path never routes through it.
 
 Every function follows the reference's op order on channels-first ``[B, C, T]`` float32 tensors
 and cites the reference file:line it restates (paths relative to the reference checkout;
@@ -308,7 +308,7 @@ def hifigan_generator(mel: torch.Tensor, weights: dict[str, Any]) -> torch.Tenso
 
 
 # --------------------------------------------------------------------------------------------
-# a8: fp8 weights (no reference implementation; defined by this build)
+# a8: fp8 weights (no reference implementation; defined by this library)
 # --------------------------------------------------------------------------------------------
 
 FP8_E4M3_MAX = 448.0

@@ -1,8 +1,8 @@
 """CPU oracle for the Qwen3-Omni code2wav decoder: a float32 PyTorch restatement of its forward.
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` may import this module, and only as the checker. The product path never
-routes through it.
+leg of ``bench.py`` may import this module, and only to check results against it. The product
+path never routes through it.
 
 It restates ``Qwen3OmniMoeCode2Wav`` (``TF/models/qwen3_omni_moe/modeling_qwen3_omni_moe.py``,
 the transformers module the reference's ``sglang_omni/models/qwen3_omni/components/code2wav.py``
@@ -208,7 +208,7 @@ def qwen3_code2wav(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) ->
 
 
 def split_rvq_decode(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
-    """The Qwen3-TTS split quantizer's dequantize as this build lays it out: the semantic
+    """The Qwen3-TTS split quantizer's dequantize as the decoder here lays it out: the semantic
     codebooks' embeddings summed and projected, plus the acoustic codebooks' summed and
     projected (each group W_g sum_k E_k[code_k]). [B, Q, T] -> [B, T, latent], float64."""
     books = w["quantizer.codebooks"].double()

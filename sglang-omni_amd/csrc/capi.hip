@@ -10,7 +10,7 @@ extern "C" const char* omni_codec_error_string(int status) {
     case OMNI_ERR_INVALID_ARG:
       return "invalid argument: a shape, stride, pointer or flag outside the contract";
     case OMNI_ERR_UNSUPPORTED:
-      return "unsupported: no kernel in this build for the requested shape";
+      return "unsupported: no kernel in this library for the requested shape";
     case OMNI_ERR_LAUNCH:
       return "kernel launch failed";
     case OMNI_ERR_DEVICE:

@@ -140,7 +140,7 @@ class Qwen3TTSCodecConfig:
     only (every decode emits frames * 1920 samples) -> SnakeBeta -> conv to one channel ->
     clamp. The transformer sizes are those of the reference's own test of the decoder
     transformer (tests/unit_test/qwen3_tts/test_incremental_codec.py:461-469); the quantizer's
-    codebook_dim and the layer count are this build's defaults."""
+    codebook_dim and the layer count are this library's defaults."""
 
     codebook_size: int = 2048
     num_quantizers: int = 16
