@@ -90,11 +90,10 @@ class _Block:
 
 # channel counts the fused residual-unit kernel handles (one column tile holds every channel)
 FUSED_UNIT_CHANNELS = (96, 192)
-# ... and those where it is the faster form: with bf16 weights the 192-channel units run as two
-# LDS-DMA conv launches (conv k7 at 96 x 384 tiles, conv k1 at 192 x 192), which beat the fused
-# register-staged kernel even with h (bf16) through HBM between them; with fp8 weights (staged
-# through registers by both forms) the fused launch stays faster
-FUSED_UNIT_CHANNELS_BF16 = (96,)
+# ... and those where it is the faster form with bf16 weights: with its 16-wave tiles (four waves
+# per SIMD) the fused register-staged launch beats the two LDS-DMA conv launches of a
+# 192-channel unit (h stays in LDS instead of a bf16 round trip through HBM): DAC step 0.97x
+FUSED_UNIT_CHANNELS_BF16 = (96, 192)
 # channel counts the residual-stack kernel (every unit of a block in one launch) handles
 STACK_CHANNELS = (96,)
 
