@@ -96,7 +96,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 5: omni_residual_stack's coefficient table */
+int omni_codec_abi_version(void); /* 6: omni_conv1d_plan / omni_conv1d_fused_with */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -197,6 +197,38 @@ typedef struct omni_conv_args {
 } omni_conv_args;
 
 int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
+
+/*
+ * Kernel families of omni_conv1d_fused, each with a list of tile configurations (output columns x
+ * positions per workgroup, waves, staged rows) that the call picks from by problem size:
+ *   OMNI_CONV_KERNEL_DMA         LDS-DMA staged; bf16 operand used as is (no in_activation), bf16
+ *                                weights, taps 1, 2 or 7, c_in a multiple of 32, no weight2; a
+ *                                list of 4 per tap count
+ *   OMNI_CONV_KERNEL_STAGED      register-staged, taps <= 7, any operand mode and weight dtype;
+ *                                10 configurations
+ *   OMNI_CONV_KERNEL_STAGED11    register-staged, taps <= 11, bf16 weights, x bf16; 10
+ *   OMNI_CONV_KERNEL_FUSED_UNIT  the weight2 form (96 or 192 columns): full and short-row tiles
+ * omni_conv1d_fused_with runs the same arithmetic with the family and the list's config-th entry
+ * (1-based) named by the caller (OMNI_ERR_UNSUPPORTED when they cannot serve the call); the
+ * results of every configuration agree to float32 summation order. omni_conv1d_plan reports,
+ * without launching and without touching any pointer, the family, the entry, the list's length and
+ * the workgroup count that omni_conv1d_fused (kernel = OMNI_CONV_KERNEL_AUTO, config = 0) or
+ * omni_conv1d_fused_with (kernel, config) would launch; *kernel_out = OMNI_CONV_KERNEL_AUTO when
+ * the call is empty. No reference counterpart: these exist so tests can hold every configuration
+ * against the float64 conv, and so a caller can see which one its shapes take.
+ */
+enum {
+  OMNI_CONV_KERNEL_AUTO = 0,
+  OMNI_CONV_KERNEL_DMA = 1,
+  OMNI_CONV_KERNEL_STAGED = 2,
+  OMNI_CONV_KERNEL_STAGED11 = 3,
+  OMNI_CONV_KERNEL_FUSED_UNIT = 4
+};
+
+int omni_conv1d_fused_with(const omni_conv_args* args, int kernel, int config,
+                           omni_stream_t stream);
+int omni_conv1d_plan(const omni_conv_args* args, int kernel, int config, int* kernel_out,
+                     int* config_out, int* configs_in_list, int64_t* workgroups);
 
 /*
  * The residual units of a DAC decoder block in one launch (Snake -> conv k = 7, dilation d ->

@@ -6,25 +6,46 @@
 namespace omni_conv {
 namespace {
 
-int dispatch(const ConvParams& p, bool x_f32, bool fp8, bool fuse2, hipStream_t stream) {
+// The kernel family and configuration for p: OMNI_CONV_KERNEL_AUTO picks the family by the
+// operand mode, weight dtype and taps (LDS-DMA for bf16 operands used as they are and bf16
+// weights, then the register-staged kernels) and the configuration by size; a named family runs
+// only if it can serve p. `kernel` returns the family that took the call.
+int dispatch(const ConvParams& p, bool x_f32, bool fp8, bool fuse2, int& kernel, Choice& ch,
+             hipStream_t stream) {
   if (p.halo > kMaxHalo) return OMNI_ERR_UNSUPPORTED;
   const int in_mode = x_f32 ? IN_F32 : (p.in_act != OMNI_ACT_NONE ? IN_ACT : IN_RAW);
-  if (in_mode == IN_RAW && !fp8 && !fuse2 && p.c_in % kChunk == 0) {
+  const int want = kernel;
+  auto allowed = [&](int family) { return want == OMNI_CONV_KERNEL_AUTO || want == family; };
+  if (allowed(OMNI_CONV_KERNEL_DMA) && in_mode == IN_RAW && !fp8 && !fuse2 &&
+      p.c_in % kChunk == 0) {
     int status = OMNI_ERR_UNSUPPORTED;
-    if (p.taps == 7) status = launch_dma_taps7(p, stream);
-    else if (p.taps == 2) status = launch_dma_taps2(p, stream);
-    else if (p.taps == 1) status = launch_dma_taps1(p, stream);
-    if (status != OMNI_ERR_UNSUPPORTED) return status;
-  }
-  if (fuse2) return fp8 ? launch_fused<true>(p, in_mode, stream) : launch_fused<false>(p, in_mode, stream);
-  if (p.taps <= 7) {
-    switch (in_mode) {
-      case IN_RAW: return fp8 ? launch_taps7<IN_RAW, true>(p, stream) : launch_taps7<IN_RAW, false>(p, stream);
-      case IN_ACT: return fp8 ? launch_taps7<IN_ACT, true>(p, stream) : launch_taps7<IN_ACT, false>(p, stream);
-      default: return fp8 ? launch_taps7<IN_F32, true>(p, stream) : launch_taps7<IN_F32, false>(p, stream);
+    if (p.taps == 7) status = launch_dma_taps7(p, ch, stream);
+    else if (p.taps == 2) status = launch_dma_taps2(p, ch, stream);
+    else if (p.taps == 1) status = launch_dma_taps1(p, ch, stream);
+    if (status != OMNI_ERR_UNSUPPORTED || want == OMNI_CONV_KERNEL_DMA) {
+      kernel = OMNI_CONV_KERNEL_DMA;
+      return status;
     }
   }
-  if (p.taps <= 11 && !fp8) return launch_taps11(p, in_mode, stream);
+  if (want == OMNI_CONV_KERNEL_DMA) return OMNI_ERR_UNSUPPORTED;
+  if (fuse2) {
+    if (!allowed(OMNI_CONV_KERNEL_FUSED_UNIT)) return OMNI_ERR_UNSUPPORTED;
+    kernel = OMNI_CONV_KERNEL_FUSED_UNIT;
+    return fp8 ? launch_fused<true>(p, in_mode, ch, stream)
+               : launch_fused<false>(p, in_mode, ch, stream);
+  }
+  if (p.taps <= 7 && allowed(OMNI_CONV_KERNEL_STAGED)) {
+    kernel = OMNI_CONV_KERNEL_STAGED;
+    switch (in_mode) {
+      case IN_RAW: return fp8 ? launch_taps7<IN_RAW, true>(p, ch, stream) : launch_taps7<IN_RAW, false>(p, ch, stream);
+      case IN_ACT: return fp8 ? launch_taps7<IN_ACT, true>(p, ch, stream) : launch_taps7<IN_ACT, false>(p, ch, stream);
+      default: return fp8 ? launch_taps7<IN_F32, true>(p, ch, stream) : launch_taps7<IN_F32, false>(p, ch, stream);
+    }
+  }
+  if (p.taps <= 11 && !fp8 && allowed(OMNI_CONV_KERNEL_STAGED11)) {
+    kernel = OMNI_CONV_KERNEL_STAGED11;
+    return launch_taps11(p, in_mode, ch, stream);
+  }
   return OMNI_ERR_UNSUPPORTED;
 }
 
@@ -191,11 +212,55 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
 
 }  // namespace omni_conv
 
-extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) {
+namespace {
+
+// Validate, then choose (and launch unless `launch` is false) through dispatch.
+int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int* kernel_out,
+               int* config_out, int* count_out, int64_t* workgroups_out, omni_stream_t stream) {
   using namespace omni_conv;
+  if (kernel < OMNI_CONV_KERNEL_AUTO || kernel > OMNI_CONV_KERNEL_FUSED_UNIT || config < 0 ||
+      (kernel == OMNI_CONV_KERNEL_AUTO && config != 0))
+    return OMNI_ERR_INVALID_ARG;
   ConvParams p;
   bool x_f32 = false, fp8 = false, fuse2 = false;
   const int status = make_conv_params(a, p, x_f32, fp8, fuse2);
-  if (status != OMNI_OK) return status < 0 ? OMNI_OK : status;
-  return dispatch(p, x_f32, fp8, fuse2, reinterpret_cast<hipStream_t>(stream));
+  if (status != OMNI_OK) {
+    if (status < 0 && kernel_out) *kernel_out = OMNI_CONV_KERNEL_AUTO;  // nothing to launch
+    return status < 0 ? OMNI_OK : status;
+  }
+  Choice ch;
+  ch.force = config;
+  ch.launch = launch;
+  int family = kernel;
+  const int r = dispatch(p, x_f32, fp8, fuse2, family, ch, reinterpret_cast<hipStream_t>(stream));
+  if (r == OMNI_OK) {
+    if (kernel_out) *kernel_out = family;
+    if (config_out) *config_out = ch.chosen;
+    if (count_out) *count_out = ch.count;
+    if (workgroups_out) *workgroups_out = ch.workgroups;
+  }
+  return r;
+}
+
+}  // namespace
+
+extern "C" int omni_conv1d_fused(const omni_conv_args* a, omni_stream_t stream) {
+  return conv_entry(a, OMNI_CONV_KERNEL_AUTO, 0, true, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int omni_conv1d_fused_with(const omni_conv_args* a, int kernel, int config,
+                                      omni_stream_t stream) {
+  if (kernel == OMNI_CONV_KERNEL_AUTO || config < 1) return OMNI_ERR_INVALID_ARG;
+  return conv_entry(a, kernel, config, true, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int omni_conv1d_plan(const omni_conv_args* a, int kernel, int config, int* kernel_out,
+                                int* config_out, int* configs_in_list, int64_t* workgroups) {
+  if (!kernel_out || !config_out) return OMNI_ERR_INVALID_ARG;
+  *kernel_out = OMNI_CONV_KERNEL_AUTO;
+  *config_out = 0;
+  if (configs_in_list) *configs_in_list = 0;
+  if (workgroups) *workgroups = 0;
+  return conv_entry(a, kernel, config, false, kernel_out, config_out, configs_in_list, workgroups,
+                    nullptr);
 }

@@ -369,9 +369,9 @@ struct DmaConfig {
 // Launch the first configuration in the list that fits and gives at least one workgroup per CU
 // (256); failing that, the fitting one with the most workgroups; OMNI_ERR_UNSUPPORTED when none
 // fits (the caller then takes conv_mfma_kernel). The lists are ordered by measured speed on the
-// decoder's layer shapes.
+// decoder's layer shapes. A forced choice (Choice::force) takes the list's entry instead.
 template <typename... Cfgs>
-int launch_first_fit(const ConvParams& p, hipStream_t stream) {
+int launch_first_fit(const ConvParams& p, Choice& ch, hipStream_t stream) {
   constexpr int64_t min_wgs = 256;
   constexpr int n = sizeof...(Cfgs);
   const bool fits[n] = {Cfgs::fits(p)...};
@@ -384,13 +384,13 @@ int launch_first_fit(const ConvParams& p, hipStream_t stream) {
     if (most < 0 || wgs[i] > wgs[most]) most = i;
   }
   if (pick < 0) pick = most;
-  return pick < 0 ? OMNI_ERR_UNSUPPORTED : launch[pick](p, stream);
+  return choose_and_launch(ch, n, fits, wgs, launch, pick, p, stream);
 }
 
 // Launchers by tap count (1: k = 1 convs, 2: transposed convs of kernel 2 * stride, 7: k = 7
 // convs), one translation unit each.
-int launch_dma_taps1(const ConvParams& p, hipStream_t stream);
-int launch_dma_taps2(const ConvParams& p, hipStream_t stream);
-int launch_dma_taps7(const ConvParams& p, hipStream_t stream);
+int launch_dma_taps1(const ConvParams& p, Choice& ch, hipStream_t stream);
+int launch_dma_taps2(const ConvParams& p, Choice& ch, hipStream_t stream);
+int launch_dma_taps7(const ConvParams& p, Choice& ch, hipStream_t stream);
 
 }  // namespace omni_conv

@@ -3,12 +3,12 @@
 
 namespace omni_conv {
 
-int launch_dma_taps1(const ConvParams& p, hipStream_t stream) {
+int launch_dma_taps1(const ConvParams& p, Choice& ch, hipStream_t stream) {
   // 192 columns x 192 positions, 16 waves of 48 x 48 (four per SIMD) or 8 of 96 x 48, with two
   // chunks per stage (16 waves with the transposed convs': DAC step 0.985x); 96 x 192, 8 waves
   // of 48 x 48 with three chunks per stage; 96 x 256, 8 waves of 96 x 32
   return launch_first_fit<DmaConfig<4, 4, 3, 3, 192, 1, 2>, DmaConfig<2, 4, 6, 3, 192, 1, 2>, DmaConfig<2, 4, 3, 3, 192, 1, 3>,
-                          DmaConfig<1, 8, 6, 2, 256, 1, 2>>(p, stream);
+                          DmaConfig<1, 8, 6, 2, 256, 1, 2>>(p, ch, stream);
 }
 
 }  // namespace omni_conv

@@ -4,12 +4,12 @@
 
 namespace omni_conv {
 
-int launch_dma_taps2(const ConvParams& p, hipStream_t stream) {
+int launch_dma_taps2(const ConvParams& p, Choice& ch, hipStream_t stream) {
   // 192 columns x 192 positions, 16 waves of 48 x 48 (four per SIMD) or 8 of 96 x 48; 96 x 192,
   // 8 waves of 48 x 48 with two
   // chunks per stage; 96 x 384, 8 waves of 96 x 48 (up to 17 short rows of one halo row each)
   return launch_first_fit<DmaConfig<4, 4, 3, 3, 224, 2, 1>, DmaConfig<2, 4, 6, 3, 224, 2, 1>, DmaConfig<2, 4, 3, 3, 224, 2, 2>,
-                          DmaConfig<1, 8, 6, 3, 432, 2, 1>>(p, stream);
+                          DmaConfig<1, 8, 6, 3, 432, 2, 1>>(p, ch, stream);
 }
 
 }  // namespace omni_conv

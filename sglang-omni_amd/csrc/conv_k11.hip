@@ -4,9 +4,9 @@
 
 namespace omni_conv {
 
-int launch_taps11(const ConvParams& p, int in_mode, hipStream_t stream) {
-  if (in_mode == IN_RAW) return Configs<11>::launch<IN_RAW, false>(p, stream);
-  if (in_mode == IN_ACT) return Configs<11>::launch<IN_ACT, false>(p, stream);
+int launch_taps11(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream) {
+  if (in_mode == IN_RAW) return Configs<11>::launch<IN_RAW, false>(p, ch, stream);
+  if (in_mode == IN_ACT) return Configs<11>::launch<IN_ACT, false>(p, ch, stream);
   return OMNI_ERR_UNSUPPORTED;
 }
 

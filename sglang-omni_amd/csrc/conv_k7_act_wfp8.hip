@@ -5,13 +5,13 @@
 namespace omni_conv {
 
 template <>
-int launch_taps7<IN_ACT, true>(const ConvParams& p, hipStream_t stream) {
-  return Configs<7>::launch<IN_ACT, true>(p, stream);
+int launch_taps7<IN_ACT, true>(const ConvParams& p, Choice& ch, hipStream_t stream) {
+  return Configs<7>::launch<IN_ACT, true>(p, ch, stream);
 }
 
 template <>
-int launch_taps7<IN_F32, true>(const ConvParams& p, hipStream_t stream) {
-  return Configs<7>::launch<IN_F32, true>(p, stream);
+int launch_taps7<IN_F32, true>(const ConvParams& p, Choice& ch, hipStream_t stream) {
+  return Configs<7>::launch<IN_F32, true>(p, ch, stream);
 }
 
 }  // namespace omni_conv

@@ -4,8 +4,8 @@
 namespace omni_conv {
 
 template <>
-int launch_taps7<IN_RAW, false>(const ConvParams& p, hipStream_t stream) {
-  return Configs<7>::launch<IN_RAW, false>(p, stream);
+int launch_taps7<IN_RAW, false>(const ConvParams& p, Choice& ch, hipStream_t stream) {
+  return Configs<7>::launch<IN_RAW, false>(p, ch, stream);
 }
 
 }  // namespace omni_conv

@@ -4,8 +4,8 @@
 namespace omni_conv {
 
 template <>
-int launch_taps7<IN_RAW, true>(const ConvParams& p, hipStream_t stream) {
-  return Configs<7>::launch<IN_RAW, true>(p, stream);
+int launch_taps7<IN_RAW, true>(const ConvParams& p, Choice& ch, hipStream_t stream) {
+  return Configs<7>::launch<IN_RAW, true>(p, ch, stream);
 }
 
 }  // namespace omni_conv

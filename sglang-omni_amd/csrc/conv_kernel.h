@@ -693,6 +693,33 @@ inline bool raise_lds_limit(const void* kernel) {
   return e == hipSuccess;
 }
 
+// The kernel configuration a launcher picks from its list: by problem size (force = 0), or the
+// list's force-th entry (1-based; OMNI_ERR_UNSUPPORTED when it does not fit the problem). With
+// launch = false the choice is reported and nothing runs.
+struct Choice {
+  int force = 0;
+  bool launch = true;
+  int chosen = 0;           // 1-based entry of the list (out)
+  int count = 0;            // entries in the list (out)
+  int64_t workgroups = 0;   // of the chosen entry (out)
+};
+
+// Record the choice (the forced entry when one is asked for) and launch it unless the caller
+// only asks which it would be.
+template <typename RunFn>
+int choose_and_launch(Choice& ch, int n, const bool* fits, const int64_t* wgs, RunFn* run,
+                      int pick, const ConvParams& p, hipStream_t stream) {
+  ch.count = n;
+  if (ch.force > 0) {
+    if (ch.force > n || !fits[ch.force - 1]) return OMNI_ERR_UNSUPPORTED;
+    pick = ch.force - 1;
+  }
+  if (pick < 0) return OMNI_ERR_UNSUPPORTED;
+  ch.chosen = pick + 1;
+  ch.workgroups = wgs[pick];
+  return ch.launch ? run[pick](p, stream) : OMNI_OK;
+}
+
 template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int MAX_TAPS>
 struct Config {
   using Tile = ConvTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, MAX_TAPS>;
@@ -747,6 +774,7 @@ template <int T>
 struct Configs {
   // register budgets (accumulators + staging) keep two waves per SIMD, four for Q (16 waves,
   // tried first: fp8 long form 1.09x, HiFiGAN 1.02x faster than starting at A)
+  using Q = Config<2, 8, 3, 3, 384 + 2 * kMaxHalo, T>;  // 96 x 384, 16 waves
   using A = Config<1, 4, 6, 3, 192 + 2 * kMaxHalo, T>;  // 96 cols x 192 positions, 4 waves
   using K = Config<2, 4, 6, 2, 128 + 4 * kMaxHalo, T>;  // 192 x 128, 8 waves
   using H = Config<2, 4, 4, 4, 256 + 2 * kMaxHalo, T>;  // 128 x 256, 8 waves
@@ -756,50 +784,42 @@ struct Configs {
   using E = Config<2, 2, 2, 2, 64 + 4 * kMaxHalo, T>;   // 64 x 64
   using F = Config<4, 1, 2, 2, 32 + 4 * kMaxHalo, T>;   // 128 x 32
   using S = Config<1, 8, 2, 4, 512 + 2 * kMaxHalo, T>;  // 32 x 512, 8 waves (32-channel layers)
-  using Q = Config<2, 8, 3, 3, 384 + 2 * kMaxHalo, T>;  // 96 x 384, 16 waves
+  static constexpr int kCount = 10;
 
-  // The first configuration, in order of measured efficiency on MI355X, that fits, wastes at
-  // most an eighth of its column tiles and still gives at least half a workgroup per CU;
-  // failing that (small problems), the fitting one with the most workgroups. The 32-column tile
-  // comes last: it is for layers with 32 output columns, where every wider tile wastes most of
-  // its matrix work.
+  // The list in order of measured efficiency on MI355X (entry k of a forced choice is the k-th):
+  // the first configuration that fits, wastes at most an eighth of its column tiles and still
+  // gives at least half a workgroup per CU; failing that (small problems), the fitting one with
+  // the most workgroups. The 32-column tile comes last: it is for layers with 32 output columns,
+  // where every wider tile wastes most of its matrix work.
   template <int IN, bool W_FP8>
-  static int launch(const ConvParams& p, hipStream_t stream) {
+  static int launch(const ConvParams& p, Choice& ch, hipStream_t stream) {
     constexpr int64_t min_wgs = 128;
+    const bool fits[kCount] = {Q::fits(p, false), A::fits(p, false), K::fits(p, false),
+                               H::fits(p, false), C::fits(p, false), B::fits(p, false),
+                               D::fits(p, false), E::fits(p, false), F::fits(p, false),
+                               S::fits(p, false)};
+    const int64_t wgs[kCount] = {Q::workgroups(p), A::workgroups(p), K::workgroups(p),
+                                 H::workgroups(p), C::workgroups(p), B::workgroups(p),
+                                 D::workgroups(p), E::workgroups(p), F::workgroups(p),
+                                 S::workgroups(p)};
+    const int bco[kCount] = {Q::Tile::BCO, A::Tile::BCO, K::Tile::BCO, H::Tile::BCO,
+                             C::Tile::BCO, B::Tile::BCO, D::Tile::BCO, E::Tile::BCO,
+                             F::Tile::BCO, S::Tile::BCO};
+    int (*const run[kCount])(ConvParams, hipStream_t) = {
+        &Q::template launch<IN, W_FP8, false>, &A::template launch<IN, W_FP8, false>,
+        &K::template launch<IN, W_FP8, false>, &H::template launch<IN, W_FP8, false>,
+        &C::template launch<IN, W_FP8, false>, &B::template launch<IN, W_FP8, false>,
+        &D::template launch<IN, W_FP8, false>, &E::template launch<IN, W_FP8, false>,
+        &F::template launch<IN, W_FP8, false>, &S::template launch<IN, W_FP8, false>};
     int pick = -1, most = -1;
-    int64_t most_wgs = -1;
-    auto consider = [&](int id, bool fits, int64_t wgs, int bco) {
-      if (!fits) return;
-      const int64_t padded = (p.n_cols + bco - 1) / bco * bco;
-      if (pick < 0 && wgs >= min_wgs && (padded - p.n_cols) * 8 <= p.n_cols) pick = id;
-      if (wgs > most_wgs) {
-        most_wgs = wgs;
-        most = id;
-      }
-    };
-    consider(9, Q::fits(p, false), Q::workgroups(p), Q::Tile::BCO);
-    consider(0, A::fits(p, false), A::workgroups(p), A::Tile::BCO);
-    consider(1, K::fits(p, false), K::workgroups(p), K::Tile::BCO);
-    consider(2, H::fits(p, false), H::workgroups(p), H::Tile::BCO);
-    consider(3, C::fits(p, false), C::workgroups(p), C::Tile::BCO);
-    consider(4, B::fits(p, false), B::workgroups(p), B::Tile::BCO);
-    consider(5, D::fits(p, false), D::workgroups(p), D::Tile::BCO);
-    consider(6, E::fits(p, false), E::workgroups(p), E::Tile::BCO);
-    consider(7, F::fits(p, false), F::workgroups(p), F::Tile::BCO);
-    consider(8, S::fits(p, false), S::workgroups(p), S::Tile::BCO);
-    switch (pick >= 0 ? pick : most) {
-      case 0: return A::template launch<IN, W_FP8, false>(p, stream);
-      case 1: return K::template launch<IN, W_FP8, false>(p, stream);
-      case 2: return H::template launch<IN, W_FP8, false>(p, stream);
-      case 3: return C::template launch<IN, W_FP8, false>(p, stream);
-      case 4: return B::template launch<IN, W_FP8, false>(p, stream);
-      case 5: return D::template launch<IN, W_FP8, false>(p, stream);
-      case 6: return E::template launch<IN, W_FP8, false>(p, stream);
-      case 7: return F::template launch<IN, W_FP8, false>(p, stream);
-      case 8: return S::template launch<IN, W_FP8, false>(p, stream);
-      case 9: return Q::template launch<IN, W_FP8, false>(p, stream);
-      default: return OMNI_ERR_UNSUPPORTED;
+    for (int i = 0; i < kCount; ++i) {
+      if (!fits[i]) continue;
+      const int64_t padded = (p.n_cols + bco[i] - 1) / bco[i] * bco[i];
+      if (pick < 0 && wgs[i] >= min_wgs && (padded - p.n_cols) * 8 <= p.n_cols) pick = i;
+      if (most < 0 || wgs[i] > wgs[most]) most = i;
     }
+    if (pick < 0) pick = most;
+    return choose_and_launch(ch, kCount, fits, wgs, run, pick, p, stream);
   }
 };
 
@@ -808,15 +828,36 @@ using ResidualUnit96Short = Config<1, 2, 6, 1, 32 + 4 * kMaxHalo, 7>;   // short
 using ResidualUnit192 = Config<4, 4, 3, 3, 192 + 3 * kMaxHalo, 7>;      // fused, 192 channels
 using ResidualUnit192Short = Config<2, 2, 6, 1, 32 + 4 * kMaxHalo, 7>;  // short rows
 
+// The fused residual-unit launch for one channel count: the full tile, or the short-row tile
+// when the full one's staged rows do not fit (entries 1 and 2 of a forced choice).
+template <bool W_FP8, typename Full, typename Short>
+int launch_fused_pair(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream) {
+  const bool fits[2] = {Full::fits(p, true), Short::fits(p, true)};
+  const int64_t wgs[2] = {Full::workgroups(p), Short::workgroups(p)};
+  int (*run[2])(ConvParams, hipStream_t);
+  if (in_mode == IN_RAW) {
+    run[0] = &Full::template launch<IN_RAW, W_FP8, true>;
+    run[1] = &Short::template launch<IN_RAW, W_FP8, true>;
+  } else if (in_mode == IN_ACT) {
+    run[0] = &Full::template launch<IN_ACT, W_FP8, true>;
+    run[1] = &Short::template launch<IN_ACT, W_FP8, true>;
+  } else {
+    run[0] = &Full::template launch<IN_F32, W_FP8, true>;
+    run[1] = &Short::template launch<IN_F32, W_FP8, true>;
+  }
+  const int pick = fits[0] ? 0 : (fits[1] ? 1 : -1);
+  return choose_and_launch(ch, 2, fits, wgs, run, pick, p, stream);
+}
+
 // Launchers, one translation unit each (they compile in parallel): taps <= 7 for each input and
-// weight dtype, taps <= 11 for bf16 input and weights, and the fused residual-unit forms.
+// weight dtype, taps <= 11 for bf16 weights, and the fused residual-unit forms.
 template <int IN, bool W_FP8>
-int launch_taps7(const ConvParams& p, hipStream_t stream);
-int launch_taps11(const ConvParams& p, int in_mode, hipStream_t stream);
+int launch_taps7(const ConvParams& p, Choice& ch, hipStream_t stream);
+int launch_taps11(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream);
 template <bool W_FP8>
-int launch_fused(const ConvParams& p, int in_mode, hipStream_t stream);
+int launch_fused(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream);
 #define OMNI_DECLARE_TAPS7(IN_, FP8_) \
-  template <> int launch_taps7<IN_, FP8_>(const ConvParams& p, hipStream_t stream);
+  template <> int launch_taps7<IN_, FP8_>(const ConvParams& p, Choice& ch, hipStream_t stream);
 OMNI_DECLARE_TAPS7(IN_RAW, false)
 OMNI_DECLARE_TAPS7(IN_RAW, true)
 OMNI_DECLARE_TAPS7(IN_ACT, false)
@@ -824,7 +865,7 @@ OMNI_DECLARE_TAPS7(IN_ACT, true)
 OMNI_DECLARE_TAPS7(IN_F32, false)
 OMNI_DECLARE_TAPS7(IN_F32, true)
 #undef OMNI_DECLARE_TAPS7
-template <> int launch_fused<false>(const ConvParams& p, int in_mode, hipStream_t stream);
-template <> int launch_fused<true>(const ConvParams& p, int in_mode, hipStream_t stream);
+template <> int launch_fused<false>(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream);
+template <> int launch_fused<true>(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream);
 
 }  // namespace omni_conv

@@ -4,27 +4,12 @@
 
 namespace omni_conv {
 
-namespace {
-template <typename Cfg>
-int launch_mode(const ConvParams& p, int in_mode, hipStream_t stream) {
-  if (in_mode == IN_RAW) return Cfg::template launch<IN_RAW, false, true>(p, stream);
-  if (in_mode == IN_ACT) return Cfg::template launch<IN_ACT, false, true>(p, stream);
-  return Cfg::template launch<IN_F32, false, true>(p, stream);
-}
-}  // namespace
-
 template <>
-int launch_fused<false>(const ConvParams& p, int in_mode, hipStream_t stream) {
-  if (p.n_cols == 96) {
-    if (ResidualUnit96::fits(p, true)) return launch_mode<ResidualUnit96>(p, in_mode, stream);
-    if (ResidualUnit96Short::fits(p, true))
-      return launch_mode<ResidualUnit96Short>(p, in_mode, stream);
-  }
-  if (p.n_cols == 192) {
-    if (ResidualUnit192::fits(p, true)) return launch_mode<ResidualUnit192>(p, in_mode, stream);
-    if (ResidualUnit192Short::fits(p, true))
-      return launch_mode<ResidualUnit192Short>(p, in_mode, stream);
-  }
+int launch_fused<false>(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream) {
+  if (p.n_cols == 96)
+    return launch_fused_pair<false, ResidualUnit96, ResidualUnit96Short>(p, in_mode, ch, stream);
+  if (p.n_cols == 192)
+    return launch_fused_pair<false, ResidualUnit192, ResidualUnit192Short>(p, in_mode, ch, stream);
   return OMNI_ERR_UNSUPPORTED;
 }
 

@@ -41,6 +41,12 @@ class OmniCodecError(RuntimeError):
 
 INVALID_ARG = 1
 UNSUPPORTED = 2
+ABI_VERSION = 6
+
+# kernel families of omni_conv1d_fused (omni_conv1d_plan / omni_conv1d_fused_with)
+CONV_KERNEL_AUTO, CONV_KERNEL_DMA, CONV_KERNEL_STAGED, CONV_KERNEL_STAGED11, CONV_KERNEL_FUSED_UNIT = range(5)
+CONV_KERNEL_NAMES = {CONV_KERNEL_DMA: "dma", CONV_KERNEL_STAGED: "staged",
+                     CONV_KERNEL_STAGED11: "staged11", CONV_KERNEL_FUSED_UNIT: "fused_unit"}
 
 
 class ConvArgs(ctypes.Structure):
@@ -172,6 +178,9 @@ SIGNATURES: dict[str, list] = {
     "omni_rvq_gather_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _INT, _I64, _I64,
                             _PTR, _INT, _I64, _I64, _I64, _INT, _PTR],
     "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
+    "omni_conv1d_fused_with": [ctypes.POINTER(ConvArgs), _INT, _INT, _PTR],
+    "omni_conv1d_plan": [ctypes.POINTER(ConvArgs), _INT, _INT, ctypes.POINTER(_INT),
+                         ctypes.POINTER(_INT), ctypes.POINTER(_INT), ctypes.POINTER(_I64)],
     "omni_residual_stack": [ctypes.POINTER(ResidualStackArgs), _PTR],
     "omni_residual_stack_coefficients": [ctypes.POINTER(ResidualStackArgs), _PTR, _I64, _PTR],
     "omni_single_output_conv": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _PTR, _PTR,
@@ -244,6 +253,47 @@ def require_device(*tensors: torch.Tensor) -> None:
             raise OmniCodecError(
                 f"the HIP codec kernels need GPU tensors; got a tensor on {t.device}"
             )
+
+
+def require_vector(t: torch.Tensor | None, n: int, what: str, device: torch.device) -> None:
+    """A per-channel coefficient array the kernels index up to n - 1: float32, contiguous, on
+    the call's GPU, at least n entries."""
+    if t is None:
+        return
+    require_device(t)
+    if t.device != device:
+        raise ValueError(f"{what} is on {t.device}, the call on {device}")
+    if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() < n:
+        raise ValueError(f"{what} must be contiguous float32 with at least {n} entries")
+
+
+def require_slot_state(history: torch.Tensor | None, slot_index: torch.Tensor | None,
+                       slot_parity: torch.Tensor | None, *, rows: int, samples: int,
+                       channels: int, device: torch.device, what: str,
+                       dtype: torch.dtype = torch.bfloat16) -> None:
+    """A streaming history pool [slots, 2, samples, channels] (dtype, contiguous rows) with the
+    int64 slot index of the call's rows and the pool's per-slot parity, all on the call's GPU:
+    the kernels read slot_index[0 .. rows-1] and slot_parity[0 .. slots-1] as device arrays."""
+    if history is None:
+        return
+    if slot_index is None or slot_parity is None:
+        raise ValueError(f"{what}: a history pool needs slot_index and slot_parity")
+    require_device(history, slot_index, slot_parity)
+    for t, name in ((history, "history"), (slot_index, "slot_index"), (slot_parity, "slot_parity")):
+        if t.device != device:
+            raise ValueError(f"{what}: {name} is on {t.device}, the call on {device}")
+    if (history.dtype != dtype or history.dim() != 4 or history.shape[1] != 2
+            or history.shape[2] != samples or history.shape[3] != channels
+            or history.stride(3) != 1 or history.stride(2) != channels
+            or history.stride(1) != samples * channels):
+        raise ValueError(f"{what}: history must be {dtype} [slots, 2, {samples}, {channels}] with "
+                         "contiguous slots")
+    if slot_index.dtype != torch.int64 or slot_index.dim() != 1 or slot_index.shape[0] < rows \
+            or slot_index.stride(0) != 1:
+        raise ValueError(f"{what}: slot_index must be contiguous int64 with {rows} entries")
+    if slot_parity.dtype != torch.int64 or slot_parity.dim() != 1 \
+            or slot_parity.shape[0] < history.shape[0] or slot_parity.stride(0) != 1:
+        raise ValueError(f"{what}: slot_parity must be contiguous int64 with an entry per slot")
 
 
 def stream_handle(device: torch.device | None = None) -> int:

@@ -16,6 +16,7 @@ them (sglang_omni/kernels/codec_state.py:150-210).
 from __future__ import annotations
 
 import ctypes
+from contextlib import contextmanager
 from dataclasses import dataclass
 
 import torch
@@ -134,7 +135,7 @@ def pack_conv_transpose1d(weight: torch.Tensor, bias: torch.Tensor | None, *, st
     return packed
 
 
-def fused_conv(
+def _conv_args(
     x: torch.Tensor,
     conv: PackedConv,
     out: torch.Tensor | None,
@@ -161,16 +162,11 @@ def fused_conv(
     slot_index: torch.Tensor | None = None,
     slot_parity: torch.Tensor | None = None,
     history_cold: bool = False,
-) -> torch.Tensor:
-    """Launch ``omni_conv1d_fused`` on the current stream.
-
-    x [B, >=x_length, C_in] bf16 or float32 (rows may sit in longer buffers; channel stride 1),
-    activated per input channel by ``in_activation`` while it is staged; ``second`` is a k = 1
-    conv (C_out -> C_out) fused behind this one with ``mid_activation`` between them;
-    out [B, length, n_cols] bf16 or float32; residual / sum_out / mix tensors float32 with out's
-    logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16.
-    """
-    N.require_device(x, out, sum_out)
+) -> N.ConvArgs:
+    """Validate a ``fused_conv`` call and fill its ``omni_conv_args``: every pointer the kernels
+    dereference is checked for device, dtype and extent here, before any launch."""
+    N.require_device(x, out, sum_out, residual, conv.weight)
+    dev = x.device
     if out is None and sum_out is None:
         raise ValueError("nothing to write: give out or sum_out")
     batch = x.shape[0]
@@ -178,17 +174,28 @@ def fused_conv(
         length = x.shape[1]
     if x_length is None:
         x_length = x.shape[1] if history is None else length
-    if x.dtype not in (torch.bfloat16, torch.float32) or x.stride(2) != 1:
-        raise ValueError("x must be bf16 or float32 with channel stride 1")
+    if x.dim() != 3 or x.dtype not in (torch.bfloat16, torch.float32) or x.stride(2) != 1:
+        raise ValueError("x must be [B, L, C] bf16 or float32 with channel stride 1")
     if x.shape[2] != conv.c_in:
         raise ValueError(f"x has {x.shape[2]} channels, the conv takes {conv.c_in}")
+    if x.shape[1] < x_length:
+        raise ValueError(f"x holds {x.shape[1]} positions, fewer than x_length {x_length}")
+    for t, name in ((conv.weight, "weight"), (conv.scale, "weight scale"), (conv.bias, "bias")):
+        if t is not None and t.device != dev:
+            raise ValueError(f"the conv's {name} is on {t.device}, x on {dev}")
     if second is not None and (second.c_in != conv.c_out or second.taps != 1
                                or conv.n_cols != conv.c_out or second.weight.dtype != conv.weight.dtype):
         raise ValueError("the fused second conv is a k = 1 conv over the first one's channels")
+    if second is not None:
+        N.require_device(second.weight)
+        if second.weight.device != dev:
+            raise ValueError(f"the second conv's weight is on {second.weight.device}, x on {dev}")
     n_cols = conv.n_cols if second is None else second.n_cols
     for t in (out, sum_out):
         if t is None:
             continue
+        if t.device != dev:
+            raise ValueError(f"an output is on {t.device}, x on {dev}")
         if t.dim() != 3 or t.shape[0] != batch or t.shape[2] != n_cols or t.stride(2) != 1:
             raise ValueError(f"outputs must be [B, {length}, {n_cols}] with channel stride 1")
         if t.shape[1] < length:
@@ -197,10 +204,23 @@ def fused_conv(
             raise ValueError("an output may not alias x")
     aux = [t for t in (residual, sum_out) if t is not None]
     if mix is not None:
+        N.require_device(mix[0], mix[1])
         aux += [mix[0], mix[1]]
     for t in aux:
         if t.dtype != torch.float32 or t.stride() != aux[0].stride():
             raise ValueError("residual / sum_out / mix must be float32 with one shared stride")
+        if (t.device != dev or t.dim() != 3 or t.shape[0] != batch or t.shape[1] < length
+                or t.shape[2] != n_cols):
+            raise ValueError(f"residual / sum_out / mix must be [B, {length}, {n_cols}] on {dev}")
+    # per-channel coefficient arrays: the staging reads c_in entries, the epilogues one per
+    # output channel (c_out; n = phase * c_out + co)
+    c_out = conv.c_out if second is None else second.c_out
+    for t, n, name in ((in_a, conv.c_in, "in_a"), (in_b, conv.c_in, "in_b"),
+                       (mid_a, conv.c_out, "mid_a"), (mid_b, conv.c_out, "mid_b"),
+                       (act_a, c_out, "act_a"), (act_b, c_out, "act_b")):
+        N.require_vector(t, n, name, dev)
+    N.require_slot_state(history, slot_index, slot_parity, rows=batch, samples=conv.left_pad,
+                         channels=conv.c_in, device=dev, what="fused_conv")
     r_strides = aux[0].stride() if aux else (0, 0, 1)
     args = N.ConvArgs()
     args.x = x.data_ptr()
@@ -233,8 +253,6 @@ def fused_conv(
         args.mid_act_b = N.ptr(mid_b)
         args.mid_act_slope = mid_slope
     if history is not None:
-        if slot_index is None or slot_parity is None:
-            raise ValueError("a history pool needs slot_index and slot_parity")
         args.hist_pool = history.data_ptr()
         args.slot_index = slot_index.data_ptr()
         args.slot_parity = slot_parity.data_ptr()
@@ -260,10 +278,107 @@ def fused_conv(
     args.act_a = N.ptr(act_a)
     args.act_b = N.ptr(act_b)
     args.act_slope = slope
+    return args
+
+
+def fused_conv(x: torch.Tensor, conv: PackedConv, out: torch.Tensor | None, *,
+               kernel: int = N.CONV_KERNEL_AUTO, config: int = 0, **kw) -> torch.Tensor:
+    """Launch ``omni_conv1d_fused`` on the current stream.
+
+    x [B, >=x_length, C_in] bf16 or float32 (rows may sit in longer buffers; channel stride 1),
+    activated per input channel by ``in_activation`` while it is staged; ``second`` is a k = 1
+    conv (C_out -> C_out) fused behind this one with ``mid_activation`` between them;
+    out [B, length, n_cols] bf16 or float32; residual / sum_out / mix tensors float32 with out's
+    logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16 with int64
+    slot_index [B] and slot_parity [slots]. ``kernel`` / ``config`` name a kernel family and the
+    1-based entry of its tile list (``omni_conv1d_fused_with``) instead of the size-based choice.
+    """
+    args = _conv_args(x, conv, out, **kw)
+    if _plan_log is not None:
+        _plan_log.append(plan_args(args, kernel, config))
     lib = N.load_library()
-    N.check(lib.omni_conv1d_fused(ctypes.byref(args), N.stream_handle(x.device)),
-            "omni_conv1d_fused")
+    stream = N.stream_handle(x.device)
+    if kernel == N.CONV_KERNEL_AUTO and config == 0:
+        N.check(lib.omni_conv1d_fused(ctypes.byref(args), stream), "omni_conv1d_fused")
+    else:
+        N.check(lib.omni_conv1d_fused_with(ctypes.byref(args), kernel, config, stream),
+                f"omni_conv1d_fused_with({N.CONV_KERNEL_NAMES.get(kernel, kernel)}, {config})")
     return out
+
+
+_plan_log: list | None = None
+
+
+@contextmanager
+def recording_plans():
+    """Collect the ``ConvPlan`` of every ``fused_conv`` call made inside the block (in call
+    order), e.g. to see which tile configurations a workload's shapes take."""
+    global _plan_log
+    previous, _plan_log = _plan_log, []
+    try:
+        yield _plan_log
+    finally:
+        _plan_log = previous
+
+
+@dataclass(frozen=True)
+class ConvPlan:
+    """The kernel family, 1-based tile entry, list length and workgroup count of a conv call."""
+
+    kernel: int
+    config: int
+    configs: int
+    workgroups: int
+
+    @property
+    def name(self) -> str:
+        return f"{N.CONV_KERNEL_NAMES.get(self.kernel, 'none')}#{self.config}"
+
+
+def plan_args(args: N.ConvArgs, kernel: int = N.CONV_KERNEL_AUTO, config: int = 0) -> ConvPlan:
+    """What ``omni_conv1d_fused`` (or ``_with``) would launch for these arguments; nothing runs
+    and no pointer is read, so this works without a GPU."""
+    lib = N.load_library()
+    k, c, n, w = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    N.check(lib.omni_conv1d_plan(ctypes.byref(args), kernel, config, ctypes.byref(k),
+                                 ctypes.byref(c), ctypes.byref(n), ctypes.byref(w)),
+            "omni_conv1d_plan")
+    return ConvPlan(k.value, c.value, n.value, w.value)
+
+
+def plan_shapes(*, batch: int, length: int, c_in: int, n_cols: int, c_out: int, taps: int,
+                dilation: int = 1, left_pad: int | None = None, x_f32: bool = False,
+                fp8: bool = False, in_activation: int = N.ACT_NONE, fused_unit: bool = False,
+                history: bool = False, kernel: int = N.CONV_KERNEL_AUTO,
+                config: int = 0) -> ConvPlan:
+    """The plan of a conv call described by its shapes alone (placeholder aligned addresses)."""
+    fake = 1 << 20
+    args = N.ConvArgs()
+    args.x = fake
+    args.x_dtype = N.DTYPE_F32 if x_f32 else N.DTYPE_BF16
+    args.x_stride_t = (c_in + 7) // 8 * 8
+    args.x_stride_b = length * args.x_stride_t
+    args.batch, args.length, args.c_in, args.x_length = batch, length, c_in, 0
+    args.in_activation = in_activation
+    if in_activation == N.ACT_SNAKE:
+        args.in_act_a = args.in_act_b = fake
+    args.weight = fake
+    args.weight_dtype = N.DTYPE_FP8_E4M3 if fp8 else N.DTYPE_BF16
+    args.weight_scale = fake if fp8 else None
+    args.n_cols, args.c_out, args.taps, args.dilation = n_cols, c_out, taps, dilation
+    args.left_pad = (taps - 1) * dilation if left_pad is None else left_pad
+    if fused_unit:
+        args.weight2 = fake
+        args.weight2_scale = fake if fp8 else None
+    if history:
+        args.hist_pool = args.slot_index = args.slot_parity = fake
+        args.hist_num_slots = batch
+        args.hist_slot_stride = 2 * args.left_pad * c_in
+    args.out = fake
+    args.out_dtype = N.DTYPE_BF16
+    args.out_stride_t = n_cols
+    args.out_stride_b = length * n_cols
+    return plan_args(args, kernel, config)
 
 
 @dataclass
@@ -314,6 +429,7 @@ def residual_stack(
     writes final.out [B, 1, L] float32 (out may then be None: the operand stays on chip); returns
     final.out, else out."""
     N.require_device(x, out, x_out)
+    dev = x.device
     if not 1 <= len(units) <= N.MAX_RESIDUAL_UNITS:
         raise ValueError(f"1..{N.MAX_RESIDUAL_UNITS} residual units per launch")
     if x.dtype != torch.float32 or x.dim() != 3 or x.stride(2) != 1:
@@ -328,6 +444,37 @@ def residual_stack(
             raise ValueError("out / x_out must be [B, L, C] (bf16 / float32) with channel stride 1")
         if t.data_ptr() == x.data_ptr():
             raise ValueError("an output may not alias x")
+    for t in (out, x_out):
+        if t is not None and t.device != dev:
+            raise ValueError(f"an output is on {t.device}, x on {dev}")
+    N.require_vector(out_a, channels, "out_a", dev)
+    N.require_vector(out_b, channels, "out_b", dev)
+    if out_a is None or out_b is None:
+        raise ValueError("the stack's output Snake needs out_a and out_b")
+    if histories is not None and len(histories) != len(units):
+        raise ValueError("one history pool (or None) per residual unit")
+    for k, u in enumerate(units):
+        for t, name in ((u.conv1.weight, "conv1 weight"), (u.conv2.weight, "conv2 weight"),
+                        (u.conv1.scale, "conv1 scale"), (u.conv2.scale, "conv2 scale"),
+                        (u.conv1.bias, "conv1 bias"), (u.conv2.bias, "conv2 bias")):
+            if t is not None:
+                N.require_device(t)
+                if t.device != dev:
+                    raise ValueError(f"unit {k}'s {name} is on {t.device}, x on {dev}")
+        for t, name in ((u.in_a, "in_a"), (u.in_b, "in_b"), (u.mid_a, "mid_a"), (u.mid_b, "mid_b")):
+            if t is None:
+                raise ValueError(f"unit {k} needs its {name} Snake coefficients")
+            N.require_vector(t, channels, f"unit {k} {name}", dev)
+        if histories is not None:
+            N.require_slot_state(histories[k], slot_index, slot_parity, rows=batch,
+                                 samples=u.conv1.left_pad, channels=channels, device=dev,
+                                 what=f"residual_stack unit {k}")
+    if final is not None:
+        N.require_device(final.weight, final.out)
+        N.require_vector(final.bias, 1, "final.bias", dev)
+        N.require_slot_state(final.history, slot_index, slot_parity, rows=batch,
+                             samples=final.weight.shape[0] - 1, channels=channels, device=dev,
+                             what="residual_stack final conv")
     wdtype = units[0].conv1.weight.dtype
     args = N.ResidualStackArgs()
     args.x = x.data_ptr()
@@ -395,7 +542,9 @@ def residual_stack(
         args.x_out = x_out.data_ptr()
         args.x_out_stride_b, args.x_out_stride_t = x_out.stride(0), x_out.stride(1)
     if coef_table is not None:
-        if coef_table.dtype != torch.float32 or coef_table.numel() != (8 * len(units) + 2) * channels:
+        N.require_device(coef_table)
+        if (coef_table.dtype != torch.float32 or coef_table.numel() != (8 * len(units) + 2) * channels
+                or coef_table.device != dev or not coef_table.is_contiguous()):
             raise ValueError("coef_table must be stack_coefficients(...) of these units")
         args.coef_table = coef_table.data_ptr()
     lib = N.load_library()

@@ -25,8 +25,13 @@ def clamped_single_output_conv(
         raise ValueError("the input carries the left context")
     if padded.stride(2) != 1 or padded.stride(1) != channels:
         raise ValueError("contiguous rows")
+    if conv.in_channels != channels:
+        raise ValueError(f"the conv takes {conv.in_channels} channels, the input has {channels}")
     weight = conv.weight.detach().float()[0].t().contiguous()  # [taps, C]
     bias = None if conv.bias is None else conv.bias.detach().float().contiguous()
+    for t in (weight, bias):
+        if t is not None and t.device != padded.device:
+            raise ValueError(f"the conv's parameters are on {t.device}, the input on {padded.device}")
     output = padded.new_empty(batch_size, 1, length)
     act = {"clamp": N.ACT_CLAMP, "tanh": N.ACT_TANH, "none": N.ACT_NONE}[activation]
     context = padded[:, taps - 1 :]
@@ -63,9 +68,23 @@ def single_output_conv(
     """Decoder form: x [B, L, C] (no context in the buffer; zeros or slot history left of 0,
     zeros right of L), activated per channel by ``in_activation`` (Snake with in_a / in_b),
     weight [taps, C] float32, out [B, 1, L]."""
-    N.require_device(x, out)
+    N.require_device(x, out, weight)
+    dev = x.device
     batch, length, channels = x.shape
     taps = weight.shape[0]
+    if (weight.dtype != torch.float32 or tuple(weight.shape) != (taps, channels)
+            or not weight.is_contiguous() or weight.device != dev):
+        raise ValueError(f"weight must be contiguous float32 [taps, {channels}] on {dev}")
+    if out.device != dev or out.dim() != 3 or out.shape[0] != batch or out.shape[2] < length:
+        raise ValueError(f"out must be [{batch}, 1, >= {length}] on {dev}")
+    N.require_vector(bias, 1, "bias", dev)
+    if in_activation == N.ACT_SNAKE:
+        if in_a is None or in_b is None:
+            raise ValueError("a Snake input activation needs in_a and in_b")
+        N.require_vector(in_a, channels, "in_a", dev)
+        N.require_vector(in_b, channels, "in_b", dev)
+    N.require_slot_state(history, slot_index, slot_parity, rows=batch, samples=left_pad,
+                         channels=channels, device=dev, what="single_output_conv")
     lib = N.load_library()
     N.check(
         lib.omni_single_output_conv(

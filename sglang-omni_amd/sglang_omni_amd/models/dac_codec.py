@@ -36,6 +36,7 @@ overlap-add.
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass, field
 from typing import Any
 
@@ -145,7 +146,14 @@ class CodecStatePool:
         self.free_slots.append(slot)
 
     def stage_index(self, slots: list[int]) -> torch.Tensor:
-        """The slots' ids on the device, copied from pinned memory so the host never waits."""
+        """The slots' ids on the device, copied from pinned memory so the host never waits.
+        The rows of one decode step must name distinct slots of this pool."""
+        slots = [int(s) for s in slots]
+        if len(set(slots)) != len(slots):
+            raise ValueError(f"the rows of a decode step name one slot twice: {slots}")
+        total = self.parity.shape[0]
+        if any(s < 0 or s >= total for s in slots):
+            raise ValueError(f"slot ids must lie in [0, {total}): {slots}")
         return torch.tensor(slots, dtype=torch.long, pin_memory=True).to(self.device,
                                                                           non_blocking=True)
 
@@ -255,6 +263,7 @@ class DacCodecDecoder:
                                and self.blocks[-1].c_out == self.final_channels
                                and self.final_taps <= 8)
         self._workspaces: dict[tuple[int, int], _Workspace] = {}
+        self._checked_index: tuple[weakref.ref, int] | None = None
         # a utils.timing.LaunchTimer installed here records every launch with its work
         self.timer = NO_TIMER
 
@@ -477,6 +486,21 @@ class DacCodecDecoder:
 
     __call__ = from_indices
 
+    def _check_distinct_slots(self, slot_index: torch.Tensor) -> None:
+        """Rows naming one slot twice would race on its history and parity: refuse them. The
+        check reads the index on the host once per index tensor (and again after any in-place
+        change to it); under graph capture it is the caller's (``CodecStatePool.stage_index``
+        and the graph runner check their host lists)."""
+        if torch.cuda.is_current_stream_capturing():
+            return
+        ref = self._checked_index
+        if ref is not None and ref[0]() is slot_index and ref[1] == slot_index._version:
+            return
+        ids = slot_index.tolist()
+        if len(set(ids)) != len(ids):
+            raise ValueError(f"the rows of a decode step name one slot twice: {ids}")
+        self._checked_index = (weakref.ref(slot_index), slot_index._version)
+
     @torch.no_grad()
     def decode_slots(self, codes: torch.Tensor, pool: CodecStatePool, slot_index: torch.Tensor,
                      *, first_decode: bool) -> torch.Tensor:
@@ -487,4 +511,10 @@ class DacCodecDecoder:
         static ``slot_index``."""
         if slot_index.dtype != torch.int64 or slot_index.shape != (codes.shape[0],):
             raise ValueError("slot_index must be int64 [B]")
+        if slot_index.device != self.device or pool.device != self.device:
+            raise ValueError(f"slot_index ({slot_index.device}) and the pool ({pool.device}) must "
+                             f"be on the decoder's device {self.device}")
+        if not slot_index.is_contiguous():
+            raise ValueError("slot_index must be contiguous")
+        self._check_distinct_slots(slot_index)
         return self._decode(codes, {"pool": pool, "slot_index": slot_index, "cold": first_decode})

@@ -25,6 +25,8 @@ def _run(x: torch.Tensor, a: torch.Tensor, b: torch.Tensor, channels_last: bool,
     y = torch.empty_like(x)
     a = a.detach().float().reshape(-1).contiguous()
     b = b.detach().float().reshape(-1).contiguous()
+    N.require_vector(a, channels, "alpha", x.device)
+    N.require_vector(b, channels, "beta", x.device)
     lib = N.load_library()
     N.check(
         lib.omni_snake(x.data_ptr(), y.data_ptr(), N.omni_dtype(x.dtype), batch, frames, channels,

@@ -1,0 +1,75 @@
+"""The conv launcher's plan and forced-configuration entry points without a GPU: the tile lists
+have the lengths the forced-tile GPU tests sweep, the benchmarked workloads' layer shapes plan to
+entries of those lists, and contract violations are refused before anything runs."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from sglang_omni_amd import _native as N
+from sglang_omni_amd.kernels.conv import plan_shapes
+from tests.test_gpu_tiles import DMA_LIST, FUSED_LIST, STAGED11_LIST, STAGED_LIST
+
+
+def test_list_lengths_match_the_forced_tile_sweep():
+    for taps, n in DMA_LIST.items():
+        c_out = 96
+        n_cols = 6 * c_out if taps == 2 else c_out
+        plan = plan_shapes(batch=2, length=300, c_in=192, n_cols=n_cols, c_out=c_out, taps=taps,
+                           left_pad=1 if taps == 2 else None)
+        assert plan.kernel == N.CONV_KERNEL_DMA and plan.configs == n
+    staged = plan_shapes(batch=2, length=300, c_in=96, n_cols=192, c_out=192, taps=7, fp8=True)
+    assert staged.kernel == N.CONV_KERNEL_STAGED and staged.configs == STAGED_LIST
+    s11 = plan_shapes(batch=2, length=300, c_in=64, n_cols=64, c_out=64, taps=11, dilation=5,
+                      left_pad=25)
+    assert s11.kernel == N.CONV_KERNEL_STAGED11 and s11.configs == STAGED11_LIST
+    fused = plan_shapes(batch=2, length=300, c_in=96, n_cols=96, c_out=96, taps=7, dilation=9,
+                        fused_unit=True)
+    assert fused.kernel == N.CONV_KERNEL_FUSED_UNIT and fused.configs == FUSED_LIST
+
+
+@pytest.mark.parametrize("layer", [
+    # (name, c_in, n_cols, c_out, taps, dilation, left_pad, fused) at 64 streams x 12 frames
+    ("in_conv", 512, 1536, 1536, 7, 1, None, False, 12),
+    ("block1.up", 768, 8 * 384, 384, 2, 1, 1, False, 96),
+    ("block1.k7d9", 384, 384, 384, 7, 9, None, False, 768),
+    ("block1.k1", 384, 384, 384, 1, 1, None, False, 768),
+    ("block2.unit", 192, 192, 192, 7, 3, None, True, 3840),
+    ("block3.up", 192, 6 * 96, 96, 2, 1, 1, False, 3840),
+])
+def test_streaming_step_layers_plan_to_swept_entries(layer):
+    name, c_in, n_cols, c_out, taps, d, left, fused, length = layer
+    plan = plan_shapes(batch=64, length=length, c_in=c_in, n_cols=n_cols, c_out=c_out, taps=taps,
+                       dilation=d, left_pad=left, fused_unit=fused, history=True)
+    assert 1 <= plan.config <= plan.configs
+    assert plan.workgroups >= 64
+    if plan.kernel == N.CONV_KERNEL_DMA:
+        assert plan.configs == DMA_LIST[taps]
+
+
+def test_forced_choice_contract():
+    kw = dict(batch=2, length=300, c_in=192, n_cols=192, c_out=192, taps=7, dilation=3)
+    # a family that cannot serve the call, and entries past the list, are "unsupported"
+    with pytest.raises(N.OmniCodecError, match="status 2"):
+        plan_shapes(**kw, kernel=N.CONV_KERNEL_FUSED_UNIT, config=1)
+    with pytest.raises(N.OmniCodecError, match="status 2"):
+        plan_shapes(**kw, kernel=N.CONV_KERNEL_DMA, config=DMA_LIST[7] + 1)
+    with pytest.raises(N.OmniCodecError, match="status 2"):  # fp8 weights never take LDS-DMA
+        plan_shapes(**kw, fp8=True, kernel=N.CONV_KERNEL_DMA, config=1)
+    # an unknown family or a configuration without a family is an invalid argument
+    with pytest.raises(N.OmniCodecError, match="status 1"):
+        plan_shapes(**kw, kernel=9, config=1)
+    with pytest.raises(N.OmniCodecError, match="status 1"):
+        plan_shapes(**kw, kernel=N.CONV_KERNEL_AUTO, config=2)
+    # the forced launch refuses the automatic family, and a null argument block
+    lib = N.load_library()
+    assert lib.omni_conv1d_fused_with(None, N.CONV_KERNEL_DMA, 1, None) == N.INVALID_ARG
+    args = N.ConvArgs()
+    assert lib.omni_conv1d_fused_with(ctypes.byref(args), N.CONV_KERNEL_AUTO, 0, None) == N.INVALID_ARG
+
+
+def test_an_empty_call_plans_nothing():
+    plan = plan_shapes(batch=0, length=12, c_in=96, n_cols=96, c_out=96, taps=7)
+    assert plan.kernel == N.CONV_KERNEL_AUTO and plan.config == 0
