@@ -271,9 +271,10 @@ def require_slot_state(history: torch.Tensor | None, slot_index: torch.Tensor | 
                        slot_parity: torch.Tensor | None, *, rows: int, samples: int,
                        channels: int, device: torch.device, what: str,
                        dtype: torch.dtype = torch.bfloat16) -> None:
-    """A streaming history pool [slots, 2, samples, channels] (dtype, contiguous rows) with the
-    int64 slot index of the call's rows and the pool's per-slot parity, all on the call's GPU:
-    the kernels read slot_index[0 .. rows-1] and slot_parity[0 .. slots-1] as device arrays."""
+    """A streaming history pool of `slots` contiguous slots, each holding at least two copies of
+    [samples, channels] (e.g. [slots, 2, samples, channels]), with the int64 slot index of the
+    call's rows and the pool's per-slot parity, all on the call's GPU: the kernels read
+    slot_index[0 .. rows-1] and slot_parity[0 .. slots-1] as device arrays."""
     if history is None:
         return
     if slot_index is None or slot_parity is None:
@@ -282,17 +283,16 @@ def require_slot_state(history: torch.Tensor | None, slot_index: torch.Tensor | 
     for t, name in ((history, "history"), (slot_index, "slot_index"), (slot_parity, "slot_parity")):
         if t.device != device:
             raise ValueError(f"{what}: {name} is on {t.device}, the call on {device}")
-    if (history.dtype != dtype or history.dim() != 4 or history.shape[1] != 2
-            or history.shape[2] != samples or history.shape[3] != channels
-            or history.stride(3) != 1 or history.stride(2) != channels
-            or history.stride(1) != samples * channels):
-        raise ValueError(f"{what}: history must be {dtype} [slots, 2, {samples}, {channels}] with "
-                         "contiguous slots")
+    slots = history.shape[0] if history.dim() else 0
+    if (history.dtype != dtype or history.dim() < 2 or slots < 1 or not history.is_contiguous()
+            or history.numel() // slots < 2 * samples * channels):
+        raise ValueError(f"{what}: history must be a contiguous {dtype} pool of slots holding "
+                         f"2 x {samples} x {channels} elements each")
     if slot_index.dtype != torch.int64 or slot_index.dim() != 1 or slot_index.shape[0] < rows \
             or slot_index.stride(0) != 1:
         raise ValueError(f"{what}: slot_index must be contiguous int64 with {rows} entries")
     if slot_parity.dtype != torch.int64 or slot_parity.dim() != 1 \
-            or slot_parity.shape[0] < history.shape[0] or slot_parity.stride(0) != 1:
+            or slot_parity.shape[0] < slots or slot_parity.stride(0) != 1:
         raise ValueError(f"{what}: slot_parity must be contiguous int64 with an entry per slot")
 
 
