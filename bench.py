@@ -425,7 +425,7 @@ def bench_hift_transforms(device) -> dict:
 def bench_egress(device) -> dict:
     """One streaming decode step's waveform (64 rows x 23 040 samples) leaving the device: the
     PCM16 egress kernel alone (HBM bytes per second), and the host-visible time of staging the
-    step through a pinned slot and reading every row back (PCIe-inclusive), as float32 and as
+    step through the pinned ring and reading every row back (PCIe-inclusive), as float32 and as
     PCM16."""
     from sglang_omni_amd.kernels.egress import waveform_egress
     from sglang_omni_amd.scheduling import WaveformEgress
@@ -448,7 +448,7 @@ def bench_egress(device) -> dict:
                              "frac": round(nbytes / dt / 1e9 / PEAK_HBM_GBPS, 4)}}
     ids = list(range(rows))
     for fmt in ("f32", "pcm16"):
-        egress = WaveformEgress(device, format=fmt, max_pinned_slots=2)
+        egress = WaveformEgress(device, format=fmt, depth=2)
         egress.stage_step(ids, w)
         egress.flush()
         reps = 20

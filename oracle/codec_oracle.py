@@ -20,8 +20,12 @@ Parity pins (what fixes each function independently of this file's own formulas)
 * ``causal_conv1d``       — float64 brute-force direct summation; split invariance.
 * ``causal_conv_transpose1d`` — brute-force scatter in float64; streaming split invariance with
                             the reference's overlap-exchange restatement.
-* decoder composition     — built from the pinned pieces; ``transformers`` ``DacResidualUnit``
-                            agrees on the non-causal padding variant of the residual unit.
+* decoder composition     — ``dac_decoder(padding="same")`` against ``transformers``
+                            ``DacDecoder`` (the un-vendored dac library's decoder restated:
+                            conv -> blocks -> Snake -> conv -> tanh) loaded with the same random
+                            weights; the causal mode shares every line but the pad / trim rules,
+                            which the causal conv pins fix; mutations of the reference module
+                            (no final Snake, no tanh, units reordered, no block Snake) fail.
 * ``history_exchange_reference`` / ``overlap_exchange_reference`` — the reference's own
                             pure-torch reference functions (tests/unit_test/kernels/
                             test_codec_state.py:17-49), pinned by the whole-stream invariants of
@@ -163,34 +167,63 @@ def padded_conv_transpose1d(
 # --------------------------------------------------------------------------------------------
 
 
-def residual_unit(x: torch.Tensor, unit: dict[str, Any]) -> torch.Tensor:
-    """``ResidualUnit.forward`` (causal): x + conv1x1(Snake(conv7_d(Snake(x)))); the causal conv
-    keeps the length, so the residual is not trimmed (modded_dac.py:619-642)."""
+def _conv(x: torch.Tensor, conv: dict[str, Any], dilation: int, padding: str) -> torch.Tensor:
+    """The decoder's stride-one conv in either padding mode: ``CausalConvNet`` (modded_dac.py:
+    541-572) or the non-causal ``WNConv1d`` with padding (k - 1) * d // 2 that the reference's
+    non-causal DAC layers (and transformers' ``DacDecoder``) use."""
+    if padding == "causal":
+        return causal_conv1d(x, conv["weight"], conv["bias"], dilation)
+    k = conv["weight"].shape[-1]
+    return F.conv1d(x, conv["weight"], conv["bias"], dilation=dilation,
+                    padding=(k - 1) * dilation // 2)
+
+
+def _upsample(x: torch.Tensor, conv: dict[str, Any], stride: int, padding: str) -> torch.Tensor:
+    """The block's ConvTranspose1d (k = 2s): ``CausalTransConvNet`` (right trim of k - s,
+    modded_dac.py:583-600) or the non-causal ``WNConvTranspose1d`` with padding ceil(s / 2)
+    (modded_dac.py:762-770 with causal=False)."""
+    if padding == "causal":
+        return causal_conv_transpose1d(x, conv["weight"], conv["bias"], stride)
+    return F.conv_transpose1d(x, conv["weight"], conv["bias"], stride=stride,
+                              padding=math.ceil(stride / 2))
+
+
+def residual_unit(x: torch.Tensor, unit: dict[str, Any], padding: str = "causal") -> torch.Tensor:
+    """``ResidualUnit.forward``: x + conv1x1(Snake(conv7_d(Snake(x)))). When the convs return
+    fewer samples than x, x is trimmed on the left (causal) or on both sides (modded_dac.py:
+    619-642); both padding modes keep the length here, so nothing is trimmed."""
     y = snake(x, unit["alpha1"])
-    y = causal_conv1d(y, unit["conv1"]["weight"], unit["conv1"]["bias"], unit["dilation"])
+    y = _conv(y, unit["conv1"], unit["dilation"], padding)
     y = snake(y, unit["alpha2"])
-    y = causal_conv1d(y, unit["conv2"]["weight"], unit["conv2"]["bias"], 1)
+    y = _conv(y, unit["conv2"], 1, padding)
+    trim = x.shape[-1] - y.shape[-1]
+    if trim > 0:
+        x = x[..., trim:] if padding == "causal" else x[..., trim // 2: x.shape[-1] - trim // 2]
     return x + y
 
 
-def decoder_block(x: torch.Tensor, block: dict[str, Any]) -> torch.Tensor:
-    """``DecoderBlock``: Snake -> causal ConvTranspose1d(k = 2s) -> residual units with
-    dilations 1, 3, 9 (modded_dac.py:742-787)."""
+def decoder_block(x: torch.Tensor, block: dict[str, Any], padding: str = "causal") -> torch.Tensor:
+    """``DecoderBlock``: Snake -> ConvTranspose1d(k = 2s) -> residual units with dilations 1, 3, 9
+    (modded_dac.py:742-787)."""
     x = snake(x, block["alpha"])
-    x = causal_conv_transpose1d(x, block["up"]["weight"], block["up"]["bias"], block["stride"])
+    x = _upsample(x, block["up"], block["stride"], padding)
     for unit in block["units"]:
-        x = residual_unit(x, unit)
+        x = residual_unit(x, unit, padding)
     return x
 
 
-def dac_decoder(z: torch.Tensor, weights: dict[str, Any]) -> torch.Tensor:
-    """``Decoder.forward``: causal conv k=7 -> decoder blocks -> Snake -> causal conv to one
-    channel k=7 -> tanh (modded_dac.py:790-835). z [B, D, T] -> [B, 1, T * prod(rates)]."""
-    x = causal_conv1d(z, weights["in_conv"]["weight"], weights["in_conv"]["bias"])
+def dac_decoder(z: torch.Tensor, weights: dict[str, Any], padding: str = "causal") -> torch.Tensor:
+    """``Decoder.forward``: conv k=7 -> decoder blocks -> Snake -> conv to one channel k=7 ->
+    tanh (modded_dac.py:790-835). z [B, D, T] -> [B, 1, T * prod(rates)] in the causal mode the
+    codec decoders run; ``padding="same"`` is the reference's non-causal variant (causal=False),
+    whose odd-stride transposed convs give T * s - 1 samples."""
+    if padding not in ("causal", "same"):
+        raise ValueError(f"padding is 'causal' or 'same', not {padding!r}")
+    x = _conv(z, weights["in_conv"], 1, padding)
     for block in weights["blocks"]:
-        x = decoder_block(x, block)
+        x = decoder_block(x, block, padding)
     x = snake(x, weights["final"]["alpha"])
-    x = causal_conv1d(x, weights["final"]["conv"]["weight"], weights["final"]["conv"]["bias"])
+    x = _conv(x, weights["final"]["conv"], 1, padding)
     return torch.tanh(x)
 
 

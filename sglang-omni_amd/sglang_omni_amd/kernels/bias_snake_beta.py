@@ -1,6 +1,12 @@
-"""SnakeBeta of a conv's output plus its bias, and a residual when given, written into the
-caller's buffer, rounded where the eager adds and SnakeBeta round in the activations' dtype —
-``fused_bias_snake_beta`` of sglang_omni/kernels/bias_snake_beta.py:102-151."""
+"""``fused_bias_snake_beta`` (sglang_omni/kernels/bias_snake_beta.py:102-151) on the HIP kernel.
+
+out = SnakeBeta(conv_output + bias [+ residual]) for bf16 / fp16 channels-last activations, with
+the sum optionally kept in sum_out. Each step rounds to the activations' dtype exactly where the
+unfused eager chain (add bias, add residual, then SnakeBeta's mul / sin / square / mul / add)
+materializes a tensor, so the result has the eager chain's bits.
+
+``SnakeBetaParameters`` and ``SnakeBetaCoefficients`` keep the reference's names and fields, the
+interface its callers build the per-channel coefficients with (bias_snake_beta.py:19-42)."""
 
 from __future__ import annotations
 
@@ -13,6 +19,9 @@ from .. import _native as N
 
 
 class SnakeBetaParameters(Protocol):
+    """Anything holding a SnakeBeta module's parameters: log-scale ``alpha`` and ``beta`` per
+    channel and the ``no_div_by_zero`` epsilon."""
+
     alpha: torch.Tensor
     beta: torch.Tensor
     no_div_by_zero: float
@@ -20,8 +29,9 @@ class SnakeBetaParameters(Protocol):
 
 @dataclass(frozen=True, kw_only=True)
 class SnakeBetaCoefficients:
-    """exp(alpha) and 1 / (exp(beta) + eps) per channel, computed once by the ops the forward
-    runs (sglang_omni/kernels/bias_snake_beta.py:29-42)."""
+    """Per-channel ``alpha_scale`` = exp(alpha) and ``inverse_beta`` = 1 / (exp(beta) + eps),
+    evaluated once with the same torch ops (and dtype) as SnakeBeta's forward, so the kernel
+    multiplies by the values the eager module would."""
 
     alpha_scale: torch.Tensor
     inverse_beta: torch.Tensor
@@ -44,9 +54,10 @@ def fused_bias_snake_beta(
     residual: torch.Tensor | None = None,
     sum_out: torch.Tensor | None = None,
 ) -> None:
-    """SnakeBeta(conv_output + bias, + residual if given) into out, the sum into sum_out if
-    given. [B, L, C] bf16 or fp16; the rows of conv_output and out may sit in longer buffers,
-    residual and sum_out are contiguous."""
+    """Write SnakeBeta(conv_output + bias (+ residual)) into ``out`` and the pre-activation sum
+    into ``sum_out`` when one is given. Tensors are [B, L, C] in bf16 or fp16: each batch row of
+    conv_output and out is one contiguous [L, C] span (rows may be spaced further apart), while
+    residual and sum_out are fully contiguous."""
     N.require_device(conv_output, out)
     batch, length, channels = conv_output.shape
     row = (channels, 1)

@@ -20,10 +20,12 @@ def history_exchange(
     new_samples: int,
     is_cold: bool,
 ) -> None:
-    """Fill a causal conv's (rows, history + new + tail, channels) input around the new samples a
-    producer already wrote: the slot's history in front (zeros for a cold slot), zeros after; then
-    keep the last ``history`` samples of history and new samples as the slot's history.
-    history_pool is (slots, history, channels); slot_index names each row's slot (distinct)."""
+    """In place on ``padded`` (rows, H + new_samples + tail, channels), whose middle
+    ``new_samples`` positions a producer has written: positions [0, H) receive the row's slot
+    history (zeros when ``is_cold``), the tail positions become zero, and the slot's history
+    becomes the last H positions of the row's [history, new samples] sequence, read before this
+    call changed anything. ``history_pool`` is (slots, H, channels); ``slot_index`` holds one
+    distinct slot per row."""
     N.require_device(padded, history_pool, slot_index)
     if padded.dtype != history_pool.dtype:
         raise ValueError("padded and history_pool must share a dtype")
@@ -51,9 +53,10 @@ def overlap_exchange(
     emitted_samples: int,
     is_cold: bool,
 ) -> None:
-    """Add each slot's overlap into the front of a transposed conv's (rows, emitted + overlap,
-    channels) output (not for a cold slot) and keep the samples past the emitted ones as the
-    slot's overlap. Needs emitted_samples >= the overlap, so the two ranges never meet."""
+    """In place on a transposed conv's ``output`` (rows, emitted + O, channels): unless
+    ``is_cold``, the first O positions of each row gain the row's slot overlap (summed in float32,
+    rounded once); the slot's overlap then becomes the row's positions [emitted, emitted + O) as
+    they were before the add. The two ranges are disjoint, which needs emitted_samples >= O."""
     N.require_device(output, overlap_pool, slot_index)
     if output.dtype != overlap_pool.dtype:
         raise ValueError("output and overlap_pool must share a dtype")

@@ -1,5 +1,5 @@
 """Host-side stepping around the codec kernels: waveform egress toward the host."""
 
-from .waveform_egress import PendingStep, WaveformEgress
+from .waveform_egress import WaveformEgress
 
-__all__ = ["PendingStep", "WaveformEgress"]
+__all__ = ["WaveformEgress"]

@@ -1,199 +1,179 @@
-"""Device-to-host egress of decoded waveforms through a bounded pool of pinned slots.
+"""Device-to-host egress of decoded waveforms through a ring of pinned step buffers.
 
-The slot policy is the reference scheduler's (``Code2WavScheduler.stage_window`` /
-``flush_pending`` / ``acquire_slot`` / ``release_slot`` / ``retire_slot`` / ``quarantine_slot`` /
-``reap_retired``, sglang_omni/models/qwen3_omni/components/code2wav_scheduler.py:756-928):
+A decode step's waveform (B rows of samples) leaves the GPU as one transfer: the rows are packed
+on the device (float32, or signed 16-bit PCM encoded by ``omni_waveform_egress``, half the bytes
+over PCIe), copied asynchronously on the decode stream into a pinned host buffer, and handed to
+the caller as owned numpy rows once that copy has completed. It replaces the per-request pinned
+staging of the reference scheduler (sglang_omni/models/qwen3_omni/components/
+code2wav_scheduler.py:756-928), which copies each request's window on its own.
 
-* a window's samples go into a free pinned slot by an asynchronous copy on the decode stream,
-  fenced by the slot's event, and are read only after the event completed;
-* at most ``max_pinned_slots`` slots exist; with none free the oldest pending window is flushed
-  first, and if that frees none the window is copied synchronously;
-* a copy that fails before its event was recorded quarantines the slot (never reused, and the
-  pipeline stops overlapping); one that fails after retires it until its event completes.
+The host side is a ring of ``depth`` entries, each a pinned buffer and one HIP event. Step n
+(counted from 0) travels through entry n % depth, so at most ``depth`` steps are in flight and
+they complete in step order: before step n reuses its entry, step n - depth, the oldest one still
+pending, is delivered (its event waited for), and every step older than that was delivered
+before it. An entry's buffer grows only while the entry holds no transfer.
 
-Where the reference stages each request's window with its own copy, a decode step here leaves
-the device as one transfer: all of the step's rows in one slot, by one copy. The samples travel
-as float32 or, with ``format="pcm16"``, as signed 16-bit PCM encoded on the device by
-``omni_waveform_egress`` (half the bytes over PCIe).
+A transfer that fails part-way leaves its buffer possibly still targeted by a copy that no event
+fences: that buffer is set aside for the life of the egress (never reused, never freed early) and
+every later step is copied synchronously. ``depth = 0`` copies every step synchronously.
 """
 
 from __future__ import annotations
 
 import time
-from collections import deque
 from collections.abc import Hashable, Sequence
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
 from ..kernels.egress import FORMATS, waveform_egress
-from ..utils.cuda_staging import PinnedTransferSlot, normalize_device
 
 
 @dataclass
-class PendingStep:
-    """A decode step's rows on their way to the host."""
+class _Entry:
+    """One ring entry: its pinned buffer, its event, and the step it carries (None when free)."""
 
-    slot: PinnedTransferSlot
-    request_ids: list[Hashable]
-    row_stride: int  # slot elements per row
-    samples: list[int]  # each row's sample count
-    launch_index: int
+    host: torch.Tensor | None = None
+    event: torch.cuda.Event | None = None
+    step: int | None = None
+    request_ids: list[Hashable] = field(default_factory=list)
+    width: int = 0  # elements per row in `host`
+    counts: list[int] = field(default_factory=list)  # samples kept per row
 
 
 class WaveformEgress:
-    """Stages decode steps' waveforms (B, 1, samples) toward the host; returns each row's audio
-    as an owned numpy array (float32, or int16 for ``format="pcm16"``) once its copy is done."""
+    """Stages decode steps' waveforms (B, 1, samples) or (B, samples) toward the host and returns
+    each row's audio as an owned numpy array (float32, or int16 for ``format="pcm16"``), in step
+    order, once its copy has completed."""
 
-    def __init__(self, device: torch.device | str, *, format: str = "f32",
-                 max_pinned_slots: int = 4, default_slot_samples: int = 0) -> None:
+    def __init__(self, device: torch.device | str, *, format: str = "f32", depth: int = 4,
+                 min_samples: int = 0) -> None:
         if format not in FORMATS:
             raise ValueError(f"format must be one of {sorted(FORMATS)}; got {format!r}")
-        if max_pinned_slots < 0:
-            raise ValueError("max_pinned_slots must be >= 0")
-        self.device = normalize_device(device)
+        if depth < 0:
+            raise ValueError(f"depth is a count of ring entries, not {depth}")
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise ValueError(f"waveform egress copies from a GPU, not {device}")
+        self.device = torch.device("cuda", device.index if device.index is not None
+                                   else torch.cuda.current_device())
         self.format = format
         self.dtype = FORMATS[format][1]
-        self.max_pinned_slots = max_pinned_slots
-        self.default_slot_samples = default_slot_samples
-        self.pinned_free: list[PinnedTransferSlot] = []
-        self.pinned_retired: list[PinnedTransferSlot] = []
-        self.pinned_quarantined: list[PinnedTransferSlot] = []
-        self.pinned_created = 0
-        self.pending: deque[PendingStep] = deque()
-        self.pipeline_active = True
-        self.step_launch_count = 0
+        self.min_samples = min_samples
+        self.ring = [_Entry() for _ in range(depth)]
+        self.steps = 0  # steps staged so far; the next one is number `steps`
+        self.delivered = 0  # steps delivered so far (they leave in step order)
+        self.overlapped = depth > 0  # False once a transfer failed: synchronous from then on
+        self.set_aside: list[torch.Tensor] = []  # buffers a failed transfer may still target
         self.wait_ns = 0  # host time spent waiting for copies
+
+    @property
+    def in_flight(self) -> int:
+        return self.steps - self.delivered
 
     # ------------------------------------------------------------------ staging
 
     def stage_step(self, request_ids: Sequence[Hashable], waveform: torch.Tensor,
                    row_samples: Sequence[int] | None = None) -> list[tuple[Hashable, np.ndarray]]:
-        """Start the copy of one decode step's waveform (B, 1, samples) or (B, samples), row r
-        belonging to request_ids[r] and keeping its first row_samples[r] samples (all by
-        default). Returns the audio that had to be completed now: earlier steps flushed to free
-        a slot, and this step itself when it was copied synchronously."""
+        """Start the transfer of one decode step, row r belonging to request_ids[r] and keeping
+        its first row_samples[r] samples (all by default). Returns the audio delivered now: the
+        step that had to leave to free this step's ring entry, and this step itself when it was
+        copied synchronously."""
         rows = waveform[:, 0] if waveform.dim() == 3 else waveform
         if rows.dim() != 2 or rows.shape[0] != len(request_ids):
-            raise ValueError("one request id per waveform row")
+            raise ValueError(f"{len(request_ids)} request ids for a waveform of shape "
+                             f"{tuple(waveform.shape)}")
         batch, width = rows.shape
         counts = [width] * batch if row_samples is None else [int(n) for n in row_samples]
-        if len(counts) != batch or any(n < 0 or n > width for n in counts):
-            raise ValueError(f"row_samples must give 0..{width} samples for each of {batch} rows")
+        if len(counts) != batch or min(counts, default=0) < 0 or max(counts, default=0) > width:
+            raise ValueError(f"row_samples must keep between 0 and {width} samples of each of "
+                             f"the {batch} rows")
         packed = self._packed(rows)
-        total = batch * width
-        ready: list[tuple[Hashable, np.ndarray]] = []
-        slot = self.acquire_slot(total)
-        if slot is None and self.pending:
-            ready += self._flush_one()
-            slot = self.acquire_slot(total)
-        if slot is None:
+        ids = list(request_ids)
+        step = self.steps
+        if not self.overlapped:
+            delivered = self.flush()  # the steps still in flight leave first
             host = packed.cpu()
-            ready += self._rows_of(host.view(batch, width), list(request_ids), counts)
-            return ready
-        recorded = False
+            self.steps += 1
+            self.delivered += 1
+            return delivered + self._rows(host, ids, width, counts)
+        delivered: list[tuple[Hashable, np.ndarray]] = []
+        entry = self.ring[step % len(self.ring)]
+        if entry.step is not None:  # the oldest pending step still holds this entry
+            delivered += self._deliver_through(entry.step)
+        total = batch * width
+        if entry.host is None or entry.host.numel() < total:
+            entry.host = torch.empty(max(total, self.min_samples), dtype=self.dtype,
+                                     pin_memory=True)
         try:
-            slot.view(total).view(batch, width).copy_(packed, non_blocking=True)
-            slot.record(torch.cuda.current_stream(self.device))
-            recorded = True
+            entry.host[:total].view(batch, width).copy_(packed, non_blocking=True)
+            if entry.event is None:
+                entry.event = torch.cuda.Event(blocking=True)
+            entry.event.record(torch.cuda.current_stream(self.device))
         except Exception:
-            if recorded:
-                self.retire_slot(slot)
-            else:
-                self.quarantine_slot(slot)
+            # no event fences whatever part of the copy was enqueued: keep the buffer alive and
+            # out of the ring, and copy synchronously from now on
+            self.set_aside.append(entry.host)
+            entry.host = None
+            entry.event = None
+            self.overlapped = False
             raise
-        self.step_launch_count += 1
-        self.pending.append(PendingStep(slot, list(request_ids), width, counts,
-                                        self.step_launch_count))
-        return ready
+        entry.step, entry.request_ids, entry.width, entry.counts = step, ids, width, counts
+        self.steps += 1
+        return delivered
 
     def _packed(self, rows: torch.Tensor) -> torch.Tensor:
-        """The step's samples in this egress's format as one contiguous (B, samples) device
-        tensor: the waveform itself when it already is one, else the egress kernel's output."""
+        """The step in this egress's format as one contiguous (B, samples) device tensor: the
+        waveform itself when it already is one, else the egress kernel's output."""
         if self.format == "f32" and rows.dtype == torch.float32 and rows.is_contiguous():
             return rows
         return waveform_egress(rows, format=self.format)
 
-    # ------------------------------------------------------------------ completion
+    # ------------------------------------------------------------------ delivery
 
     def poll(self) -> list[tuple[Hashable, np.ndarray]]:
-        """The audio of every pending step whose copy has finished, in launch order, without
-        blocking."""
-        ready: list[tuple[Hashable, np.ndarray]] = []
-        while self.pending and self.pending[0].slot.query():
-            ready += self._flush_one()
-        return ready
+        """The audio of the pending steps whose copies have completed, oldest first, without
+        blocking (delivery stops at the first step still in flight)."""
+        out: list[tuple[Hashable, np.ndarray]] = []
+        while self.in_flight:
+            entry = self._entry_of(self.delivered)
+            if not entry.event.query():
+                break
+            out += self._deliver(entry)
+        return out
 
     def flush(self) -> list[tuple[Hashable, np.ndarray]]:
         """The audio of every pending step, waiting for their copies."""
-        ready: list[tuple[Hashable, np.ndarray]] = []
-        while self.pending:
-            ready += self._flush_one()
-        return ready
+        return self._deliver_through(self.steps - 1) if self.in_flight else []
 
-    def _flush_one(self) -> list[tuple[Hashable, np.ndarray]]:
-        step = self.pending.popleft()
+    def _entry_of(self, step: int) -> _Entry:
+        entry = self.ring[step % len(self.ring)]
+        assert entry.step == step, "ring entries are delivered in step order"
+        return entry
+
+    def _deliver_through(self, step: int) -> list[tuple[Hashable, np.ndarray]]:
+        out: list[tuple[Hashable, np.ndarray]] = []
+        while self.delivered <= step:
+            out += self._deliver(self._entry_of(self.delivered))
+        return out
+
+    def _deliver(self, entry: _Entry) -> list[tuple[Hashable, np.ndarray]]:
         start = time.monotonic_ns()
-        if not step.slot.query():
-            step.slot.synchronize()
+        entry.event.synchronize()
         self.wait_ns += time.monotonic_ns() - start
-        host = step.slot.view(len(step.request_ids) * step.row_stride)
-        audio = self._rows_of(host.view(-1, step.row_stride), step.request_ids, step.samples)
-        self.release_slot(step.slot)
+        audio = self._rows(entry.host, entry.request_ids, entry.width, entry.counts)
+        entry.step = None
+        entry.request_ids, entry.counts = [], []
+        self.delivered += 1
         return audio
 
     @staticmethod
-    def _rows_of(host: torch.Tensor, request_ids: list[Hashable],
-                 counts: list[int]) -> list[tuple[Hashable, np.ndarray]]:
-        array = host.numpy()
-        return [(rid, array[r, :n].copy()) for r, (rid, n) in enumerate(zip(request_ids, counts))]
-
-    # ------------------------------------------------------------------ slot pool
-
-    def acquire_slot(self, elements: int) -> PinnedTransferSlot | None:
-        self.reap_retired()
-        if self.pinned_free:
-            slot = self.pinned_free.pop()
-            try:
-                slot.ensure_capacity(elements)
-            except Exception:
-                self.release_slot(slot)
-                raise
-            return slot
-        if self.pinned_created < self.max_pinned_slots:
-            slot = PinnedTransferSlot(self.device, self.dtype,
-                                      initial_capacity=max(elements, self.default_slot_samples),
-                                      blocking=True)
-            self.pinned_created += 1
-            return slot
-        return None
-
-    def release_slot(self, slot: PinnedTransferSlot) -> None:
-        self.pinned_free.append(slot)
-
-    def retire_slot(self, slot: PinnedTransferSlot) -> None:
-        self.pinned_retired.append(slot)
-
-    def quarantine_slot(self, slot: PinnedTransferSlot) -> None:
-        self.pinned_quarantined.append(slot)
-        self.pipeline_active = False
-
-    def reap_retired(self) -> None:
-        """Return retired slots whose copies finished to the free list, without blocking; a slot
-        whose event cannot be queried is quarantined."""
-        still: list[PinnedTransferSlot] = []
-        for slot in self.pinned_retired:
-            try:
-                complete = slot.query()
-            except Exception:
-                self.quarantine_slot(slot)
-                continue
-            if complete:
-                self.release_slot(slot)
-            else:
-                still.append(slot)
-        self.pinned_retired = still
+    def _rows(host: torch.Tensor, request_ids: list[Hashable], width: int,
+              counts: list[int]) -> list[tuple[Hashable, np.ndarray]]:
+        flat = host.reshape(-1).numpy()
+        return [(rid, flat[r * width: r * width + n].copy())
+                for r, (rid, n) in enumerate(zip(request_ids, counts))]
 
 
-__all__ = ["PendingStep", "WaveformEgress"]
+__all__ = ["WaveformEgress"]

@@ -1,63 +1,63 @@
-"""The audio payload wire format of the vocoder stage's output messages.
+"""The audio payload the vocoder stage puts on the wire.
 
-Same fields and encoding as ``sglang_omni/utils/audio_payload.py:13-65`` and
-``build_audio_chunk_payload`` (``sglang_omni/scheduling/audio_stream.py:336-344``): the samples
-as little-endian float32 bytes, their shape (flattened to one dimension unless a two-dimensional
-waveform keeps its channels), the dtype name, and optionally the sample rate and modality.
-Signed 16-bit PCM for realtime sessions is encoded on the device (``kernels.egress``).
+The keys and their encoding are the relay's wire format (sglang_omni/utils/audio_payload.py:
+23-65 builds them, sglang_omni/scheduling/audio_stream.py:336-344 for streamed chunks), so they
+are kept exactly: ``audio_waveform`` holds the samples as little-endian float32 bytes,
+``audio_waveform_shape`` their shape (one dimension, or [channels, samples] when a two-dimensional
+waveform keeps its channels), ``audio_waveform_dtype`` the string "float32", and ``sample_rate``
+/ ``modality`` appear only when given. Signed 16-bit PCM for realtime sessions is produced on the
+device instead (``kernels.egress``).
 """
 
 from __future__ import annotations
 
-from collections.abc import Mapping
+from typing import Any
 
 import numpy as np
 import torch
-from numpy.typing import ArrayLike
+
+_LITTLE_ENDIAN_F32 = np.dtype("<f4")
 
 
-def audio_data_uri_from_reference(reference: Mapping[str, object]) -> str | None:
-    """A data: URI for a reference audio mapping with base64 ``data`` (media type defaults to
-    audio/wav), or None without data."""
-    data = reference.get("data")
-    if data is None:
-        return None
-    media_type = reference.get("media_type") or "audio/wav"
-    return f"data:{media_type};base64,{data}"
+def _samples(audio: Any, keep_channels: bool, what: str) -> np.ndarray:
+    """The waveform as a C-ordered little-endian float32 array: kept [channels, samples] when
+    asked and two-dimensional, one dimension otherwise."""
+    if isinstance(audio, torch.Tensor):
+        array = audio.detach().to(device="cpu", dtype=torch.float32).numpy()
+    else:
+        try:
+            array = np.asarray(audio, dtype=np.float32)
+        except (TypeError, ValueError) as exc:
+            raise TypeError(f"{what} audio of type {type(audio).__name__} is not a waveform of "
+                            "numbers") from exc
+    if array.ndim != 2 or not keep_channels:
+        array = array.reshape(-1)
+    return np.ascontiguousarray(array, dtype=_LITTLE_ENDIAN_F32)
 
 
-def audio_waveform_payload(audio: ArrayLike | torch.Tensor, *, sample_rate: int | None = None,
+def audio_waveform_payload(audio: Any, *, sample_rate: int | None = None,
                            modality: str | None = None, source_hint: str = "audio",
                            keep_channels: bool = False) -> dict[str, bytes | list[int] | str | int]:
-    """Serialize a waveform: float32 bytes, shape, dtype, and the optional rate / modality. A
-    (channels, samples) array keeps its shape with keep_channels; anything else is flattened."""
-    if isinstance(audio, torch.Tensor):
-        audio = audio.detach().float().cpu().numpy()
-    try:
-        array = np.asarray(audio, dtype=np.float32)
-        if not (keep_channels and array.ndim == 2):
-            array = array.reshape(-1)
-    except (TypeError, ValueError) as exc:
-        raise TypeError(f"Unsupported {source_hint} audio output type: {type(audio)}") from exc
-    array = np.ascontiguousarray(array)
+    """The wire payload of a waveform (a tensor, array or nested sequence of numbers);
+    ``source_hint`` names the producer in the error raised for anything else."""
+    samples = _samples(audio, keep_channels, source_hint)
     payload: dict[str, bytes | list[int] | str | int] = {
-        "audio_waveform": array.astype("<f4", copy=False).tobytes(),
-        "audio_waveform_shape": list(array.shape),
+        "audio_waveform": samples.tobytes(),
+        "audio_waveform_shape": [int(n) for n in samples.shape],
         "audio_waveform_dtype": "float32",
     }
-    if sample_rate is not None:
-        payload["sample_rate"] = int(sample_rate)
-    if modality is not None:
-        payload["modality"] = modality
+    for key, value in (("sample_rate", None if sample_rate is None else int(sample_rate)),
+                       ("modality", modality)):
+        if value is not None:
+            payload[key] = value
     return payload
 
 
-def build_audio_chunk_payload(audio_data: ArrayLike | torch.Tensor, *,
+def build_audio_chunk_payload(audio_data: Any, *,
                               sample_rate: int) -> dict[str, bytes | list[int] | str | int]:
-    """A streamed chunk's payload (modality "audio")."""
+    """A streamed chunk's payload: modality "audio" and its sample rate."""
     return audio_waveform_payload(audio_data, sample_rate=sample_rate, modality="audio",
                                   source_hint="streaming codec")
 
 
-__all__ = ["audio_data_uri_from_reference", "audio_waveform_payload",
-           "build_audio_chunk_payload"]
+__all__ = ["audio_waveform_payload", "build_audio_chunk_payload"]

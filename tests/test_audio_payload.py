@@ -1,4 +1,4 @@
-"""The audio payload wire format (sglang_omni/utils/audio_payload.py:13-65,
+"""The audio payload wire format (the keys built at sglang_omni/utils/audio_payload.py:23-65 and
 sglang_omni/scheduling/audio_stream.py:336-344) on the CPU."""
 
 from __future__ import annotations
@@ -7,11 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from sglang_omni_amd.utils.audio_payload import (
-    audio_data_uri_from_reference,
-    audio_waveform_payload,
-    build_audio_chunk_payload,
-)
+from sglang_omni_amd.utils.audio_payload import audio_waveform_payload, build_audio_chunk_payload
 
 
 def test_payload_fields_and_bytes():
@@ -40,17 +36,18 @@ def test_payload_keep_channels():
 
 
 def test_payload_rejects_non_numeric():
-    with pytest.raises(TypeError, match="Unsupported streaming codec audio output type"):
+    with pytest.raises(TypeError, match="streaming codec audio of type object"):
         build_audio_chunk_payload(object(), sample_rate=16000)
+
+
+def test_payload_of_lists_and_big_endian_arrays_is_little_endian_float32():
+    payload = audio_waveform_payload([[0.5, -1.0], [2.0, 0.25]], keep_channels=True)
+    assert payload["audio_waveform_shape"] == [2, 2]
+    assert payload["audio_waveform"] == np.array([0.5, -1.0, 2.0, 0.25], dtype="<f4").tobytes()
+    big = np.array([1.5, -2.0], dtype=">f8")
+    assert audio_waveform_payload(big)["audio_waveform"] == np.array([1.5, -2.0], "<f4").tobytes()
 
 
 def test_chunk_payload_modality():
     payload = build_audio_chunk_payload(torch.zeros(1, 1, 5), sample_rate=24000)
     assert payload["modality"] == "audio" and payload["sample_rate"] == 24000
-
-
-def test_data_uri():
-    assert audio_data_uri_from_reference({}) is None
-    assert audio_data_uri_from_reference({"data": "QUJD"}) == "data:audio/wav;base64,QUJD"
-    assert audio_data_uri_from_reference({"data": "QUJD", "media_type": "audio/ogg"}) == \
-        "data:audio/ogg;base64,QUJD"

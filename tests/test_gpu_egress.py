@@ -13,7 +13,6 @@ from oracle import codec_oracle as O
 from sglang_omni_amd import _native as N
 from sglang_omni_amd.kernels.egress import waveform_egress
 from sglang_omni_amd.scheduling import WaveformEgress
-from sglang_omni_amd.utils.cuda_staging import GrowablePinnedBuffer, PinnedTransferSlot
 
 pytestmark = pytest.mark.gpu
 
@@ -80,30 +79,12 @@ def test_egress_rejects_bad_arguments(gpu):
                                     N.stream_handle(w.device)) == N.INVALID_ARG
 
 
-def test_pinned_buffer_and_slot(gpu):
-    buf = GrowablePinnedBuffer(torch.float32, initial_capacity=10)
-    assert buf.capacity == 10 and buf.storage.is_pinned()
-    buf.ensure_capacity(4)
-    assert buf.capacity == 10
-    with pytest.raises(ValueError):
-        buf.view(11)
-    slot = PinnedTransferSlot(gpu, torch.float32, initial_capacity=8, blocking=True)
-    with pytest.raises(RuntimeError, match="not recorded"):
-        slot.query()
-    src = torch.arange(8, dtype=torch.float32, device=gpu)
-    slot.view(8).copy_(src, non_blocking=True)
-    slot.record(torch.cuda.current_stream(gpu))
-    slot.synchronize()
-    assert slot.query()
-    assert torch.equal(slot.view(8), src.cpu())
-
-
 @pytest.mark.parametrize("fmt", ["f32", "pcm16"])
 def test_waveform_egress_steps(gpu, fmt):
-    """Eight decode steps through a two-slot pool: every row's audio equals the oracle's
-    encoding of the waveform that step produced, in launch order, whether it completed by poll,
-    by flushing to free a slot, or at the final flush."""
-    egress = WaveformEgress(gpu, format=fmt, max_pinned_slots=2)
+    """Eight decode steps through a two-entry ring: every row's audio equals the oracle's
+    encoding of the waveform that step produced, in step order, whether it left by poll, to
+    free its ring entry for a later step, or at the final flush."""
+    egress = WaveformEgress(gpu, format=fmt, depth=2)
     expected: dict[str, np.ndarray] = {}
     got: dict[str, np.ndarray] = {}
     order: list[str] = []
@@ -126,12 +107,59 @@ def test_waveform_egress_steps(gpu, fmt):
         assert audio.dtype == (np.int16 if fmt == "pcm16" else np.float32)
         assert np.array_equal(audio.view(np.int16 if fmt == "pcm16" else np.int32),
                               expected[rid].view(np.int16 if fmt == "pcm16" else np.int32))
-    assert egress.pinned_created <= 2 and not egress.pending
+    assert egress.in_flight == 0 and egress.steps == egress.delivered == 8
+    assert all(e.host is None or e.host.is_pinned() for e in egress.ring)
 
 
-def test_waveform_egress_without_slots_copies_synchronously(gpu):
-    egress = WaveformEgress(gpu, max_pinned_slots=0)
+def test_waveform_egress_without_a_ring_copies_synchronously(gpu):
+    egress = WaveformEgress(gpu, depth=0)
     w = _wave(2, 100, 3)
     ready = egress.stage_step(["a", "b"], w.to(gpu))
-    assert [rid for rid, _ in ready] == ["a", "b"] and not egress.pending
+    assert [rid for rid, _ in ready] == ["a", "b"] and egress.in_flight == 0
     assert np.array_equal(ready[1][1].view(np.int32), w[1, 0].numpy().view(np.int32))
+
+
+def test_a_ring_entry_is_reused_only_after_its_step_left(gpu):
+    """Step n waits for step n - depth: with depth 3 the fourth step's staging delivers the
+    first, and the buffers grow only between transfers."""
+    egress = WaveformEgress(gpu, depth=3)
+    waves = [_wave(2, 64 * (k + 1), 10 + k) for k in range(4)]
+    assert egress.stage_step(["a0", "b0"], waves[0].to(gpu)) == []
+    egress.stage_step(["a1", "b1"], waves[1].to(gpu))
+    egress.stage_step(["a2", "b2"], waves[2].to(gpu))
+    assert egress.in_flight == 3
+    out = egress.stage_step(["a3", "b3"], waves[3].to(gpu))  # entry 0 again: step 0 leaves
+    assert [rid for rid, _ in out] == ["a0", "b0"]
+    assert np.array_equal(out[0][1].view(np.int32), waves[0][0, 0].numpy().view(np.int32))
+    rest = egress.flush()
+    assert [rid for rid, _ in rest] == ["a1", "b1", "a2", "b2", "a3", "b3"]
+    assert np.array_equal(rest[-1][1].view(np.int32), waves[3][1, 0].numpy().view(np.int32))
+    assert egress.ring[0].host.numel() >= 2 * 64 * 4
+
+
+def test_a_failed_transfer_sets_its_buffer_aside_and_goes_synchronous(gpu, monkeypatch):
+    """The failure is forced on the host (the event record raises): the step's buffer is kept
+    out of the ring for good, the steps already in flight still arrive in order, and later steps
+    are copied synchronously."""
+    egress = WaveformEgress(gpu, depth=2)
+    w = [_wave(1, 80, 20 + k) for k in range(3)]
+    egress.stage_step(["x"], w[0].to(gpu))
+    real_event = torch.cuda.Event
+
+    class FailingEvent:
+        def __init__(self, *args, **kwargs):
+            pass
+
+        def record(self, stream=None):
+            raise RuntimeError("record refused")
+
+    monkeypatch.setattr(torch.cuda, "Event", FailingEvent)
+    with pytest.raises(RuntimeError, match="record refused"):
+        egress.stage_step(["y"], w[1].to(gpu))
+    monkeypatch.setattr(torch.cuda, "Event", real_event)
+    assert not egress.overlapped and len(egress.set_aside) == 1
+    assert egress.ring[1].host is None
+    out = egress.stage_step(["z"], w[2].to(gpu))
+    assert [rid for rid, _ in out] == ["x", "z"]
+    assert np.array_equal(out[1][1].view(np.int32), w[2][0, 0].numpy().view(np.int32))
+    assert egress.in_flight == 0

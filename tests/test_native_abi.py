@@ -96,7 +96,7 @@ def test_channel_embedding_tables_refuse_host_tables():
     tables = ChannelEmbeddingTables()
     weights = [torch.zeros(4, 8, dtype=torch.bfloat16) for _ in range(3)]
     assert not tables.refresh(weights)
-    assert tables.weight_pointer_tensor is None
+    assert tables._table_info is None
     try:
         tables.embed(torch.zeros(2, 3, dtype=torch.int64), weights)
     except N.OmniCodecError:

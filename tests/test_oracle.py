@@ -624,3 +624,98 @@ def test_channel_embedding_sum_pins():
     got = O.channel_embedding_sum(inr[:, :2], bt)
     ref = (bt[0][inr[:, 0]].float() + bt[1][inr[:, 1]].float()).to(torch.bfloat16)
     assert torch.equal(got, ref)
+
+
+# ------------------------------------------------------------------------------------------
+# The whole DAC decoder composition against transformers' DacDecoder
+# ------------------------------------------------------------------------------------------
+
+
+def _tf_dac_decoder(seed: int):
+    """transformers' DacDecoder (the dac library's decoder restated: conv -> blocks of Snake ->
+    ConvTranspose -> residual units -> Snake -> conv -> tanh, non-causal padding) with random
+    Snake alphas and conv weights scaled to keep the output inside tanh's linear range."""
+    from transformers.models.dac.configuration_dac import DacConfig
+    from transformers.models.dac.modeling_dac import DacDecoder
+
+    cfg = DacConfig(hidden_size=12, decoder_hidden_size=32, upsampling_ratios=[2, 3, 4])
+    torch.manual_seed(seed)
+    dec = DacDecoder(cfg).eval()
+    gen = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for m in dec.modules():
+            if hasattr(m, "alpha"):
+                m.alpha.copy_(torch.rand(m.alpha.shape, generator=gen) * 1.5 + 0.3)
+            if isinstance(m, (torch.nn.Conv1d, torch.nn.ConvTranspose1d)):
+                fan_in = m.weight.shape[1 if isinstance(m, torch.nn.Conv1d) else 0] * m.weight.shape[2]
+                m.weight.copy_(torch.randn(m.weight.shape, generator=gen) * 0.7 / math.sqrt(fan_in))
+                m.bias.copy_(torch.randn(m.bias.shape, generator=gen) * 0.05)
+    return dec
+
+
+def _weights_of_tf_decoder(dec) -> dict:
+    """The oracle's weight tree of a transformers DacDecoder, read attribute by attribute."""
+
+    def conv(m):
+        return {"weight": m.weight.detach().clone(), "bias": m.bias.detach().clone()}
+
+    def alpha(m):
+        return m.alpha.detach().reshape(-1).clone()
+
+    blocks = []
+    for blk in dec.block:
+        units = [{"alpha1": alpha(ru.snake1), "conv1": conv(ru.conv1),
+                  "dilation": ru.conv1.dilation[0], "alpha2": alpha(ru.snake2),
+                  "conv2": conv(ru.conv2)}
+                 for ru in (blk.res_unit1, blk.res_unit2, blk.res_unit3)]
+        blocks.append({"alpha": alpha(blk.snake1), "up": conv(blk.conv_t1),
+                       "stride": blk.conv_t1.stride[0], "units": units})
+    return {"in_conv": conv(dec.conv1), "blocks": blocks,
+            "final": {"alpha": alpha(dec.snake1), "conv": conv(dec.conv2)}}
+
+
+def test_dac_decoder_composition_matches_transformers_dac_decoder():
+    """dac_decoder(padding="same") equals DacDecoder end to end (float64 activations on both
+    sides, odd and even strides, the odd one giving T * s - 1 samples); the causal mode runs the
+    same composition with the causal pad / trim rules pinned by the conv tests above. The only
+    difference is the oracle's float32 Snake coefficient 1 / (alpha + 1e-9), as the reference's
+    float32 Snake1d computes it: a relative 1e-7 per Snake, far below any composition mistake
+    (the mutation test below)."""
+    dec = _tf_dac_decoder(80).double()
+    weights = _weights_of_tf_decoder(dec)
+    z = torch.randn(2, 12, 9, generator=torch.Generator().manual_seed(81), dtype=torch.float64)
+    with torch.no_grad():
+        expected = dec(z)
+    ours = O.dac_decoder(z, weights, padding="same")
+    assert ours.shape == expected.shape == (2, 1, ((9 * 2) * 3 - 1) * 4)
+    rms = expected.pow(2).mean().sqrt().item()
+    assert 0.02 < rms < 0.5, rms  # inside tanh's linear range, far from zero
+    torch.testing.assert_close(ours, expected, rtol=1e-6, atol=1e-7)
+    causal = O.dac_decoder(z, weights)
+    assert causal.shape == (2, 1, 9 * 2 * 3 * 4)
+
+
+@pytest.mark.parametrize("mutation", ["no_final_snake", "no_tanh", "units_reordered",
+                                      "no_block_snake", "blocks_share_alpha"])
+def test_the_decoder_pin_fails_for_a_miscomposed_decoder(mutation):
+    """Each plausible composition mistake, made on the reference side, moves the output far
+    outside the pin's tolerance: the pin would catch the same mistake in the oracle."""
+    dec = _tf_dac_decoder(82).double()
+    weights = _weights_of_tf_decoder(dec)
+    z = torch.randn(1, 12, 7, generator=torch.Generator().manual_seed(83), dtype=torch.float64)
+    with torch.no_grad():
+        if mutation == "no_final_snake":
+            dec.snake1 = torch.nn.Identity()
+        elif mutation == "no_tanh":
+            dec.tanh = torch.nn.Identity()
+        elif mutation == "units_reordered":
+            b = dec.block[1]
+            b.res_unit1, b.res_unit2 = b.res_unit2, b.res_unit1
+        elif mutation == "no_block_snake":
+            dec.block[2].snake1 = torch.nn.Identity()
+        else:
+            dec.block[0].snake1.alpha.copy_(dec.block[0].snake1.alpha.mean().expand_as(
+                dec.block[0].snake1.alpha))
+        mutated = dec(z)
+    ours = O.dac_decoder(z, weights, padding="same")
+    assert (ours - mutated).abs().max().item() > 1e-4
