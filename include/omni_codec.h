@@ -36,8 +36,12 @@
  *   omni_bias_snake_beta         fused_bias_snake_beta (sglang_omni/kernels/bias_snake_beta.py:
  *                                102-151)
  *   omni_snake                   snake_channels_last_kernel (sglang_omni/models/fishaudio_drama3/
- *                                channels_last_decoder.py:35-67,157-184) and fused_snake_beta
- *                                (sglang_omni/utils/snake_beta.py:200-234)
+ *                                channels_last_decoder.py:35-67,157-184)
+ *   omni_snake_beta              fused_snake_beta's launch (sglang_omni/utils/snake_beta.py:
+ *                                164-234) with its bitwise eager-chain contract
+ *   omni_conv1d_general          channels_last_conv1d / channels_last_conv_transpose1d
+ *                                (sglang_omni/utils/channels_last_conv.py:45-120) for grouped,
+ *                                strided, padded or odd-channel convs and float32 / fp16
  *   omni_advance_slots           pool.frame_positions.index_put_ at the end of decode_slots
  *                                (sglang_omni/models/qwen3_omni/components/code2wav.py:459)
  *   omni_codec_capabilities      no kernel counterpart; the platform query of
@@ -400,6 +404,42 @@ int omni_bias_snake_beta(const void* conv, int64_t conv_stride_b, int64_t batch,
 int omni_snake(const void* x, void* y, int dtype, int64_t batch, int64_t frames,
                int64_t channels, int channels_last, const float* a, const float* b,
                int round_intermediates, omni_stream_t stream);
+
+/*
+ * fused_snake_beta with the module's parameters (sglang_omni/utils/snake_beta.py:200-234): alpha
+ * and beta are SnakeBeta's log-scale [channels] parameters in x's dtype (bf16 or f16), read on the
+ * device at every launch, eps its no_div_by_zero; every op of the eager chain rounds to the dtype:
+ *   a = exp(alpha), e = exp(beta), t = e + eps, r = 1 / t, y = x + r * sin(x * a)^2.
+ * x is [B, C, T] contiguous (channels_last = 0) or the [B, C, T] view of a contiguous [B, T, C]
+ * (channels_last = 1); y has x's layout and must not overlap it.
+ */
+int omni_snake_beta(const void* x, void* y, int dtype, int64_t batch, int64_t channels,
+                    int64_t frames, int channels_last, const void* alpha, const void* beta,
+                    int param_dtype, float eps, omni_stream_t stream);
+
+/*
+ * Conv1d / ConvTranspose1d of channels-last activations in the general form of the reference's
+ * channels-last conv API (sglang_omni/utils/channels_last_conv.py:45-120), for what the MFMA
+ * kernel does not take: any channel counts, groups, stride, dilation and zero padding, float32,
+ * bf16 or f16 activations, weights and bias of that dtype, float32 accumulation (taps ascending,
+ * then the group's input channels), one rounding to the dtype:
+ *   conv        y[b, i, co] = bias[co] + sum_{j, c} W[co, c, j] x[b, i * stride + j * dilation -
+ *               pad_left, g * C_in / groups + c]
+ *   transposed  y[b, i, co] = bias[co] + sum_{j, c} W[g * C_in / groups + c, co - g * C_out /
+ *               groups, j] x[b, q, g * C_in / groups + c] over q * stride + j * dilation = i +
+ *               pad_left
+ * with g = co / (C_out / groups) and inputs outside [0, length_in) zero. x, W and y at the given
+ * element strides (W in the module's layout: [C_out, C_in / groups, k] for a conv, [C_in,
+ * C_out / groups, k] for a transposed conv); y must not overlap x.
+ */
+int omni_conv1d_general(const void* x, int dtype, int64_t batch, int64_t length_in, int64_t c_in,
+                        int64_t x_stride_b, int64_t x_stride_t, int64_t x_stride_c,
+                        const void* weight, int64_t taps, int64_t weight_stride0,
+                        int64_t weight_stride1, int64_t weight_stride2, const void* bias,
+                        int64_t c_out, int64_t groups, int64_t stride, int64_t dilation,
+                        int64_t pad_left, int transposed, void* y, int64_t length_out,
+                        int64_t y_stride_b, int64_t y_stride_t, int64_t y_stride_c,
+                        omni_stream_t stream);
 
 /* slot_parity[slot_index[r]] += 1 for r < rows whose slot is in [0, num_slots), ending a decode
    step (graph-capturable). */

@@ -76,6 +76,32 @@ __global__ void snake_kernel(const void* x, void* y, int64_t n, int64_t channels
   st<DT>(y, idx, out);
 }
 
+// SnakeBeta from the module's raw log-scale parameters, read at every launch (a captured graph
+// sees the parameters' current values), with the eager op chain's rounding in DT:
+//   a = rnd(exp(alpha)), e = rnd(exp(beta)), t = rnd(e + eps), r = rnd(1 / t)
+//   y = rnd(x + rnd(r * rnd(rnd(sin(rnd(x * a)))^2)))
+// Layout: [B, C, T] contiguous, or (channels_last) its [B, T, C] transpose contiguous; y has
+// x's layout. Each thread takes consecutive elements of one row, so loads and stores coalesce
+// in both layouts.
+template <int DT, int PDT>
+__global__ void __launch_bounds__(256) snake_beta_params_kernel(
+    const void* x, void* y, int64_t n, int64_t channels, int64_t frames, int channels_last,
+    const void* alpha, const void* beta, float eps) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int64_t c = channels_last ? idx % channels : (idx / frames) % channels;
+  const float a = rnd<DT>(expf(ld<PDT>(alpha, c)));
+  const float e = rnd<DT>(expf(ld<PDT>(beta, c)));
+  const float t = rnd<DT>(e + eps);
+  const float r = rnd<DT>(1.0f / t);
+  const float v = ld<DT>(x, idx);
+  const float phase = rnd<DT>(v * a);
+  const float sine = rnd<DT>(sinf(phase));
+  const float sq = rnd<DT>(sine * sine);
+  const float scaled = rnd<DT>(r * sq);
+  st<DT>(y, idx, v + scaled);
+}
+
 bool half_like(int dt) { return dt == OMNI_DTYPE_BF16 || dt == OMNI_DTYPE_F16; }
 
 template <int DT>
@@ -145,6 +171,30 @@ extern "C" int omni_snake(const void* x, void* y, int dtype, int64_t batch, int6
   else
     hipLaunchKernelGGL(snake_kernel<OMNI_DTYPE_F16>, grid, block, 0, s, x, y, n, channels, frames,
                        channels_last, a, b, round_intermediates);
+  OMNI_LAUNCH_CHECK();
+  return OMNI_OK;
+}
+
+extern "C" int omni_snake_beta(const void* x, void* y, int dtype, int64_t batch, int64_t channels,
+                               int64_t frames, int channels_last, const void* alpha,
+                               const void* beta, int param_dtype, float eps,
+                               omni_stream_t stream) {
+  if (!x || !y || !alpha || !beta) return OMNI_ERR_INVALID_ARG;
+  if (!half_like(dtype) || param_dtype != dtype) return OMNI_ERR_INVALID_ARG;
+  if (batch < 0 || frames < 0 || channels < 1) return OMNI_ERR_INVALID_ARG;
+  const int64_t n = batch * frames * channels;
+  if (n == 0) return OMNI_OK;
+  const int64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == OMNI_DTYPE_BF16)
+    hipLaunchKernelGGL((snake_beta_params_kernel<OMNI_DTYPE_BF16, OMNI_DTYPE_BF16>),
+                       dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, channels, frames,
+                       channels_last, alpha, beta, eps);
+  else
+    hipLaunchKernelGGL((snake_beta_params_kernel<OMNI_DTYPE_F16, OMNI_DTYPE_F16>),
+                       dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, channels, frames,
+                       channels_last, alpha, beta, eps);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
 }

@@ -193,6 +193,11 @@ SIGNATURES: dict[str, list] = {
     "omni_bias_snake_beta": [_PTR, _I64, _I64, _I64, _I64, _PTR, _PTR, _PTR, _INT, _PTR, _PTR,
                              _PTR, _I64, _INT, _PTR],
     "omni_snake": [_PTR, _PTR, _INT, _I64, _I64, _I64, _INT, _PTR, _PTR, _INT, _PTR],
+    "omni_snake_beta": [_PTR, _PTR, _INT, _I64, _I64, _I64, _INT, _PTR, _PTR, _INT, ctypes.c_float,
+                        _PTR],
+    "omni_conv1d_general": [_PTR, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _PTR, _I64, _I64, _I64,
+                            _I64, _PTR, _I64, _I64, _I64, _I64, _I64, _INT, _PTR, _I64, _I64, _I64,
+                            _I64, _PTR],
     "omni_advance_slots": [_PTR, _I64, _PTR, _I64, _PTR],
     "omni_short_time_spectrum": [_PTR, _I64, _I64, _I64, _INT, _PTR, _I64, _I64, _I64, _PTR, _I64,
                                  _PTR],

@@ -70,32 +70,42 @@ def _chunked(w: torch.Tensor) -> torch.Tensor:
     return padded.view(n_cols, taps, chunks, CHUNK).permute(2, 0, 1, 3).contiguous()
 
 
-def polyphase_taps(weight: torch.Tensor, stride: int, padding: int) -> tuple[torch.Tensor, int]:
-    """A ConvTranspose1d weight [C_in, C_out, k] of stride s and padding p as the stride-one
-    weight [s*C_out, taps, C_in] over the input: output s*i + r takes input i + delta through tap
-    j = j0 + s*m (j0 = (r + p) mod s, delta = floor((r + p)/s) - m). Returns (weight, left_pad)."""
+def polyphase_taps(weight: torch.Tensor, stride: int, padding: int,
+                   dilation: int = 1) -> tuple[torch.Tensor, int]:
+    """A ConvTranspose1d weight [C_in, C_out, k] of stride s, padding p and dilation d as the
+    stride-one weight [s*C_out, taps, C_in] over the input: output s*i + r is the transposed
+    conv's sample s*i + r + p, which input q reaches through tap j when q*s + j*d = s*i + r + p,
+    i.e. q = i + delta with delta = (r + p - j*d) / s for the taps j that make it whole.
+    Returns (weight, left_pad) with tap index delta - min(delta)."""
     c_in, c_out, k = weight.shape
     s = stride
     entries = []  # (r, delta, j)
     for r in range(s):
-        j0 = (r + padding) % s
-        c_r = (r + padding) // s
-        m = 0
-        while j0 + s * m < k:
-            entries.append((r, c_r - m, j0 + s * m))
-            m += 1
+        for j in range(k):
+            num = r + padding - j * dilation
+            if num % s == 0:
+                entries.append((r, num // s, j))
+    if not entries:
+        raise ValueError("no tap reaches any output phase")
     d_min = min(e[1] for e in entries)
     d_max = max(e[1] for e in entries)
     taps = d_max - d_min + 1
     out = torch.zeros(s * c_out, taps, c_in, dtype=weight.dtype, device=weight.device)
     wt = weight.permute(1, 0, 2)  # [C_out, C_in, k]
     for r, delta, j in entries:
-        out[r * c_out:(r + 1) * c_out, delta - d_min, :] = wt[:, :, j]
+        out[r * c_out:(r + 1) * c_out, delta - d_min, :] += wt[:, :, j]
     return out, -d_min
 
 
 def _finish(w_ntc: torch.Tensor, bias: torch.Tensor | None, *, c_in: int, c_out: int, taps: int,
-            dilation: int, left_pad: int, phases: int, fp8: bool) -> PackedConv:
+            dilation: int, left_pad: int, phases: int, fp8: bool,
+            scale: torch.Tensor | None = None) -> PackedConv:
+    if fp8 and scale is not None:
+        # an E4M3 weight with its per-output-channel scale (held exactly in float32 here)
+        q = w_ntc.to(torch.float8_e4m3fn)
+        scale_n = scale.float().reshape(c_out).repeat(phases).contiguous()
+        return PackedConv(_chunked(q), scale_n, None if bias is None else bias.float(), c_in,
+                          c_out, phases * c_out, taps, dilation, left_pad, phases)
     if fp8:
         # per-output-channel scales (shared by every phase of a transposed conv's channel)
         w = w_ntc.float().contiguous()
@@ -111,26 +121,38 @@ def _finish(w_ntc: torch.Tensor, bias: torch.Tensor | None, *, c_in: int, c_out:
 
 
 def pack_conv1d(weight: torch.Tensor, bias: torch.Tensor | None, *, dilation: int = 1,
-                causal: bool = True, fp8: bool = False) -> PackedConv:
+                causal: bool = True, fp8: bool = False,
+                scale: torch.Tensor | None = None) -> PackedConv:
     """Conv1d weight [C_out, C_in, k]: causal (left pad (k-1)*d, ``CausalConvNet``,
-    modded_dac.py:541-572) or 'same' (pad (k*d-d)//2, hift_layers.py:67-92)."""
+    modded_dac.py:541-572) or 'same' (pad (k*d-d)//2, hift_layers.py:67-92). An E4M3 weight
+    comes with its float32 ``scale`` per output channel and is packed as it is."""
     c_out, c_in, k = weight.shape
     left = (k - 1) * dilation if causal else (k * dilation - dilation) // 2
+    if weight.dtype == torch.float8_e4m3fn:
+        if scale is None:
+            raise ValueError("an E4M3 weight needs its per-output-channel scale")
+        fp8, weight = True, weight.float()  # E4M3 values are exact in float32
     packed = _finish(weight.permute(0, 2, 1), bias, c_in=c_in, c_out=c_out, taps=k,
-                     dilation=dilation, left_pad=left, phases=1, fp8=fp8)
+                     dilation=dilation, left_pad=left, phases=1, fp8=fp8, scale=scale)
     packed.macs_per_position = c_out * c_in * k
     return packed
 
 
 def pack_conv_transpose1d(weight: torch.Tensor, bias: torch.Tensor | None, *, stride: int,
-                          padding: int = 0, fp8: bool = False) -> PackedConv:
-    """ConvTranspose1d weight [C_in, C_out, k] in its polyphase form. ``padding = 0`` with a
-    right trim of k - s is ``CausalTransConvNet`` (modded_dac.py:583-600); ``padding = (k-s)//2``
-    is the HiFT upsampler (hift.py:143-156). Either way L inputs give L*s outputs."""
+                          padding: int = 0, dilation: int = 1, fp8: bool = False,
+                          scale: torch.Tensor | None = None) -> PackedConv:
+    """ConvTranspose1d weight [C_in, C_out, k] in its polyphase form (output position i holds
+    the transposed conv's samples s*i + p .. s*i + p + s - 1). ``padding = 0`` with a right trim
+    of k - s is ``CausalTransConvNet`` (modded_dac.py:583-600); ``padding = (k-s)//2`` is the HiFT
+    upsampler (hift.py:143-156)."""
     c_in, c_out, k = weight.shape
-    w, left = polyphase_taps(weight, stride, padding)
+    if weight.dtype == torch.float8_e4m3fn:
+        if scale is None:
+            raise ValueError("an E4M3 weight needs its per-output-channel scale")
+        fp8, weight = True, weight.float()  # E4M3 values are exact in float32
+    w, left = polyphase_taps(weight, stride, padding, dilation)
     packed = _finish(w, bias, c_in=c_in, c_out=c_out, taps=w.shape[1], dilation=1,
-                     left_pad=left, phases=stride, fp8=fp8)
+                     left_pad=left, phases=stride, fp8=fp8, scale=scale)
     packed.macs_per_position = c_out * c_in * k  # every input sample meets all k taps
     return packed
 

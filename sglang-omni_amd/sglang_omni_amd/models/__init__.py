@@ -15,6 +15,7 @@ from .configs import (
     make_qwen3_code2wav_weights,
 )
 from .dac_codec import CodecStatePool, DacCodecDecoder
+from .dac_weights import dac_weight_tree
 from .graph_runner import CodecGraphRunner, GraphKey
 from .hifigan import HifiGanVocoder
 from .qwen3_code2wav import (
@@ -45,5 +46,6 @@ __all__ = [
     "Qwen3TTSCodecState",
     "make_dac_weights",
     "make_hifigan_weights",
+    "dac_weight_tree",
     "make_qwen3_code2wav_weights",
 ]

@@ -209,13 +209,17 @@ class DacCodecDecoder:
                           if "codebooks" in ref else None)
         self.num_codebooks = None if self.codebooks is None else self.codebooks.shape[0]
 
+        # fp8: a float weight is quantized per output channel here; an E4M3 weight (a
+        # checkpoint's, see quantization.fp8_conv_weight) is packed with its own scale
         def conv1d(src: dict, rsrc: dict, dilation: int = 1) -> PackedConv:
             w = src["weight"] if fp8 else rsrc["weight"]
-            return pack_conv1d(w, rsrc["bias"], dilation=dilation, fp8=fp8).to(dev)
+            return pack_conv1d(w, rsrc["bias"], dilation=dilation, fp8=fp8,
+                               scale=src.get("weight_scale") if fp8 else None).to(dev)
 
         def convt(src: dict, rsrc: dict, stride: int) -> PackedConv:
             w = src["weight"] if fp8 else rsrc["weight"]
-            return pack_conv_transpose1d(w, rsrc["bias"], stride=stride, fp8=fp8).to(dev)
+            return pack_conv_transpose1d(w, rsrc["bias"], stride=stride, fp8=fp8,
+                                         scale=src.get("weight_scale") if fp8 else None).to(dev)
 
         blocks_w, blocks_r = weights["blocks"], ref["blocks"]
         a0, b0 = _snake_coefficients(blocks_r[0]["alpha"], dev)
@@ -311,7 +315,8 @@ class DacCodecDecoder:
     def _view(flat: torch.Tensor, batch: int, length: int, channels: int) -> torch.Tensor:
         return flat[: batch * length * channels].view(batch, length, channels)
 
-    def _decode(self, codes: torch.Tensor, state: dict | None) -> torch.Tensor:
+    def _decode(self, codes: torch.Tensor, state: dict | None, *,
+                latents: bool = False) -> torch.Tensor:
         if codes.dim() != 3:
             raise ValueError(f"codes must be [B, Q, T], got {tuple(codes.shape)}")
         batch, _, frames = codes.shape
@@ -333,7 +338,12 @@ class DacCodecDecoder:
 
         timer = self.timer
         snake = N.ACT_SNAKE
-        z, length = self._front(codes, ws, state)
+        if latents:
+            # layout / dtype plumbing of the caller's [B, D, T] latents: the input conv's
+            # channels-last bf16 operand
+            z, length = codes.transpose(1, 2).to(torch.bfloat16).contiguous(), frames
+        else:
+            z, length = self._front(codes, ws, state)
         # the whole decode and a stream's first decode drop each transposed conv's first s
         # samples when the decoder trims both sides
         trim = self.trim_first and (state is None or state["cold"])
@@ -438,6 +448,12 @@ class DacCodecDecoder:
                state: dict | None) -> tuple[torch.Tensor, int]:
         """The input conv's operand [B, L, C] bf16 and L: the RVQ gather-sum of the codes."""
         batch, _, frames = codes.shape
+        if self.codebooks is None:
+            raise ValueError("this decoder has no codebooks (its quantizer does more than a "
+                             "gather-sum): decode its latents with decode(z)")
+        if ws.z is None:
+            ws.z = torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16,
+                               device=self.device)
         k_books, _, dim = self.codebooks.shape
         rvq_bytes = batch * frames * (k_books * dim * 2 + dim * 2 + k_books * codes.element_size())
         with self.timer.launch("rvq", rvq_bytes):
@@ -485,6 +501,27 @@ class DacCodecDecoder:
         return torch.cat(parts, dim=-1)
 
     __call__ = from_indices
+
+    @torch.no_grad()
+    def decode(self, z: torch.Tensor) -> torch.Tensor:
+        """[B, D, T] latents -> [B, 1, T * frame_length] float32 waveform: the decoder without
+        the quantizer (``DAC.decode``, modded_dac.py:1004-1020). Long inputs decode in chunks
+        through slot state, which gives the same bits."""
+        if z.dim() != 3 or z.shape[1] != self.in_conv.conv.c_in:
+            raise ValueError(f"latents must be [B, {self.in_conv.conv.c_in}, T], got "
+                             f"{tuple(z.shape)}")
+        if not z.is_floating_point():
+            raise ValueError(f"latents must be floating point, got {z.dtype}")
+        batch, _, frames = z.shape
+        step = self.frames_per_call(batch)
+        if frames <= step:
+            return self._decode(z, None, latents=True)
+        pool = self.new_state_pool(num_slots=batch)
+        rows = torch.arange(batch, device=self.device)
+        parts = [self._decode(z[..., s:s + step], {"pool": pool, "slot_index": rows,
+                                                   "cold": s == 0}, latents=True)
+                 for s in range(0, frames, step)]
+        return torch.cat(parts, dim=-1)
 
     def _check_distinct_slots(self, slot_index: torch.Tensor) -> None:
         """Rows naming one slot twice would race on its history and parity: refuse them. The

@@ -8,6 +8,13 @@ kernel dequantizes them to bf16 in LDS and applies ``s`` in its epilogue (W8A16 
 ``reference_weights`` returns the float32 weights a decoder with a given weight format actually
 multiplies by (bf16-rounded, or fp8-dequantized), which is what a float32 reference of that
 decoder must use.
+
+Checkpoints that already hold E4M3 weights carry a dequantization multiplier named
+``weight_scale_inv`` (per tensor, per output channel, or per [rows x cols] block of the weight
+flattened to [C_out, C_in * k]); ``fp8_conv_weight`` maps one onto this module's format, with the
+reference's checks and its optional reciprocal (sglang_omni/quantization.py:137-166,
+``convert_fp8_weight_scale_inv``). A conv dict of a weight tree may then hold the E4M3 ``weight``
+with its ``weight_scale`` [C_out], which the decoders pack as they are.
 """
 
 from __future__ import annotations
@@ -34,6 +41,57 @@ def dequantize_fp8(q: torch.Tensor, scale: torch.Tensor, channel_dim: int) -> to
     return q.float() * scale.view(shape)
 
 
+def checkpoint_fp8_multiplier(name: str, scale: torch.Tensor, *, inverted: bool) -> torch.Tensor:
+    """A checkpoint's ``weight_scale_inv`` as the float32 multiplier that dequantizes its E4M3
+    weight, refusing what the reference's loader refuses: a non-floating-point, empty,
+    non-finite or zero scale. ``inverted`` checkpoints store the multiplier's reciprocal."""
+    if not torch.is_floating_point(scale):
+        raise TypeError(f"FP8 scale tensor for {name} must be floating point")
+    if scale.numel() == 0:
+        raise ValueError(f"FP8 scale tensor for {name} is empty")
+    if not bool(torch.isfinite(scale).all()):
+        raise ValueError(f"FP8 scale tensor for {name} holds non-finite values")
+    if bool((scale == 0).any()):
+        raise ValueError(f"FP8 scale tensor for {name} holds zeros")
+    scale = scale.detach().float()
+    return scale.reciprocal() if inverted else scale
+
+
+def fp8_conv_weight(name: str, weight: torch.Tensor, scale_inv: torch.Tensor, *,
+                    inverted: bool = False, block_size: tuple[int, int] | None = None,
+                    transposed: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """(E4M3 weight, float32 scale per output channel) for the conv kernels from a checkpoint's
+    E4M3 conv weight ([C_out, C_in, k], or [C_in, C_out, k] when ``transposed``) and its
+    ``weight_scale_inv``: a scalar, one value per output channel, or (Conv1d only, with
+    ``block_size`` = (rows, cols)) one per block of the weight viewed as [C_out, C_in * k].
+    Per-tensor and per-channel multipliers, and blocks whose multipliers are constant along each
+    row of blocks, map exactly; other block layouts are dequantized and requantized per output
+    channel (one E4M3 rounding)."""
+    if weight.dtype != torch.float8_e4m3fn or weight.dim() != 3:
+        raise ValueError(f"{name}: expected a 3-dimensional float8_e4m3fn conv weight")
+    m = checkpoint_fp8_multiplier(name, scale_inv, inverted=inverted)
+    ch_dim = 1 if transposed else 0
+    c_out = weight.shape[ch_dim]
+    if m.numel() == 1:
+        return weight, m.reshape(1).expand(c_out).contiguous()
+    if block_size is None:
+        if m.numel() != c_out:
+            raise ValueError(f"{name}: {m.numel()} scales for {c_out} output channels")
+        return weight, m.reshape(c_out).contiguous()
+    if transposed:
+        raise ValueError(f"{name}: block scales are read for Conv1d weights only")
+    rows, cols = block_size
+    flat = weight.reshape(c_out, -1)
+    blocks = (-(-c_out // rows), -(-flat.shape[1] // cols))
+    if tuple(m.shape) != blocks:
+        raise ValueError(f"{name}: block scales of shape {tuple(m.shape)}, expected {blocks}")
+    if bool((m == m[:, :1]).all()):
+        return weight, m[:, 0].repeat_interleave(rows)[:c_out].contiguous()
+    full = m.repeat_interleave(rows, 0)[:c_out].repeat_interleave(cols, 1)[:, :flat.shape[1]]
+    dense = (flat.float() * full).reshape(weight.shape)
+    return quantize_fp8(dense, 0)
+
+
 def _map_convs(weights: dict[str, Any], fn) -> dict[str, Any]:
     """Apply fn(conv_dict, kind) to every conv of a DAC or HiFiGAN weight tree; copies the rest."""
 
@@ -50,13 +108,22 @@ def _map_convs(weights: dict[str, Any], fn) -> dict[str, Any]:
     return walk(weights, None)
 
 
+def _float_weight(node: dict[str, Any], kind: str) -> torch.Tensor:
+    """A conv dict's weight as float32 values: an E4M3 weight dequantized by its
+    ``weight_scale`` (per output channel)."""
+    w = node["weight"]
+    if w.dtype == torch.float8_e4m3fn:
+        return dequantize_fp8(w, node["weight_scale"], 1 if kind == "transpose" else 0)
+    return w
+
+
 def round_bf16(weights: dict[str, Any]) -> dict[str, Any]:
     """The weight tree with every conv weight and bias, and the codebooks, rounded to bf16
     (kept as float32 values). Snake alphas stay float32."""
 
     def conv(node: dict[str, Any], kind: str) -> dict[str, Any]:
-        out = dict(node)
-        out["weight"] = node["weight"].to(torch.bfloat16).float()
+        out = {k: v for k, v in node.items() if k != "weight_scale"}
+        out["weight"] = _float_weight(node, kind).to(torch.bfloat16).float()
         if node.get("bias") is not None:
             out["bias"] = node["bias"].to(torch.bfloat16).float()
         return out
@@ -68,14 +135,18 @@ def round_bf16(weights: dict[str, Any]) -> dict[str, Any]:
 
 
 def fp8_dequantized(weights: dict[str, Any]) -> dict[str, Any]:
-    """The weight tree with every conv weight replaced by its fp8 per-output-channel
-    quantize -> dequantize round trip (biases bf16-rounded; codebooks bf16-rounded)."""
+    """The weight tree with every conv weight replaced by the values its fp8 form holds: the
+    per-output-channel quantize -> dequantize round trip of a float weight, or an E4M3 weight
+    dequantized by its own scale (biases bf16-rounded; codebooks bf16-rounded)."""
 
     def conv(node: dict[str, Any], kind: str) -> dict[str, Any]:
-        out = dict(node)
+        out = {k: v for k, v in node.items() if k != "weight_scale"}
         dim = 1 if kind == "transpose" else 0
-        q, s = quantize_fp8(node["weight"], dim)
-        out["weight"] = dequantize_fp8(q, s, dim)
+        if node["weight"].dtype == torch.float8_e4m3fn:
+            out["weight"] = _float_weight(node, kind)
+        else:
+            q, s = quantize_fp8(node["weight"], dim)
+            out["weight"] = dequantize_fp8(q, s, dim)
         if node.get("bias") is not None:
             out["bias"] = node["bias"].to(torch.bfloat16).float()
         return out

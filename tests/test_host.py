@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import codec_oracle as O
 from sglang_omni_amd import _native as N
@@ -240,3 +241,100 @@ def test_rocm_platform_entry():
     assert current_platform.device_type == "cuda"
     assert current_platform.get_device_graph_backend() == "hip_graph"
     assert current_platform.is_cuda() is False
+
+
+@pytest.mark.parametrize("stride,k,padding,output_padding,dilation", [
+    (4, 8, 2, 0, 2), (3, 6, 1, 2, 3), (5, 10, 0, 0, 1), (2, 7, 3, 1, 2)])
+def test_polyphase_form_with_dilation_and_output_padding(stride, k, padding, output_padding,
+                                                         dilation):
+    """The general transposed conv (F.conv_transpose1d with padding, output padding and
+    dilation) is the packed form's first L_out samples, with as many positions as cover them."""
+    gen = torch.Generator().manual_seed(stride * k + dilation)
+    w = torch.randn(16, 8, k, generator=gen).to(torch.bfloat16).float()
+    b = torch.randn(8, generator=gen)
+    x = torch.randn(2, 9, 16, generator=gen)
+    conv = pack_conv_transpose1d(w, b, stride=stride, padding=padding, dilation=dilation)
+    expected = F.conv_transpose1d(x.double().transpose(1, 2), w.double(), b.double(),
+                                  stride=stride, padding=padding, output_padding=output_padding,
+                                  dilation=dilation).transpose(1, 2)
+    length_out = expected.shape[1]
+    positions = -(-length_out // stride)
+    got = emulate(x, conv, positions).view(2, positions * stride, 8)[:, :length_out]
+    torch.testing.assert_close(got, expected, rtol=1e-9, atol=1e-9)
+
+
+def test_channels_last_weight_helpers():
+    """tests/unit_test/utils/test_channels_last_conv.py:103-115: the channels-last weight keeps
+    the module's values and leaves the module alone; the folded weight of a stride-s conv is the
+    stride-one conv over the input's phases."""
+    from sglang_omni_amd.utils.channels_last_conv import (
+        channels_last_folded_weight,
+        channels_last_weight,
+    )
+
+    conv = torch.nn.Conv1d(4, 6, 7)
+    weight = channels_last_weight(conv)
+    assert torch.equal(weight, conv.weight)
+    assert weight.transpose(1, 2).is_contiguous() and conv.weight.is_contiguous()
+    strided = torch.nn.Conv1d(4, 6, 6, stride=3)
+    x = torch.randn(2, 4, 30)
+    folded = channels_last_folded_weight(strided.weight.data, 3)
+    phases = x.transpose(1, 2).reshape(2, 10, 12).transpose(1, 2)
+    torch.testing.assert_close(F.conv1d(phases, folded, strided.bias), strided(x))
+
+
+def test_checkpoint_fp8_scales_map_onto_per_channel_scales():
+    """A checkpoint's E4M3 conv weight with its weight_scale_inv (per tensor, per channel, row
+    blocks, inverted) gives the per-output-channel form whose dequantized values are the
+    checkpoint's; the reference's refusals (sglang_omni/quantization.py:137-166) hold."""
+    from sglang_omni_amd.quantization import fp8_conv_weight
+
+    gen = torch.Generator().manual_seed(12)
+    w = torch.randn(24, 16, 7, generator=gen)
+    q, s = quantize_fp8(w, 0)
+    deq = dequantize_fp8(q, s, 0)
+    q2, s2 = fp8_conv_weight("conv", q, s)
+    assert q2 is q and torch.equal(s2, s)
+    q3, s3 = fp8_conv_weight("conv", q, 1.0 / s, inverted=True)
+    torch.testing.assert_close(dequantize_fp8(q3, s3, 0), deq)
+    # blocks of 8 rows whose multipliers are constant along the row: exact
+    blocks = s.view(3, 8).amax(1, keepdim=True).expand(3, 4).contiguous()
+    qb = (w / blocks.repeat_interleave(8, 0)[:, :1].view(24, 1, 1)).to(torch.float8_e4m3fn)
+    q4, s4 = fp8_conv_weight("conv", qb, blocks, block_size=(8, 28))
+    torch.testing.assert_close(dequantize_fp8(q4, s4, 0),
+                               qb.float() * blocks[:, :1].repeat_interleave(8, 0).view(24, 1, 1))
+    # varying along the row: requantized per channel, within one E4M3 rounding
+    varying = torch.rand(3, 4, generator=gen) * 0.01 + 0.001
+    q5, s5 = fp8_conv_weight("conv", q, varying, block_size=(8, 28))
+    dense = (q.float().view(24, -1) * varying.repeat_interleave(8, 0).repeat_interleave(28, 1)
+             ).view(24, 16, 7)
+    err = (dequantize_fp8(q5, s5, 0) - dense).abs() / dense.abs().amax(dim=(1, 2), keepdim=True)
+    assert err.max() <= 2 ** -4
+    with pytest.raises(TypeError):
+        fp8_conv_weight("conv", q, torch.ones(24, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        fp8_conv_weight("conv", q, torch.tensor([]))
+    with pytest.raises(ValueError):
+        fp8_conv_weight("conv", q, torch.full((24,), float("inf")))
+    with pytest.raises(ValueError):
+        fp8_conv_weight("conv", q, torch.zeros(24))
+
+
+def test_e4m3_weights_in_a_tree_pack_as_they_are():
+    gen = torch.Generator().manual_seed(13)
+    w = torch.randn(16, 40, 7, generator=gen)
+    q, s = quantize_fp8(w, 0)
+    packed = pack_conv1d(q, None, fp8=True, scale=s)
+    assert packed.weight.dtype == torch.float8_e4m3fn
+    exact = q.float().double() * s.double().view(-1, 1, 1)
+    torch.testing.assert_close(unpack(packed)[..., :40], exact.permute(0, 2, 1), rtol=0, atol=0)
+    wt = torch.randn(32, 8, 12, generator=gen)
+    qt, st = quantize_fp8(wt, 1)
+    pt = pack_conv_transpose1d(qt, None, stride=6, scale=st)
+    x = torch.randn(1, 5, 32, generator=gen)
+    got = emulate(x, pt, 5).view(1, 30, 8)
+    w_deq = qt.float().double() * st.double().view(1, -1, 1)  # the dequantized values, exactly
+    expected = O.causal_conv_transpose1d(x.double().transpose(1, 2), w_deq, None, 6)
+    torch.testing.assert_close(got, expected.transpose(1, 2), rtol=1e-9, atol=1e-9)
+    tree = {"in_conv": {"weight": q, "weight_scale": s, "bias": None}}
+    assert torch.equal(reference_weights(tree, "fp8")["in_conv"]["weight"], dequantize_fp8(q, s, 0))
