@@ -154,6 +154,8 @@ class CodecStatePool:
         total = self.parity.shape[0]
         if any(s < 0 or s >= total for s in slots):
             raise ValueError(f"slot ids must lie in [0, {total}): {slots}")
+        if self.device.type != "cuda":
+            return torch.tensor(slots, dtype=torch.long, device=self.device)
         return torch.tensor(slots, dtype=torch.long, pin_memory=True).to(self.device,
                                                                           non_blocking=True)
 

@@ -33,8 +33,9 @@ def test_graph_runner_replays_streams_like_eager(gpu):
     assert set(runner.graphs) == {GraphKey(2, 6, "first"), GraphKey(2, 6, "next")}
     used = []
     for (a, b, f), ref in zip(splits, eager):
-        out, graphed = runner.run(codes[..., a:b], idx, first_decode=f)
-        used.append(graphed)
+        res = runner.run(codes[..., a:b], idx, first_decode=f)
+        out = res.output
+        used.append(res.graph)
         torch.cuda.synchronize()
         _ = torch.randn(1000, device=gpu).sum().item()  # eager work between replays
         assert torch.equal(out, ref), (a, b)

@@ -363,9 +363,11 @@ def test_small_decoder_graph_replay(small, gpu):
     runner.capture_all()
     codes = _codes(SMALL, 2, 12, 9).to(gpu)
     index = torch.tensor([1, 3], dtype=torch.int64, device=gpu)
-    out1, graphed1 = runner.run(codes[..., :6], index, first_decode=True)
+    r1 = runner.run(codes[..., :6], index, first_decode=True)
+    out1, graphed1 = r1.output, r1.graph
     out1 = out1.clone()
-    out2, graphed2 = runner.run(codes[..., 6:], index, first_decode=False)
+    r2 = runner.run(codes[..., 6:], index, first_decode=False)
+    out2, graphed2 = r2.output, r2.graph
     assert graphed1 and graphed2
     eager_pool = dec.new_state_pool(num_slots=4)
     e1 = dec.decode_slots(codes[..., :6], eager_pool, index, first_decode=True)
