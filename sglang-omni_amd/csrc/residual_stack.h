@@ -38,6 +38,12 @@ using omni_conv::pack_bf16x2;
 constexpr int kMaxUnits = OMNI_MAX_RESIDUAL_UNITS;
 constexpr int kTaps = 7;    // the residual unit's dilated conv
 constexpr int kGuard = 64;  // LDS rows ahead of row 0: the largest unit halo taken (6 * 10 = 60)
+// The sweep form (a workgroup runs consecutive tiles of one stream row): the largest unit or
+// final-conv halo it takes (6 * 9 = 54), the units its coefficient table holds, and the rows of
+// its halo store (the dilations 1, 3, 9 and a final conv of up to 7 taps: 6 + 18 + 54 + 6)
+constexpr int kSweepGuard = 56;
+constexpr int kSweepUnits = 3;
+constexpr int kSweepHaloRows = 84;
 constexpr int kCoefRows = 8;
 
 struct StackUnit {
@@ -89,6 +95,12 @@ struct StackParams {
   int seg_len;        // long rows: output positions per tile; short rows: the row length
   int tiles_per_row;  // long rows: tiles per stream row; 0: short rows, whole rows per tile
   int rows_per_tile;  // short rows: stream rows per tile
+  int sweep_segments;   // sweep: workgroups per stream row
+  int sweep_positions;  // sweep: positions per workgroup (the last one of a row may hold fewer)
+  // sweep: the halo store's rows of operand k (unit k's input; k = nunits: the final conv's)
+  // and where they start
+  int halo_rows[kMaxUnits + 1];
+  int halo_off[kMaxUnits + 1];
 };
 
 // LDS element offset of 16-byte slot `slot` of staged row `row` (guard included) in chunk kc.
@@ -129,13 +141,16 @@ __global__ void stack_coef_kernel(const StackParams p, float* table) {
   if (e < (p.nunits * kCoefRows + 2) * C) table[e] = stack_coef(p, e, C);
 }
 
-template <int C, int WCO, int WP, int TP, bool DMA = false>
+template <int C, int WCO, int WP, int TP, bool DMA = false, bool SWEEP = false>
 struct StackTile {
   static constexpr int NT = 64 * WCO * WP;
   static constexpr int TCO = C / (16 * WCO);
   static constexpr int R = WP * TP * 16;  // staged rows per tile
   static constexpr int CH = C / kChunk;
-  static constexpr int UROWS = kGuard + R;
+  // LDS rows ahead of row 0, holding the halo rows a unit's dilated conv reads before the tile's
+  // first row (zeros, or in the sweep the previous tile's last rows of the unit's operand)
+  static constexpr int GUARD = SWEEP ? kSweepGuard : kGuard;
+  static constexpr int UROWS = GUARD + R;
   static constexpr int WROW = kTaps * kChunk + 8;
   static constexpr int W1_PIECES = (C * kTaps * 4 + NT - 1) / NT;
   static constexpr int W2_PIECES = (C * C / 8 + NT - 1) / NT;
@@ -151,17 +166,24 @@ struct StackTile {
   static_assert(CH * C * 4 <= RING_SLOTS, "the k = 1 weights fit one ring buffer");
   static constexpr int W_ELEMS = DMA ? 2 * RING_ELEMS
                                      : (C * WROW > CH * C * kChunk ? C * WROW : CH * C * kChunk);
-  static constexpr int COEF = (kMaxUnits * kCoefRows + 2) * C;  // floats
+  static constexpr int UNITS = SWEEP ? kSweepUnits : kMaxUnits;  // units the coefficients hold
+  static constexpr int COEF = (UNITS * kCoefRows + 2) * C;  // floats
+  // the sweep's halo store: per unit input operand and the final conv's, the previous tile's
+  // last rows ([HALO_ROWS][C] bf16, rows of the operands in order)
+  static constexpr int HALO_ROWS = SWEEP ? kSweepHaloRows : 0;
   static constexpr size_t lds_bytes() {
-    return (size_t)CH * UROWS * kChunk * 2 + (size_t)W_ELEMS * 2 + (size_t)COEF * 4;
+    return (size_t)CH * UROWS * kChunk * 2 + (size_t)W_ELEMS * 2 + (size_t)COEF * 4 +
+           (size_t)HALO_ROWS * C * 2;
   }
   static_assert(C % (16 * WCO) == 0 && C % kChunk == 0, "tile shape");
+  static_assert(!SWEEP || (DMA && R % 16 == 0), "the sweep runs the DMA form on 16-row groups");
 };
 
-template <int C, int WCO, int WP, int TP, bool W_FP8, bool DMA>
+template <int C, int WCO, int WP, int TP, bool W_FP8, bool DMA, bool SWEEP>
 __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const StackParams p) {
   static_assert(!(DMA && W_FP8), "the DMA ring copies bf16 weights as they are");
-  using Tile = StackTile<C, WCO, WP, TP, DMA>;
+  using Tile = StackTile<C, WCO, WP, TP, DMA, SWEEP>;
+  constexpr int GUARD = Tile::GUARD;
   constexpr int NT = Tile::NT;
   constexpr int TCO = Tile::TCO;
   constexpr int CH = Tile::CH;
@@ -174,6 +196,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   u16* ws = lds + CH * UROWS * kChunk;  // weights
   float* coef = reinterpret_cast<float*>(ws + Tile::W_ELEMS);
   float* in0 = coef + p.nunits * kCoefRows * C;  // unit 0's input Snake a, b
+  u16* halo = reinterpret_cast<u16*>(coef + Tile::COEF);  // the sweep's halo store
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -184,9 +207,16 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   const int lk = (lane >> 4) * 8;
   const int wco0 = wave_co * TCO * 16;
 
-  // The tile: nseg row segments of len output positions starting at position i0 of rows b0..
-  int b0, i0, nseg, len;
-  if (p.tiles_per_row > 0) {
+  // The workgroup's positions: nseg row segments of len positions from position i0 of rows b0..
+  // (one tile), or in the sweep the positions [i0, seg_end) of row b0, tile after tile.
+  int b0, i0, nseg, len, seg_end = 0;
+  if constexpr (SWEEP) {
+    b0 = blockIdx.x / p.sweep_segments;
+    i0 = (blockIdx.x - b0 * p.sweep_segments) * p.sweep_positions;
+    seg_end = min(p.length, i0 + p.sweep_positions);
+    nseg = 1;
+    len = 0;  // set per tile
+  } else if (p.tiles_per_row > 0) {
     b0 = blockIdx.x / p.tiles_per_row;
     i0 = (blockIdx.x - b0 * p.tiles_per_row) * p.seg_len;
     nseg = 1;
@@ -197,50 +227,25 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     nseg = min(p.rows_per_tile, p.batch - b0);
     len = p.length;
   }
-  const int H = p.H;
   const int L = p.length;
-  const int span = len + H;  // staged rows per segment
-  const int rows = nseg * span;
-
-  // This lane's staged rows in the accumulator layout and their stream positions.
-  int rrow[TP], rb[TP], rpos[TP];
-#pragma unroll
-  for (int t = 0; t < TP; ++t) {
-    const int r = wave_p * TP * 16 + t * 16 + lrow;
-    const int s = r / span;
-    rrow[t] = r;
-    rb[t] = b0 + s;
-    rpos[t] = r < rows ? i0 - H + (r - s * span) : -(1 << 30);
-  }
-
-  // ---- set-up: x into registers, coefficients and guard rows into LDS, the first weights
-  f32x4 xv[TCO][TP];
-  {
-    const auto xr = buffer_rsrc(p.x, p.x_bytes);
-#pragma unroll
-    for (int c = 0; c < TCO; ++c) {
-      const int n = wco0 + c * 16 + (lane >> 4) * 4;
-#pragma unroll
-      for (int t = 0; t < TP; ++t) {
-        const bool ok = rpos[t] >= 0 && rpos[t] < L;
-        const uint32_t off = ok ? (uint32_t)(rb[t] * p.x_sb + rpos[t] * p.x_st + n) * 4 : kOutOfRange;
-        xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-      }
-    }
-  }
+  // ---- set-up, once per workgroup: coefficients, zero guard rows (and halo store) in LDS
   const int ncoef = (p.nunits * kCoefRows + 2) * C;
   if (p.coef_table != nullptr) {
-    // a straight copy of the precomputed rows: independent 16-byte loads, in flight with x's
+    // a straight copy of the precomputed rows: independent 16-byte loads
     for (int e = tid * 4; e < ncoef; e += NT * 4)
       *reinterpret_cast<f32x4*>(coef + e) = *reinterpret_cast<const f32x4*>(p.coef_table + e);
   } else {
     for (int e = tid; e < ncoef; e += NT) coef[e] = stack_coef(p, e, C);
   }
-  for (int e = tid; e < CH * kGuard * 4; e += NT) {
-    const int kc = e / (kGuard * 4);
-    const int rem = e - kc * kGuard * 4;
+  for (int e = tid; e < CH * GUARD * 4; e += NT) {
+    const int kc = e / (GUARD * 4);
+    const int rem = e - kc * GUARD * 4;
     *reinterpret_cast<u32x4*>(us + (kc * UROWS + (rem >> 2)) * kChunk + (rem & 3) * 8) =
         u32x4{0u, 0u, 0u, 0u};
+  }
+  if constexpr (SWEEP) {
+    for (int e = tid; e < Tile::HALO_ROWS * C / 8; e += NT)
+      *reinterpret_cast<u32x4*>(halo + e * 8) = u32x4{0u, 0u, 0u, 0u};
   }
 
   u32x4 wr[W_FP8 ? 1 : Tile::WPR];
@@ -366,10 +371,10 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   };
 
   // LDS addressing of the operand tile from the accumulator layout. Staged rows of this lane are
-  // kGuard + wave_p * TP * 16 + t * 16 + lrow, so the slot rotation (row / 4) % 4 is the lane's
-  // (lrow / 4) % 4 for every t: each access is a per-lane base plus a compile-time offset.
-  const int row0 = kGuard + wave_p * TP * 16 + lrow;  // staged row of t = 0 (guard included)
-  const int sw = (lrow >> 2) & 3;
+  // row0 + 16 t, so the slot rotation (row / 4) % 4 is row0's for every t: each access is a
+  // per-lane base plus a compile-time offset.
+  const int row0 = GUARD + wave_p * TP * 16 + lrow;  // staged row of t = 0 (guard included)
+  const int sw = (row0 >> 2) & 3;
   // columns n = c * 16 + (lane / 16) * 4 .. + 3 of the lane: chunk c / 2, 16-byte slot
   // 2 * (c % 2) + lane / 32, element (lane / 16 % 2) * 4 within the slot
   const int put_base0 = row0 * kChunk + ((((lane >> 5)) ^ sw) << 3) + ((lane >> 4) & 1) * 4;
@@ -384,9 +389,78 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     *reinterpret_cast<uint2*>(us + base + (c >> 1) * UROWS * kChunk + t * 16 * kChunk) = o;
   };
 
+  // ---- the tiles: one (nseg row segments), or in the sweep consecutive tiles of one row, the
+  // first staging the causal halo H of the whole stack ahead of its positions, the later ones
+  // taking each operand's halo from the previous tile (the halo store, copied into the guard)
+  f32x4 xv[TCO][TP];
+  f32x4 acc[TCO][TP];
+  for (int tile = 0;; ++tile) {
+  const int H = (SWEEP && tile > 0) ? 0 : p.H;
+  if constexpr (SWEEP) len = min(Tile::R - H, seg_end - i0);
+  const bool has_next = SWEEP && i0 + len < seg_end;  // then this tile holds R rows
+  const int span = len + H;  // staged rows per segment
+  const int rows = nseg * span;
+
+  // This lane's staged row t in the accumulator layout, its segment, stream row and position
+  // (recomputed where needed rather than held in registers; in the sweep every row is of row b0)
+  auto row_of = [&](int t) __attribute__((always_inline)) -> int {
+    return wave_p * TP * 16 + t * 16 + lrow;
+  };
+  auto seg_of = [&](int t) __attribute__((always_inline)) -> int {
+    return SWEEP ? 0 : row_of(t) / span;
+  };
+  auto pos_of = [&](int t) __attribute__((always_inline)) -> int {
+    const int r = row_of(t);
+    return r < rows ? i0 - H + (r - seg_of(t) * span) : -(1 << 30);
+  };
+  if (tile > 0) __syncthreads();  // the previous tile's reads of the tile, guard and ring are done
+  {
+    const auto xr = buffer_rsrc(p.x, p.x_bytes);
+#pragma unroll
+    for (int c = 0; c < TCO; ++c) {
+      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const int pos = pos_of(t);
+        const bool ok = pos >= 0 && pos < L;
+        const uint32_t off =
+            ok ? (uint32_t)((b0 + seg_of(t)) * p.x_sb + pos * p.x_st + n) * 4 : kOutOfRange;
+        xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+      }
+    }
+  }
+  // Write operand k's value for (c, t) into the tile; in the sweep, when the row is one of the
+  // operand's last halo rows, first move the halo store's old row (the previous tile's, zeros in
+  // the first tile) into the guard row the operand's conv reads before row 0, then, when another
+  // tile follows, keep the new one there. The lane reads and writes only its own 4 channels of
+  // those rows, so the move and the overwrite are ordered without a barrier; the guard is free
+  // here (every wave has passed the barrier that ends the previous reader of the guard).
+  auto put_operand = [&](int k, int c, int t, float y0, float y1, float y2, float y3)
+                         __attribute__((always_inline)) {
+    put(c, t, y0, y1, y2, y3);
+    if constexpr (SWEEP) {
+      const int hk = p.halo_rows[k];
+      const int j = (wave_p * TP * 16 + t * 16 + lrow) - (Tile::R - hk);
+      if (j >= 0) {
+        const int n = wco0 + c * 16 + (lane >> 4) * 4;
+        uint2* slot = reinterpret_cast<uint2*>(halo + (p.halo_off[k] + j) * C + n);
+        const int base = (c & 1) ? put_base1 : put_base0;
+        // the guard row r - R sits R rows before row r: same 16-row phase, same slot rotation
+        *reinterpret_cast<uint2*>(us + base + (c >> 1) * UROWS * kChunk + t * 16 * kChunk -
+                                  Tile::R * kChunk) = *slot;
+        if (has_next) {
+          uint2 o;
+          o.x = pack_bf16x2(y0, y1);
+          o.y = pack_bf16x2(y2, y3);
+          *slot = o;
+        }
+      }
+    }
+  };
+
   if constexpr (DMA) dma_stage(0);
   else load_w1(0, 0);
-  __syncthreads();  // coefficients and guard rows
+  if (tile == 0) __syncthreads();  // coefficients and guard rows
   // unit 0's operand
 #pragma unroll
   for (int c = 0; c < TCO; ++c) {
@@ -396,12 +470,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
       const f32x4 v = xv[c][t];
-      put(c, t, snake_rev(v[0], a[0], b[0]), snake_rev(v[1], a[1], b[1]),
-          snake_rev(v[2], a[2], b[2]), snake_rev(v[3], a[3], b[3]));
+      put_operand(0, c, t, snake_rev(v[0], a[0], b[0]), snake_rev(v[1], a[1], b[1]),
+                  snake_rev(v[2], a[2], b[2]), snake_rev(v[3], a[3], b[3]));
     }
   }
 
-  f32x4 acc[TCO][TP];
   for (int k = 0; k < p.nunits; ++k) {
     const int h = p.unit[k].halo;
     const int d = p.unit[k].dil;
@@ -430,7 +503,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
           }
         }
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, 0);
-        const int row = kGuard + s * span + H - h + j;
+        const int row = GUARD + s * span + H - h + j;
         *reinterpret_cast<u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3)) = v;
       }
       __syncthreads();
@@ -448,7 +521,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         const int64_t slot = p.slot_index[b0 + s];
         if (own && slot >= 0 && slot < p.hist_slots) {
           const int parity = (int)(p.slot_parity[slot] & 1);
-          const int row = kGuard + s * span + (pos - i0) + H;
+          const int row = GUARD + s * span + (pos - i0) + H;
           const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
           const uint32_t off = (uint32_t)((int)slot * hstride + ((1 - parity) * h + j) * C + piece * 8) * 2;
           __builtin_amdgcn_raw_buffer_store_b128(v, hr, off, 0, 0);
@@ -586,8 +659,8 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         f32x4 v = acc[c][t] * sc + bi;
         v += xv[c][t];
         xv[c][t] = v;
-        put(c, t, snake_rev(v[0], na[0], nb[0]), snake_rev(v[1], na[1], nb[1]),
-            snake_rev(v[2], na[2], nb[2]), snake_rev(v[3], na[3], nb[3]));
+        put_operand(k + 1, c, t, snake_rev(v[0], na[0], nb[0]), snake_rev(v[1], na[1], nb[1]),
+                    snake_rev(v[2], na[2], nb[2]), snake_rev(v[3], na[3], nb[3]));
       }
     }
   }
@@ -600,7 +673,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       const int rem = e - s * len * PIECES_PER_ROW;
       const int q = rem / PIECES_PER_ROW;
       const int piece = rem - q * PIECES_PER_ROW;
-      const int row = kGuard + s * span + H + q;
+      const int row = GUARD + s * span + H + q;
       const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
       const uint32_t off = (uint32_t)((b0 + s) * p.o_sb + (i0 + q) * p.o_st + piece * 8) * 2;
       __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, off, 0, 0);
@@ -628,7 +701,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
           }
         }
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(fr, off, 0, 0);
-        const int row = kGuard + s * span + H - fh + j;
+        const int row = GUARD + s * span + H - fh + j;
         *reinterpret_cast<u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3)) = v;
       }
     }
@@ -646,7 +719,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         const int64_t slot = p.slot_index[b0 + s];
         if (own && slot >= 0 && slot < p.hist_slots) {
           const int parity = (int)(p.slot_parity[slot] & 1);
-          const int row = kGuard + s * span + (pos - i0) + H;
+          const int row = GUARD + s * span + (pos - i0) + H;
           const u32x4 v = *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, row, piece & 3));
           const uint32_t off =
               (uint32_t)((int)slot * p.fin_hist_stride + ((1 - parity) * fh + j) * C + piece * 8) * 2;
@@ -683,9 +756,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     if (lane < 16) {
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
-        const int q = rrow[t] - (rrow[t] / span) * span;
-        if (rrow[t] < rows && q >= H)
-          p.fin_out[(int64_t)rb[t] * p.fin_o_sb + rpos[t]] =
+        const int q = row_of(t) - seg_of(t) * span;
+        if (row_of(t) < rows && q >= H)
+          p.fin_out[(int64_t)(b0 + seg_of(t)) * p.fin_o_sb + pos_of(t)] =
               apply_act(p.fin_act, acc[0][t][0] + bias, 0.f, 0.f, 0.f);
       }
     }
@@ -697,14 +770,18 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       const int n = wco0 + c * 16 + (lane >> 4) * 4;
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
-        const int q = rrow[t] - (rrow[t] / span) * span;
-        const bool ok = rrow[t] < rows && q >= H;
+        const int q = row_of(t) - seg_of(t) * span;
+        const bool ok = row_of(t) < rows && q >= H;
         const uint32_t off =
-            ok ? (uint32_t)(rb[t] * p.xo_sb + rpos[t] * p.xo_st + n) * 4 : kOutOfRange;
+            ok ? (uint32_t)((b0 + seg_of(t)) * p.xo_sb + pos_of(t) * p.xo_st + n) * 4
+               : kOutOfRange;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xv[c][t]), xo, off, 0, 0);
       }
     }
   }
+  if (!has_next) break;
+  i0 += len;
+  }  // tiles
 }
 
 // 96 channels, 8 waves, each with all 96 columns. fp8 weights are converted to bf16 on their way
@@ -713,10 +790,12 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 // DMA, which frees the staging registers: 48 of 384 rows per wave.
 using Stack96 = StackTile<96, 1, 8, 2>;
 using Stack96Dma = StackTile<96, 1, 8, 3, true>;
+using Stack96Sweep = StackTile<96, 1, 8, 3, true, true>;
+static_assert(Stack96Sweep::lds_bytes() <= 160 * 1024, "the sweep form fits the CU's LDS");
 
 template <bool W_FP8>
-int launch_stack96(const StackParams& p, int grid, hipStream_t stream);
-template <> int launch_stack96<false>(const StackParams& p, int grid, hipStream_t stream);
-template <> int launch_stack96<true>(const StackParams& p, int grid, hipStream_t stream);
+int launch_stack96(const StackParams& p, int grid, bool sweep, hipStream_t stream);
+template <> int launch_stack96<false>(const StackParams& p, int grid, bool sweep, hipStream_t stream);
+template <> int launch_stack96<true>(const StackParams& p, int grid, bool sweep, hipStream_t stream);
 
 }  // namespace omni_stack

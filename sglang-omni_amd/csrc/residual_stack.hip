@@ -5,6 +5,22 @@ namespace {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
+// Compute units of the current device (the sweep sizes its grid to one workgroup per unit),
+// queried once per process; 256 (MI355X) when the query fails.
+int64_t compute_units() {
+  static const int64_t cached = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < 1) {
+      (void)hipGetLastError();
+      return (int64_t)256;
+    }
+    return (int64_t)n;
+  }();
+  return cached;
+}
+
 // The arrays the coefficient rows come from (omni_stack::stack_coef).
 void coef_sources(const omni_residual_stack_args* a, bool fp8, omni_stack::StackParams& p) {
   p.nunits = a->num_units;
@@ -188,10 +204,40 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
     p.fin_o_sb = a->final_out_stride_b;
   }
 
-  // Long rows: tiles inside one row, as many as the staged rows need, evened out; short rows:
-  // as many whole rows (each with its halo) as the staged rows hold.
+  // Long rows with bf16 weights: the sweep (each workgroup runs consecutive tiles of one row,
+  // the causal halo staged once per workgroup instead of once per tile), one workgroup per
+  // compute unit where the rows allow. Otherwise long rows take tiles inside one row, as many as
+  // the staged rows need, evened out; short rows as many whole rows (each with its halo) as the
+  // staged rows hold.
   int64_t grid;
-  if (L + H > R) {
+  bool sweep = false;
+  if (!fp8 && L + H > R && a->num_units <= kSweepUnits) {
+    int64_t halo_rows = fin ? a->final_taps - 1 : 0;
+    bool fits = halo_rows <= kSweepGuard;
+    for (int k = 0; k < a->num_units; ++k) {
+      halo_rows += 6 * a->units[k].dilation;
+      fits = fits && 6 * a->units[k].dilation <= kSweepGuard;
+    }
+    sweep = fits && halo_rows <= kSweepHaloRows;
+  }
+  if (sweep) {
+    int off = 0;
+    for (int k = 0; k <= a->num_units; ++k) {
+      const int rows_k = k < a->num_units ? (int)(6 * a->units[k].dilation)
+                                          : (fin ? (int)(a->final_taps - 1) : 0);
+      p.halo_rows[k] = rows_k;
+      p.halo_off[k] = off;
+      off += rows_k;
+    }
+    const int64_t cus = compute_units();
+    int64_t segments = B >= cus ? 1 : cus / B;
+    // at least two tiles per segment, or the sweep saves no halo
+    const int64_t max_segments = (L + 2 * R - 1) / (2 * R);
+    segments = segments < 1 ? 1 : (segments > max_segments ? max_segments : segments);
+    p.sweep_segments = (int)segments;
+    p.sweep_positions = (int)((L + segments - 1) / segments);
+    grid = B * segments;
+  } else if (L + H > R) {
     const int64_t tiles = (L + (R - H) - 1) / (R - H);
     p.seg_len = (int)((L + tiles - 1) / tiles);
     p.tiles_per_row = (int)((L + p.seg_len - 1) / p.seg_len);
@@ -204,5 +250,6 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   }
   if (grid > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  return fp8 ? launch_stack96<true>(p, (int)grid, s) : launch_stack96<false>(p, (int)grid, s);
+  return fp8 ? launch_stack96<true>(p, (int)grid, false, s)
+             : launch_stack96<false>(p, (int)grid, sweep, s);
 }
