@@ -429,31 +429,29 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       }
     }
   }
-  // Write operand k's value for (c, t) into the tile; in the sweep, when the row is one of the
-  // operand's last halo rows, first move the halo store's old row (the previous tile's, zeros in
-  // the first tile) into the guard row the operand's conv reads before row 0, then, when another
-  // tile follows, keep the new one there. The lane reads and writes only its own 4 channels of
-  // those rows, so the move and the overwrite are ordered without a barrier; the guard is free
-  // here (every wave has passed the barrier that ends the previous reader of the guard).
-  auto put_operand = [&](int k, int c, int t, float y0, float y1, float y2, float y3)
-                         __attribute__((always_inline)) {
-    put(c, t, y0, y1, y2, y3);
+  // The sweep's halo rows of operand k, once the wave has written its rows of the operand: for
+  // each of the operand's last halo rows that this wave owns, move the halo store's old row (the
+  // previous tile's, zeros in the first tile) into the guard row the operand's conv reads before
+  // row 0 (the guard row r - R sits R rows before row r), then, when another tile follows, keep
+  // the new row there. Only this wave reads and writes these rows of the store, and its LDS
+  // operations complete in order, so no barrier is needed; the guard is free (every wave has
+  // passed the barrier that ends the previous reader of the guard).
+  auto halo_move = [&](int k) __attribute__((always_inline)) {
     if constexpr (SWEEP) {
-      const int hk = p.halo_rows[k];
-      const int j = (wave_p * TP * 16 + t * 16 + lrow) - (Tile::R - hk);
-      if (j >= 0) {
-        const int n = wco0 + c * 16 + (lane >> 4) * 4;
-        uint2* slot = reinterpret_cast<uint2*>(halo + (p.halo_off[k] + j) * C + n);
-        const int base = (c & 1) ? put_base1 : put_base0;
-        // the guard row r - R sits R rows before row r: same 16-row phase, same slot rotation
-        *reinterpret_cast<uint2*>(us + base + (c >> 1) * UROWS * kChunk + t * 16 * kChunk -
-                                  Tile::R * kChunk) = *slot;
-        if (has_next) {
-          uint2 o;
-          o.x = pack_bf16x2(y0, y1);
-          o.y = pack_bf16x2(y2, y3);
-          *slot = o;
-        }
+      const int first = Tile::R - p.halo_rows[k];
+      const int w0 = wave_p * TP * 16;
+      const int lo = first > w0 ? first : w0;
+      const int n = (w0 + TP * 16 - lo) * PIECES_PER_ROW;
+      for (int e = lane; e < n; e += 64) {
+        const int r = lo + e / PIECES_PER_ROW;
+        const int piece = e - (r - lo) * PIECES_PER_ROW;
+        u32x4* st = reinterpret_cast<u32x4*>(halo + (p.halo_off[k] + r - first) * C + piece * 8);
+        const u32x4 old = *st;
+        const u32x4 cur =
+            *reinterpret_cast<const u32x4*>(us + uaddr<UROWS>(piece >> 2, GUARD + r, piece & 3));
+        *reinterpret_cast<u32x4*>(us + uaddr<UROWS>(piece >> 2, GUARD + r - Tile::R, piece & 3)) =
+            old;
+        if (has_next) *st = cur;
       }
     }
   };
@@ -470,10 +468,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
       const f32x4 v = xv[c][t];
-      put_operand(0, c, t, snake_rev(v[0], a[0], b[0]), snake_rev(v[1], a[1], b[1]),
-                  snake_rev(v[2], a[2], b[2]), snake_rev(v[3], a[3], b[3]));
+      put(c, t, snake_rev(v[0], a[0], b[0]), snake_rev(v[1], a[1], b[1]),
+          snake_rev(v[2], a[2], b[2]), snake_rev(v[3], a[3], b[3]));
     }
   }
+  halo_move(0);
 
   for (int k = 0; k < p.nunits; ++k) {
     const int h = p.unit[k].halo;
@@ -659,10 +658,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         f32x4 v = acc[c][t] * sc + bi;
         v += xv[c][t];
         xv[c][t] = v;
-        put_operand(k + 1, c, t, snake_rev(v[0], na[0], nb[0]), snake_rev(v[1], na[1], nb[1]),
-                    snake_rev(v[2], na[2], nb[2]), snake_rev(v[3], na[3], nb[3]));
+        put(c, t, snake_rev(v[0], na[0], nb[0]), snake_rev(v[1], na[1], nb[1]),
+            snake_rev(v[2], na[2], nb[2]), snake_rev(v[3], na[3], nb[3]));
       }
     }
+    halo_move(k + 1);
   }
   __syncthreads();
   // ---- the output operand rows of the tile's positions, 16 contiguous bytes per thread
