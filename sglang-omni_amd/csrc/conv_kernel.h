@@ -82,22 +82,6 @@ struct ConvParams {
   uint32_t x_bytes, w_bytes, w2_bytes, hist_bytes, r_bytes, o_bytes;
 };
 
-// OCP e4m3fn -> float (exact). 0x7f / 0xff are NaN; there are no infinities.
-__device__ __forceinline__ float fp8_e4m3_to_float(uint32_t v) {
-  const uint32_t s = (v & 0x80u) << 24;
-  const uint32_t e = (v >> 3) & 0xfu;
-  const uint32_t m = v & 0x7u;
-  float f;
-  if (e == 0) {
-    f = (float)m * 0.001953125f;  // m * 2^-9
-  } else if (e == 15 && m == 7) {
-    f = __uint_as_float(0x7fc00000u);
-  } else {
-    f = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  }
-  return __uint_as_float(__float_as_uint(f) | s);
-}
-
 // Two floats to a bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -105,12 +89,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
 }
 
+// Eight OCP e4m3fn bytes -> eight bf16, byte i to element i (exact: every e4m3fn value, the
+// subnormals included, is a bf16 value; 0x7f / 0xff are NaN). gfx950 converts a byte pair per
+// v_cvt_scalef32_pk_bf16_fp8 (scale 1; word_sel picks bytes 0-1 or 2-3 of the dword).
+template <bool HIGH>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t word) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.0f, HIGH));
+}
 __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 raw) {
-  return u32x4{
-      pack_bf16x2(fp8_e4m3_to_float(raw[0] & 0xff), fp8_e4m3_to_float((raw[0] >> 8) & 0xff)),
-      pack_bf16x2(fp8_e4m3_to_float((raw[0] >> 16) & 0xff), fp8_e4m3_to_float(raw[0] >> 24)),
-      pack_bf16x2(fp8_e4m3_to_float(raw[1] & 0xff), fp8_e4m3_to_float((raw[1] >> 8) & 0xff)),
-      pack_bf16x2(fp8_e4m3_to_float((raw[1] >> 16) & 0xff), fp8_e4m3_to_float(raw[1] >> 24))};
+  return u32x4{fp8x2_to_bf16x2<false>(raw[0]), fp8x2_to_bf16x2<true>(raw[0]),
+               fp8x2_to_bf16x2<false>(raw[1]), fp8x2_to_bf16x2<true>(raw[1])};
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

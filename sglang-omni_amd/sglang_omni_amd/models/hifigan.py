@@ -66,6 +66,19 @@ class HifiGanVocoder:
         if len(self.stages[0]["blocks"]) != 3:
             raise ValueError("the MRF mean is fused for three ResBlocks per stage")
 
+    def _workspace(self, elements: int) -> tuple[torch.Tensor, ...]:
+        """The intermediate activations of a call: four bf16 and three float32 flat buffers of
+        at least ``elements`` each, kept between calls and grown (never shrunk) when a call
+        needs more. Calls on one vocoder share them, so they must not overlap (one stream, or
+        calls ordered between streams)."""
+        ws = getattr(self, "_ws", None)
+        if ws is None or ws[0].numel() < elements:
+            bf, f32 = torch.bfloat16, torch.float32
+            ws = tuple(torch.empty(elements, dtype=dt, device=self.device)
+                       for dt in (bf, bf, bf, bf, f32, f32, f32))
+            self._ws = ws
+        return ws
+
     @torch.no_grad()
     def forward(self, mel: torch.Tensor) -> torch.Tensor:
         N.require_device(mel)
@@ -81,13 +94,8 @@ class HifiGanVocoder:
             ll *= st["rate"]
             cc = st["up"].c_out
             sizes.append(ll * cc)
-        big = batch * max(sizes)
-        act_p = torch.empty(big, dtype=torch.bfloat16, device=dev)
-        act_q = torch.empty(big, dtype=torch.bfloat16, device=dev)
-        h = torch.empty(big, dtype=torch.bfloat16, device=dev)
-        run = torch.empty(big, dtype=torch.bfloat16, device=dev)
-        xs = torch.empty(big, dtype=torch.float32, device=dev)
-        xb = [torch.empty(big, dtype=torch.float32, device=dev) for _ in range(2)]
+        act_p, act_q, h, run, xs, xb0, xb1 = self._workspace(batch * max(sizes))
+        xb = [xb0, xb1]
 
         def view(flat: torch.Tensor, length: int, ch: int) -> torch.Tensor:
             return flat[: batch * length * ch].view(batch, length, ch)

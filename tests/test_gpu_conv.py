@@ -203,6 +203,25 @@ def test_fp8_weights_match_dequantized_reference(gpu):
     close(out_t, convt_ref64(x, dequantize_fp8(qt, st, 1), b, stride=6), rtol=1e-5, atol=1e-5)
 
 
+def test_fp8_weight_decode_is_exact_for_every_encoding(gpu):
+    """Every finite E4M3 encoding, at every byte position of the packed weights, reaches the MFMA
+    as its exact value: a k = 1 conv with one-hot inputs returns one weight per output, which
+    must equal torch's float8_e4m3fn -> float32 conversion times the channel's scale (a power of
+    two, so the product is exact too)."""
+    c_in, c_out = 32, 256
+    codes = (torch.arange(c_out * c_in) * 37 % 256).to(torch.uint8)  # every byte, shuffled
+    codes[(codes == 0x7F) | (codes == 0xFF)] = 0  # the two NaN encodings
+    assert codes.unique().numel() == 254
+    q = codes.view(torch.float8_e4m3fn).view(c_out, c_in, 1)
+    scale = 2.0 ** torch.randint(-3, 4, (c_out,), generator=torch.Generator().manual_seed(3))
+    packed = pack_conv1d(q, None, fp8=True, scale=scale.float()).to(gpu)
+    x = torch.eye(c_in).view(1, c_in, c_in)  # position p holds channel p
+    out = torch.empty(1, c_in, c_out, dtype=torch.float32, device=gpu)
+    fused_conv(x.to(gpu, torch.bfloat16), packed, out)
+    expect = (q.float()[:, :, 0] * scale[:, None]).t()  # [position = c_in, c_out]
+    assert torch.equal(out[0].cpu(), expect)
+
+
 @pytest.mark.parametrize("dilation", [1, 3, 9])
 @pytest.mark.parametrize("chunks", [(10, 10, 7), (1, 2, 1, 3, 40), (32, 1, 32)])
 def test_streamed_causal_conv_equals_the_whole_stream_bitwise(gpu, dilation, chunks):
