@@ -7,21 +7,20 @@ namespace omni_conv {
 namespace {
 
 // The kernel family and configuration for p: OMNI_CONV_KERNEL_AUTO picks the family by the
-// operand mode, weight dtype and taps (LDS-DMA for bf16 operands used as they are and bf16
-// weights, then the register-staged kernels) and the configuration by size; a named family runs
-// only if it can serve p. `kernel` returns the family that took the call.
+// operand mode, weight dtype and taps (LDS-DMA for bf16 operands used as they are, with bf16 or
+// E4M3 weights, then the register-staged kernels) and the configuration by size; a named family
+// runs only if it can serve p. `kernel` returns the family that took the call.
 int dispatch(const ConvParams& p, bool x_f32, bool fp8, bool fuse2, int& kernel, Choice& ch,
              hipStream_t stream) {
   if (p.halo > kMaxHalo) return OMNI_ERR_UNSUPPORTED;
   const int in_mode = x_f32 ? IN_F32 : (p.in_act != OMNI_ACT_NONE ? IN_ACT : IN_RAW);
   const int want = kernel;
   auto allowed = [&](int family) { return want == OMNI_CONV_KERNEL_AUTO || want == family; };
-  if (allowed(OMNI_CONV_KERNEL_DMA) && in_mode == IN_RAW && !fp8 && !fuse2 &&
-      p.c_in % kChunk == 0) {
+  if (allowed(OMNI_CONV_KERNEL_DMA) && in_mode == IN_RAW && !fuse2 && p.c_in % kChunk == 0) {
     int status = OMNI_ERR_UNSUPPORTED;
-    if (p.taps == 7) status = launch_dma_taps7(p, ch, stream);
-    else if (p.taps == 2) status = launch_dma_taps2(p, ch, stream);
-    else if (p.taps == 1) status = launch_dma_taps1(p, ch, stream);
+    if (p.taps == 7) status = launch_dma_taps7(p, fp8, ch, stream);
+    else if (p.taps == 2) status = launch_dma_taps2(p, fp8, ch, stream);
+    else if (p.taps == 1) status = launch_dma_taps1(p, fp8, ch, stream);
     if (status != OMNI_ERR_UNSUPPORTED || want == OMNI_CONV_KERNEL_DMA) {
       kernel = OMNI_CONV_KERNEL_DMA;
       return status;

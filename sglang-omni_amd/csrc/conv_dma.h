@@ -1,6 +1,6 @@
 // Polyphase convolution with LDS-DMA staging (gfx950 bf16 MFMA), for bf16 operands used as they
-// are (no activation on the way in) and bf16 weights: the conv layers of the codec decoder, whose
-// producers write the next conv's operand u = act(x) from their epilogues.
+// are (no activation on the way in) and bf16 or E4M3 weights: the conv layers of the codec
+// decoder, whose producers write the next conv's operand u = act(x) from their epilogues.
 //
 // The GEMM is conv_mfma_kernel's (conv_kernel.h): output columns n as the MFMA M dimension,
 // positions m = b * length + i as N, (tap, c_in) as K, batch rows sharing one position space with
@@ -16,7 +16,10 @@
 //         nothing (causal zero padding, written once as zeros into both ring buffers);
 //       - weights [BCO][TAPS * 4 + 1] 16-byte slots per column (taps x 32 channels plus one pad
 //         slot, an odd row pitch, so the 16 column rows an MFMA operand read touches start on
-//         distinct banks); pad slots reload a real piece.
+//         distinct banks); pad slots reload a real piece. E4M3 weights keep their bytes in LDS
+//         ([BCO][TAPS * 2 + 1] slots, half the LDS bytes per operand read) and are widened to
+//         bf16 (exactly) as the MFMA operand is read; their per-column scale is applied in the
+//         epilogue.
 //   * A two-buffer ring of stages, each KC 32-channel chunks: one barrier per stage, after which
 //     the next stage's DMA is issued and runs during this stage's MFMAs. k = 1 and transposed
 //     (two-tap) convs take several chunks per stage so each barrier covers enough matrix work.
@@ -35,14 +38,16 @@
 
 namespace omni_conv {
 
-template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC>
+template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false>
 struct DmaTile {
   using Base = ConvTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS>;  // epilogue geometry
   static constexpr int NT = Base::NT;
   static constexpr int BCO = Base::BCO;
   static constexpr int BP = Base::BP;
   static constexpr int NW = NT / 64;
-  static constexpr int P = TAPS * 4 + 1;           // 16-byte slots per weight row (one pad)
+  // 16-byte slots per weight row: a tap's 32 channels take 4 (bf16) or 2 (E4M3), plus one pad
+  static constexpr int WSLOTS = TAPS * (W8 ? 2 : 4);
+  static constexpr int P = WSLOTS + 1;
   static constexpr int NIW = (BCO * P + 63) / 64;  // weight DMA instructions per chunk
   static constexpr int NIX = MAX_ROWS / 16;        // input-row DMA instructions per chunk
   static constexpr int W_PIECES = (NIW + NW - 1) / NW;
@@ -61,11 +66,11 @@ struct DmaTile {
 
 // The ring takes most of a CU's LDS, so one workgroup runs per CU: WAVES_CO * WAVES_P / 4 waves
 // per SIMD, which the register allocation may assume.
-template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC>
+template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8>
 __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     __attribute__((amdgpu_waves_per_eu(WAVES_CO * WAVES_P / 4, WAVES_CO * WAVES_P / 4)))
     conv_dma_kernel(const ConvParams p) {
-  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC>;
+  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
   constexpr int NT = Tile::NT;
   constexpr int NW = Tile::NW;
   constexpr int BCO = Tile::BCO;
@@ -179,7 +184,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     const int s = (wave + u * NW) * 64 + lane;
     const int n = s / P;
     const int piece = s - n * P;
-    woff[u] = (n < BCO && piece < TAPS * 4) ? (uint32_t)(n * TAPS * 4 + piece) * 16 : 0u;
+    woff[u] = (n < BCO && piece < Tile::WSLOTS) ? (uint32_t)(n * Tile::WSLOTS + piece) * 16 : 0u;
   }
 
   float* coef = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds) + Tile::coef_offset);
@@ -216,7 +221,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       {
         u16* xs = xs_of(buf, c);
         u16* ws = xs + Tile::XCHUNK;
-        const uint32_t wbase = (uint32_t)(kc * n_cols + n0) * (uint32_t)(TAPS * kChunk * 2);
+        const uint32_t wbase = (uint32_t)(kc * n_cols + n0) * (uint32_t)(Tile::WSLOTS * 16);
 #pragma unroll
         for (int u = 0; u < Tile::W_PIECES; ++u) {
           const int iw = wave + u * NW;
@@ -298,9 +303,19 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       const int c = i / TAPS;
       const int j = i - c * TAPS;
       const u16* xs = xs0 + c * (Tile::XCHUNK + Tile::WCHUNK);
-      const u16* wtap = xs + Tile::XCHUNK + (wco0 + lrow) * P * 8 + lk + j * kChunk;
+      if constexpr (W8) {
+        // the lane's 8 weight bytes of tap j (channels lk .. lk + 7), widened to bf16 (exact)
+        const u16* wtap = xs + Tile::XCHUNK + (wco0 + lrow) * P * 8 + j * (kChunk / 2) + lk / 2;
 #pragma unroll
-      for (int cc = 0; cc < TCO; ++cc) a[cc] = *reinterpret_cast<const bf16x8*>(wtap + cc * 16 * P * 8);
+        for (int cc = 0; cc < TCO; ++cc)
+          a[cc] = __builtin_bit_cast(
+              bf16x8, fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(wtap + cc * 16 * P * 8)));
+      } else {
+        const u16* wtap = xs + Tile::XCHUNK + (wco0 + lrow) * P * 8 + lk + j * kChunk;
+#pragma unroll
+        for (int cc = 0; cc < TCO; ++cc)
+          a[cc] = *reinterpret_cast<const bf16x8*>(wtap + cc * 16 * P * 8);
+      }
       const int shift = j * dil;
 #pragma unroll
       for (int t = 0; t < TP; ++t)
@@ -324,9 +339,9 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
                                                        m_end, wave_p, wco0);
 }
 
-template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC>
+template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false>
 struct DmaConfig {
-  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC>;
+  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
 
   // Staged rows of the fullest tile: BP positions over at most nseg row segments, each with its
   // own halo.
@@ -355,7 +370,7 @@ struct DmaConfig {
     const int64_t positions = (int64_t)p.batch * p.length;
     p.p_tiles = (int)((positions + Tile::BP - 1) / Tile::BP);
     p.n_tiles = (int)((p.n_cols + Tile::BCO - 1) / Tile::BCO);
-    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC>;
+    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
     // raised once per instantiation, on its first launch (no attribute calls inside a capture)
     static const bool raised = raise_lds_limit((const void*)k);
     (void)raised;
@@ -389,8 +404,9 @@ int launch_first_fit(const ConvParams& p, Choice& ch, hipStream_t stream) {
 
 // Launchers by tap count (1: k = 1 convs, 2: transposed convs of kernel 2 * stride, 7: k = 7
 // convs), one translation unit each.
-int launch_dma_taps1(const ConvParams& p, Choice& ch, hipStream_t stream);
-int launch_dma_taps2(const ConvParams& p, Choice& ch, hipStream_t stream);
-int launch_dma_taps7(const ConvParams& p, Choice& ch, hipStream_t stream);
+// `fp8`: the packed weights are E4M3 (one byte per weight, per-column scales in the epilogue).
+int launch_dma_taps1(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
+int launch_dma_taps2(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
+int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 
 }  // namespace omni_conv

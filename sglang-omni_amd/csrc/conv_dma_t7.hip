@@ -1,15 +1,23 @@
-// LDS-DMA convolution kernels for k = 7 convs (bf16 operand and weights).
+// LDS-DMA convolution kernels for k = 7 convs (bf16 operand; bf16 or E4M3 weights).
 #include "conv_dma.h"
 
 namespace omni_conv {
 
-int launch_dma_taps7(const ConvParams& p, Choice& ch, hipStream_t stream) {
+int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream) {
   // 96 columns x 384 positions, 16 waves of 48 x 48 (four per SIMD: 0.97x the step time of 8
   // waves of 96 x 48 on the 24 kHz decoder, while one wave per SIMD of 96 x 96 took 1.07x), or
   // 8 waves of 96 x 48; 96 x 192, 8 waves of 48 x 48;
   // 96 x 192, 4 waves of 96 x 48 (staged rows: positions plus a halo of up to 54 per segment)
-  return launch_first_fit<DmaConfig<2, 8, 3, 3, 496, 7, 1>, DmaConfig<1, 8, 6, 3, 496, 7, 1>, DmaConfig<2, 4, 3, 3, 368, 7, 1>,
-                          DmaConfig<1, 4, 6, 3, 368, 7, 1>>(p, ch, stream);
+  // (the same tiles for E4M3 weights)
+  if (fp8)
+    return launch_first_fit<DmaConfig<2, 8, 3, 3, 496, 7, 1, true>,
+                            DmaConfig<1, 8, 6, 3, 496, 7, 1, true>,
+                            DmaConfig<2, 4, 3, 3, 368, 7, 1, true>,
+                            DmaConfig<1, 4, 6, 3, 368, 7, 1, true>>(p, ch, stream);
+  return launch_first_fit<DmaConfig<2, 8, 3, 3, 496, 7, 1>,
+                            DmaConfig<1, 8, 6, 3, 496, 7, 1>,
+                            DmaConfig<2, 4, 3, 3, 368, 7, 1>,
+                            DmaConfig<1, 4, 6, 3, 368, 7, 1>>(p, ch, stream);
 }
 
 }  // namespace omni_conv

@@ -130,22 +130,28 @@ def snake64(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
 DMA_CASES = [(taps, k) for taps in (7, 1, 2) for k in range(1, DMA_LIST[taps] + 1)]
 
 
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
 @pytest.mark.parametrize("taps,config", DMA_CASES, ids=lambda v: str(v))
-def test_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, config):
-    gen = torch.Generator().manual_seed(100 * taps + config)
+def test_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, config, fp8):
+    """bf16 weights, or E4M3 weights kept as bytes in LDS and widened on the operand read (held
+    against the float64 conv with the dequantized weights)."""
+    gen = torch.Generator().manual_seed(100 * taps + config + 7 * fp8)
     if taps == 2:  # the polyphase transposed conv 192 -> 96, stride 6 (k = 12)
         c_in, c_out, stride = 192, 96, 6
-        w = bf(torch.randn(c_in, c_out, 2 * stride, generator=gen) / math.sqrt(2 * c_in))
+        w = torch.randn(c_in, c_out, 2 * stride, generator=gen) / math.sqrt(2 * c_in)
+        w = dequantize_fp8(*quantize_fp8(w, 1), 1) if fp8 else bf(w)
         b = bf(torch.randn(c_out, generator=gen) * 0.1)
-        packed = pack_conv_transpose1d(w, b, stride=stride).to(gpu)
-        plan_kw = dict(c_in=c_in, n_cols=stride * c_out, c_out=c_out, taps=2, left_pad=1)
+        packed = pack_conv_transpose1d(w, b, stride=stride, fp8=fp8).to(gpu)
+        plan_kw = dict(c_in=c_in, n_cols=stride * c_out, c_out=c_out, taps=2, left_pad=1, fp8=fp8)
     else:
         c_in = c_out = 192
         d = 9 if taps == 7 else 1
-        w = bf(torch.randn(c_out, c_in, taps, generator=gen) / math.sqrt(c_in * taps))
+        w = torch.randn(c_out, c_in, taps, generator=gen) / math.sqrt(c_in * taps)
+        w = dequantize_fp8(*quantize_fp8(w, 0), 0) if fp8 else bf(w)
         b = bf(torch.randn(c_out, generator=gen) * 0.1)
-        packed = pack_conv1d(w, b, dilation=d).to(gpu)
-        plan_kw = dict(c_in=c_in, n_cols=c_out, c_out=c_out, taps=taps, dilation=d)
+        packed = pack_conv1d(w, b, dilation=d, fp8=fp8).to(gpu)
+        plan_kw = dict(c_in=c_in, n_cols=c_out, c_out=c_out, taps=taps, dilation=d, fp8=fp8)
+    assert (packed.weight.dtype == torch.float8_e4m3fn) == fp8
     shape = pick_shape(plan_kw, N.CONV_KERNEL_DMA, config, streamed=True)
     assert shape is not None, "every LDS-DMA entry serves one of the test shapes"
     batch, length = shape

@@ -17,10 +17,12 @@ def test_list_lengths_match_the_forced_tile_sweep():
     for taps, n in DMA_LIST.items():
         c_out = 96
         n_cols = 6 * c_out if taps == 2 else c_out
-        plan = plan_shapes(batch=2, length=300, c_in=192, n_cols=n_cols, c_out=c_out, taps=taps,
-                           left_pad=1 if taps == 2 else None)
-        assert plan.kernel == N.CONV_KERNEL_DMA and plan.configs == n
-    staged = plan_shapes(batch=2, length=300, c_in=96, n_cols=192, c_out=192, taps=7, fp8=True)
+        for fp8 in (False, True):  # E4M3 weights take the same tile lists
+            plan = plan_shapes(batch=2, length=300, c_in=192, n_cols=n_cols, c_out=c_out,
+                               taps=taps, left_pad=1 if taps == 2 else None, fp8=fp8)
+            assert plan.kernel == N.CONV_KERNEL_DMA and plan.configs == n
+    staged = plan_shapes(batch=2, length=300, c_in=96, n_cols=192, c_out=192, taps=7, fp8=True,
+                         in_activation=N.ACT_SNAKE)
     assert staged.kernel == N.CONV_KERNEL_STAGED and staged.configs == STAGED_LIST
     s11 = plan_shapes(batch=2, length=300, c_in=64, n_cols=64, c_out=64, taps=11, dilation=5,
                       left_pad=25)
@@ -56,8 +58,10 @@ def test_forced_choice_contract():
         plan_shapes(**kw, kernel=N.CONV_KERNEL_FUSED_UNIT, config=1)
     with pytest.raises(N.OmniCodecError, match="status 2"):
         plan_shapes(**kw, kernel=N.CONV_KERNEL_DMA, config=DMA_LIST[7] + 1)
-    with pytest.raises(N.OmniCodecError, match="status 2"):  # fp8 weights never take LDS-DMA
-        plan_shapes(**kw, fp8=True, kernel=N.CONV_KERNEL_DMA, config=1)
+    # LDS-DMA copies the operand as it is: an operand activated on the way in never takes it
+    with pytest.raises(N.OmniCodecError, match="status 2"):
+        plan_shapes(**kw, in_activation=N.ACT_SNAKE, kernel=N.CONV_KERNEL_DMA, config=1)
+    assert plan_shapes(**kw, fp8=True, kernel=N.CONV_KERNEL_DMA, config=1).config == 1
     # an unknown family or a configuration without a family is an invalid argument
     with pytest.raises(N.OmniCodecError, match="status 1"):
         plan_shapes(**kw, kernel=9, config=1)
