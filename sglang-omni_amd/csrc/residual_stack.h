@@ -16,8 +16,11 @@
 //     [C/32][guard + rows][32] (64-byte rows, the 16-byte slots rotated by (row / 4) % 4 so the
 //     accumulator-layout writes and the operand reads both spread over all banks); guard rows
 //     ahead of row 0 keep the taps of the first rows inside the tile.
-//   * weights: the dilated conv's chunk [C][7 * 32 + 8] or the k = 1 conv's [C/32][C][32] in one
-//     LDS region, each prefetched into registers while the previous one is in use.
+//   * weights: by LDS DMA into a two-buffer ring of stages (a 32-channel chunk of the dilated
+//     conv, or the k = 1 conv), the next stage's DMA running during this stage's MFMAs; bf16
+//     weights as they are, E4M3 weights as bytes widened to bf16 (exactly) when read.
+//   * long rows (sweep): a workgroup runs consecutive tiles of one stream row, and each operand's
+//     last halo rows pass from one tile to the next through LDS instead of being recomputed.
 //   * streaming: rows left of position 0 of a stream row take each unit's own history copy (or
 //     zeros), and the workgroup that owns the last 6 * d positions of a row writes them as the
 //     unit's new history, as the one-unit kernel does.
@@ -141,7 +144,7 @@ __global__ void stack_coef_kernel(const StackParams p, float* table) {
   if (e < (p.nunits * kCoefRows + 2) * C) table[e] = stack_coef(p, e, C);
 }
 
-template <int C, int WCO, int WP, int TP, bool DMA = false, bool SWEEP = false>
+template <int C, int WCO, int WP, int TP, bool SWEEP = false, bool W8 = false>
 struct StackTile {
   static constexpr int NT = 64 * WCO * WP;
   static constexpr int TCO = C / (16 * WCO);
@@ -151,21 +154,22 @@ struct StackTile {
   // first row (zeros, or in the sweep the previous tile's last rows of the unit's operand)
   static constexpr int GUARD = SWEEP ? kSweepGuard : kGuard;
   static constexpr int UROWS = GUARD + R;
-  static constexpr int WROW = kTaps * kChunk + 8;
-  static constexpr int W1_PIECES = (C * kTaps * 4 + NT - 1) / NT;
-  static constexpr int W2_PIECES = (C * C / 8 + NT - 1) / NT;
-  static constexpr int WPR = W1_PIECES > W2_PIECES ? W1_PIECES : W2_PIECES;
-  // LDS DMA ring (bf16 weights): two buffers, each holding one stage of weights: the dilated
-  // conv's chunk kc for taps 0-3 or 4-6 ([C][ntaps * 32 + 8], rows an odd multiple of 16 bytes)
-  // or the k = 1 conv ([C/32][C][32]); a stage is whole 64-lane DMA instructions of 16 bytes.
-  static constexpr int P_LO = 4 * 4 + 1;  // 16-byte slots per weight row, taps 0-3 (+1 pad)
-  static constexpr int P_HI = 3 * 4 + 1;  // taps 4-6
+  // LDS DMA ring: two buffers, each holding one stage of weights as they are stored (bf16, or
+  // E4M3 bytes widened when read): the dilated conv's chunk kc ([C][ntaps * 32 elements + one
+  // 16-byte pad], rows an odd multiple of 16 bytes) for taps 0-3 or 4-6 (bf16) or all 7 taps
+  // (E4M3), or the k = 1 conv ([C/32][C][32]); a stage is whole 64-lane DMA instructions of 16
+  // bytes.
+  static constexpr int WE = W8 ? 1 : 2;              // bytes per weight
+  static constexpr int P_LO = W8 ? 7 * 2 + 1 : 4 * 4 + 1;  // 16-byte slots per weight row,
+                                                     // taps 0-6 (E4M3) or 0-3 (bf16), +1 pad
+  static constexpr int P_HI = 3 * 4 + 1;             // bf16 taps 4-6
   static constexpr int RING_SLOTS = (C * P_LO + 63) / 64 * 64;
   static constexpr int RING_ELEMS = RING_SLOTS * 8;
-  static constexpr int STAGES = 7;  // per unit: 3 chunks x 2 tap halves, then the k = 1 conv
-  static_assert(CH * C * 4 <= RING_SLOTS, "the k = 1 weights fit one ring buffer");
-  static constexpr int W_ELEMS = DMA ? 2 * RING_ELEMS
-                                     : (C * WROW > CH * C * kChunk ? C * WROW : CH * C * kChunk);
+  static constexpr int W2_SLOTS = CH * C * 2 * WE;   // the k = 1 conv's weights
+  static constexpr int CONV_STAGES = W8 ? CH : 2 * CH;  // per unit: chunks (x 2 tap halves)
+  static constexpr int STAGES = CONV_STAGES + 1;        // then the k = 1 conv
+  static_assert(W2_SLOTS <= RING_SLOTS, "the k = 1 weights fit one ring buffer");
+  static constexpr int W_ELEMS = 2 * RING_ELEMS;
   static constexpr int UNITS = SWEEP ? kSweepUnits : kMaxUnits;  // units the coefficients hold
   static constexpr int COEF = (UNITS * kCoefRows + 2) * C;  // floats
   // the sweep's halo store: per unit input operand and the final conv's, the previous tile's
@@ -176,21 +180,18 @@ struct StackTile {
            (size_t)HALO_ROWS * C * 2;
   }
   static_assert(C % (16 * WCO) == 0 && C % kChunk == 0, "tile shape");
-  static_assert(!SWEEP || (DMA && R % 16 == 0), "the sweep runs the DMA form on 16-row groups");
+  static_assert(R % 16 == 0, "staged rows in 16-row groups");
 };
 
-template <int C, int WCO, int WP, int TP, bool W_FP8, bool DMA, bool SWEEP>
+template <int C, int WCO, int WP, int TP, bool W_FP8, bool SWEEP>
 __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const StackParams p) {
-  static_assert(!(DMA && W_FP8), "the DMA ring copies bf16 weights as they are");
-  using Tile = StackTile<C, WCO, WP, TP, DMA, SWEEP>;
+  using Tile = StackTile<C, WCO, WP, TP, SWEEP, W_FP8>;
   constexpr int GUARD = Tile::GUARD;
   constexpr int NT = Tile::NT;
   constexpr int TCO = Tile::TCO;
   constexpr int CH = Tile::CH;
   constexpr int UROWS = Tile::UROWS;
-  constexpr int WROW = Tile::WROW;
   constexpr int PIECES_PER_ROW = C / 8;  // 16-byte pieces of a staged row
-  constexpr uint32_t WE = W_FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) u16 lds[];
   u16* us = lds;                        // operand / h tile
   u16* ws = lds + CH * UROWS * kChunk;  // weights
@@ -248,89 +249,50 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       *reinterpret_cast<u32x4*>(halo + e * 8) = u32x4{0u, 0u, 0u, 0u};
   }
 
-  u32x4 wr[W_FP8 ? 1 : Tile::WPR];
-  u32x2 wr8[W_FP8 ? Tile::WPR : 1];
-  auto load_w1 = [&](int k, int kc) __attribute__((always_inline)) {
-    const auto rs = buffer_rsrc(p.unit[k].w1, p.unit[k].w1_bytes);
-    const uint32_t base = (uint32_t)(kc * C * kTaps * kChunk);
-#pragma unroll
-    for (int u = 0; u < Tile::W1_PIECES; ++u) {
-      const int piece = tid + u * NT;
-      const uint32_t off = piece < C * kTaps * 4 ? (base + (uint32_t)piece * 8) * WE : kOutOfRange;
-      if constexpr (W_FP8) wr8[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
-      else wr[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-    }
-  };
-  auto load_w2 = [&](int k) __attribute__((always_inline)) {
-    const auto rs = buffer_rsrc(p.unit[k].w2, p.unit[k].w2_bytes);
-#pragma unroll
-    for (int u = 0; u < Tile::W2_PIECES; ++u) {
-      const int piece = tid + u * NT;
-      const uint32_t off = piece < C * C / 8 ? (uint32_t)piece * 8 * WE : kOutOfRange;
-      if constexpr (W_FP8) wr8[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
-      else wr[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-    }
-  };
-  auto wpiece = [&](int u) __attribute__((always_inline)) -> u32x4 {
-    if constexpr (W_FP8) return fp8x8_to_bf16x8(wr8[u]);
-    else return wr[u];
-  };
-  auto store_w1 = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < Tile::W1_PIECES; ++u) {
-      const int piece = tid + u * NT;
-      if (piece < C * kTaps * 4) {
-        const int nl = piece / (kTaps * 4);
-        const int rem = piece - nl * kTaps * 4;
-        *reinterpret_cast<u32x4*>(ws + nl * WROW + (rem >> 2) * kChunk + (rem & 3) * 8) = wpiece(u);
-      }
-    }
-  };
-  auto store_w2 = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < Tile::W2_PIECES; ++u) {
-      const int piece = tid + u * NT;
-      if (piece < C * C / 8) *reinterpret_cast<u32x4*>(ws + piece * 8) = wpiece(u);
-    }
-  };
-  // DMA of weight stage g (g = unit * 7 + r: r < 6 the dilated conv's chunk r / 2, taps 0-3 or
-  // 4-6; r = 6 the k = 1 conv) into ring buffer g % 2: this wave's share of the stage's 64-lane
-  // 16-byte instructions. Lane i of an instruction fills ring slot 64 * instr + i, so each lane
-  // loads the global piece that belongs in its slot (pad slots reload the chunk's first piece).
+  // DMA of weight stage g (g = unit * STAGES + r: r < CONV_STAGES the dilated conv's chunk, with
+  // bf16 weights r / 2 for taps 0-3 or 4-6, with E4M3 weights r for all taps; r = CONV_STAGES
+  // the k = 1 conv) into ring buffer g % 2: this wave's share of the stage's 64-lane 16-byte
+  // instructions. Lane i of an instruction fills ring slot 64 * instr + i, so each lane loads the
+  // global piece that belongs in its slot (pad slots reload the chunk's first piece).
   //
-  // The per-lane byte offsets of the two dilated-conv patterns (taps 0-3: 17 slots per column
-  // row, taps 4-6: 13) are the same for every chunk and unit up to the chunk's base, which goes
-  // in the scalar offset, so they are computed once here.
+  // The per-lane byte offsets of the dilated-conv patterns (bf16 taps 0-3: 17 slots per column
+  // row, taps 4-6: 13; E4M3 taps 0-6: 15) are the same for every chunk and unit up to the chunk's
+  // base, which goes in the scalar offset, so they are computed once here.
   constexpr int NWAVES = NT / 64;
   constexpr int LO_INSTRS = (C * Tile::P_LO + 63) / 64;
-  constexpr int HI_INSTRS = (C * Tile::P_HI + 63) / 64;
-  constexpr int W2_INSTRS = CH * C * 4 / 64;
+  constexpr int HI_INSTRS = W_FP8 ? 0 : (C * Tile::P_HI + 63) / 64;
+  constexpr int W2_INSTRS = Tile::W2_SLOTS / 64;
+  static_assert(Tile::W2_SLOTS % 64 == 0, "the k = 1 stage is whole DMA instructions");
   constexpr int LO_PER_WAVE = (LO_INSTRS + NWAVES - 1) / NWAVES;
   constexpr int HI_PER_WAVE = (HI_INSTRS + NWAVES - 1) / NWAVES;
-  uint32_t lo_off[DMA ? LO_PER_WAVE : 1], hi_off[DMA ? HI_PER_WAVE : 1];
-  if constexpr (DMA) {
+  uint32_t lo_off[LO_PER_WAVE], hi_off[HI_PER_WAVE > 0 ? HI_PER_WAVE : 1];
+  {
+    // slot j of column row n holds bytes j * 16 .. of the column's taps t0 .. t0 + nt - 1
+    // (packed [C][7][32] per chunk)
     auto slot_offset = [&](int di, int P, int t0, int nt) __attribute__((always_inline)) {
       const int slot = di * 64 + lane;
       const int n = slot / P;
       const int j = slot - n * P;
-      return (n < C && j < nt * 4)
-                 ? (uint32_t)(((n * kTaps + t0 + (j >> 2)) * kChunk + (j & 3) * 8) * 2) : 0u;
+      return (n < C && j < nt * 2 * Tile::WE)
+                 ? (uint32_t)((n * kTaps + t0) * kChunk * Tile::WE + j * 16) : 0u;
     };
 #pragma unroll
-    for (int i = 0; i < LO_PER_WAVE; ++i) lo_off[i] = slot_offset(wave + i * NWAVES, Tile::P_LO, 0, 4);
+    for (int i = 0; i < LO_PER_WAVE; ++i)
+      lo_off[i] = slot_offset(wave + i * NWAVES, Tile::P_LO, 0, W_FP8 ? kTaps : 4);
 #pragma unroll
     for (int i = 0; i < HI_PER_WAVE; ++i) hi_off[i] = slot_offset(wave + i * NWAVES, Tile::P_HI, 4, 3);
   }
   auto dma_stage = [&](int g) __attribute__((always_inline)) {
-    if constexpr (DMA) {
+    {
       const int k = g / Tile::STAGES;
       const int r = g - k * Tile::STAGES;
       if (k >= p.nunits) return;
       u16* buf = ws + (g & 1) * Tile::RING_ELEMS;
-      if (r < 6) {
+      if (r < Tile::CONV_STAGES) {
         const auto rs = buffer_rsrc(p.unit[k].w1, p.unit[k].w1_bytes);
-        const int chunk_base = (r >> 1) * C * kTaps * kChunk * 2;  // bytes
-        if (r & 1) {
+        const int chunk = W_FP8 ? r : r >> 1;
+        const int chunk_base = chunk * C * kTaps * kChunk * Tile::WE;  // bytes
+        if (!W_FP8 && (r & 1)) {
 #pragma unroll
           for (int i = 0; i < HI_PER_WAVE; ++i) {
             const int di = wave + i * NWAVES;
@@ -456,8 +418,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     }
   };
 
-  if constexpr (DMA) dma_stage(0);
-  else load_w1(0, 0);
+  dma_stage(0);
   if (tile == 0) __syncthreads();  // coefficients and guard rows
   // unit 0's operand
 #pragma unroll
@@ -480,11 +441,10 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     u16* hist = p.unit[k].hist;
     const auto hr = buffer_rsrc(hist, p.unit[k].hist_bytes);
     const int hstride = p.unit[k].hist_stride;
-    // the operand tile is complete (every wave's (f) of the previous unit); with the DMA ring
-    // the first weight stage's barrier is that point: (a) and (b) below touch only rows that the
-    // dilated conv reads after it
-    if constexpr (DMA) stage_begin(k * Tile::STAGES);
-    else __syncthreads();
+    // the operand tile is complete (every wave's (f) of the previous unit): the unit's first
+    // weight stage's barrier is that point; (a) and (b) below touch only rows that the dilated
+    // conv reads after it
+    stage_begin(k * Tile::STAGES);
     // (a) operand rows left of position 0 (segments that start a stream row): the history copy
     // of the row's slot, or zeros
     if (i0 == 0 && h > 0) {
@@ -532,21 +492,28 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     for (int c = 0; c < TCO; ++c)
 #pragma unroll
       for (int t = 0; t < TP; ++t) acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (DMA) {
-      for (int r = 0; r < 6; ++r) {
+    {
+      for (int r = 0; r < Tile::CONV_STAGES; ++r) {
         const int g = k * Tile::STAGES + r;
         if (r > 0) stage_begin(g);  // stage 0 began at the top of the unit
-        const int kc = r >> 1;
-        const int t0 = (r & 1) ? 4 : 0;
-        const int nt = (r & 1) ? 3 : 4;
-        const int P8 = (nt * 4 + 1) * 8;  // elements per weight row
-        const u16* wtap = ws + (g & 1) * Tile::RING_ELEMS + (wco0 + lrow) * P8 + lk;
+        const int kc = W_FP8 ? r : r >> 1;
+        const int t0 = (!W_FP8 && (r & 1)) ? 4 : 0;
+        const int nt = W_FP8 ? kTaps : ((r & 1) ? 3 : 4);
+        const int P8 = (W_FP8 ? Tile::P_LO : nt * 4 + 1) * 8;  // u16 elements per weight row
+        // the lane's 8 weights of tap t0 + jj: 16 bytes (bf16) or 8 (E4M3, widened when read)
+        const u16* wtap = ws + (g & 1) * Tile::RING_ELEMS + (wco0 + lrow) * P8 + (W_FP8 ? lk / 2 : lk);
         const u16* ukc = us + kc * UROWS * kChunk;
 #pragma unroll 1
         for (int jj = 0; jj < nt; ++jj) {
           bf16x8 a[TCO];
 #pragma unroll
-          for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * P8);
+          for (int c = 0; c < TCO; ++c) {
+            if constexpr (W_FP8)
+              a[c] = __builtin_bit_cast(
+                  bf16x8, fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(wtap + c * 16 * P8)));
+            else
+              a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * P8);
+          }
           const int rj = row0 + (t0 + jj) * d - h;
           const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
 #pragma unroll
@@ -556,48 +523,16 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
             for (int c = 0; c < TCO; ++c)
               acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
           }
-          wtap += kChunk;
-        }
-      }
-    } else {
-      for (int kc = 0; kc < CH; ++kc) {
-        if (kc > 0) __syncthreads();  // the previous chunk's weights are no longer read
-        store_w1();
-        __syncthreads();
-        if (kc + 1 < CH) load_w1(k, kc + 1);
-        else load_w2(k);
-        const u16* wtap = ws + (wco0 + lrow) * WROW + lk;
-        const u16* ukc = us + kc * UROWS * kChunk;
-#pragma unroll 1
-        for (int j = 0; j < kTaps; ++j) {
-          bf16x8 a[TCO];
-#pragma unroll
-          for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * WROW);
-          // rows row0 + j * d - h + 16 t: one rotation for every t
-          const int rj = row0 + j * d - h;
-          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
-#pragma unroll
-          for (int t = 0; t < TP; ++t) {
-            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
-#pragma unroll
-            for (int c = 0; c < TCO; ++c)
-              acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
-          }
-          wtap += kChunk;
+          wtap += kChunk * Tile::WE / 2;  // one tap: 32 weights
         }
       }
     }
     // every wave's reads of the operand tile (its rows are other waves' halo) and of the last
-    // tap half's weights are done before h overwrites the tile: with the DMA ring, the k = 1
-    // weights' stage barrier (its DMA ran during the last tap half) is that point
-    const u16* w2s = ws;
-    if constexpr (DMA) {
-      const int g = k * Tile::STAGES + 6;
-      stage_begin(g);
-      w2s = ws + (g & 1) * Tile::RING_ELEMS;
-    } else {
-      __syncthreads();
-    }
+    // conv stage's weights are done before h overwrites the tile: the k = 1 weights' stage
+    // barrier (its DMA ran during the last conv stage) is that point
+    const int g2 = k * Tile::STAGES + Tile::CONV_STAGES;
+    stage_begin(g2);
+    const u16* w2s = ws + (g2 & 1) * Tile::RING_ELEMS;
     // (d) h = Snake(acc * scale + bias) over the operand tile; the k = 1 weights
     const float* cf = coef + k * kCoefRows * C;
 #pragma unroll
@@ -617,20 +552,20 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    // (e) reads only the rows this wave wrote in (d), so no barrier is needed between them with
-    // the DMA ring (LDS operations of one wave complete in order)
-    if constexpr (!DMA) {
-      store_w2();
-      __syncthreads();
-      if (k + 1 < p.nunits) load_w1(k + 1, 0);
-    }
-    // (e) the k = 1 conv
+    // (e) the k = 1 conv; it reads only the rows this wave wrote in (d), so no barrier is needed
+    // between them (LDS operations of one wave complete in order)
 #pragma unroll
     for (int kc = 0; kc < CH; ++kc) {
       bf16x8 a[TCO];
 #pragma unroll
-      for (int c = 0; c < TCO; ++c)
-        a[c] = *reinterpret_cast<const bf16x8*>(w2s + (kc * C + wco0 + c * 16 + lrow) * kChunk + lk);
+      for (int c = 0; c < TCO; ++c) {
+        const int row = kc * C + wco0 + c * 16 + lrow;
+        if constexpr (W_FP8)  // the ring holds the E4M3 bytes: 32 per row
+          a[c] = __builtin_bit_cast(bf16x8, fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(
+                                                w2s + row * (kChunk / 2) + lk / 2)));
+        else
+          a[c] = *reinterpret_cast<const bf16x8*>(w2s + row * kChunk + lk);
+      }
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
         const bf16x8 bv = *reinterpret_cast<const bf16x8*>(
@@ -640,10 +575,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
           acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
       }
     }
-    // (f) overwrites only this wave's rows of the tile, which no other wave reads in (e); with the
-    // DMA ring the k = 1 weights' buffer is next written after the next unit's first stage
-    // barrier, so only the register-staged form (store_w1 of the next unit) needs one here
-    if constexpr (!DMA) __syncthreads();  // h and the k = 1 weights are no longer read
+    // (f) overwrites only this wave's rows of the tile, which no other wave reads in (e), and the
+    // k = 1 weights' buffer is next written after the next unit's first stage barrier: no
+    // barrier here
     // (f) x += acc * scale + bias; the next operand Snake(x) (the next unit's input Snake, or
     // the output Snake)
 #pragma unroll
@@ -784,14 +718,16 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   }  // tiles
 }
 
-// 96 channels, 8 waves, each with all 96 columns. fp8 weights are converted to bf16 on their way
-// to LDS, so they are staged through registers, and the register budget of two waves per SIMD
-// (x and the accumulators) leaves 32 of 256 staged rows per wave; bf16 weights arrive by LDS
-// DMA, which frees the staging registers: 48 of 384 rows per wave.
-using Stack96 = StackTile<96, 1, 8, 2>;
-using Stack96Dma = StackTile<96, 1, 8, 3, true>;
-using Stack96Sweep = StackTile<96, 1, 8, 3, true, true>;
+// 96 channels, 8 waves, each with all 96 columns and 48 of the 384 staged rows (the register
+// budget of two waves per SIMD: x and the accumulators); bf16 or E4M3 weights by LDS DMA.
+using Stack96Dma = StackTile<96, 1, 8, 3>;
+using Stack96Sweep = StackTile<96, 1, 8, 3, true>;
+using Stack96Dma8 = StackTile<96, 1, 8, 3, false, true>;
+using Stack96Sweep8 = StackTile<96, 1, 8, 3, true, true>;
 static_assert(Stack96Sweep::lds_bytes() <= 160 * 1024, "the sweep form fits the CU's LDS");
+static_assert(Stack96Sweep8::lds_bytes() <= Stack96Sweep::lds_bytes() &&
+              Stack96Dma8::R == Stack96Dma::R && Stack96Sweep8::R == Stack96Dma::R,
+              "E4M3 weights take the bf16 forms' tiles");
 
 template <bool W_FP8>
 int launch_stack96(const StackParams& p, int grid, bool sweep, hipStream_t stream);

@@ -125,7 +125,7 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   if (any_hist && (!a->slot_index || !a->slot_parity || a->hist_num_slots < 1))
     return OMNI_ERR_INVALID_ARG;
   if (a->batch == 0 || a->length == 0) return OMNI_OK;
-  const int64_t R = fp8 ? Stack96::R : Stack96Dma::R;  // staged rows per tile
+  const int64_t R = Stack96Dma::R;  // staged rows per tile (both weight formats)
   if (H + 16 > R) return OMNI_ERR_UNSUPPORTED;
 
   // byte extents (buffer offsets are 32-bit)
@@ -204,14 +204,14 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
     p.fin_o_sb = a->final_out_stride_b;
   }
 
-  // Long rows with bf16 weights: the sweep (each workgroup runs consecutive tiles of one row,
+  // Long rows: the sweep (each workgroup runs consecutive tiles of one row,
   // the causal halo staged once per workgroup instead of once per tile), one workgroup per
   // compute unit where the rows allow. Otherwise long rows take tiles inside one row, as many as
   // the staged rows need, evened out; short rows as many whole rows (each with its halo) as the
   // staged rows hold.
   int64_t grid;
   bool sweep = false;
-  if (!fp8 && L + H > R && a->num_units <= kSweepUnits) {
+  if (L + H > R && a->num_units <= kSweepUnits) {
     int64_t halo_rows = fin ? a->final_taps - 1 : 0;
     bool fits = halo_rows <= kSweepGuard;
     for (int k = 0; k < a->num_units; ++k) {
@@ -250,6 +250,6 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   }
   if (grid > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  return fp8 ? launch_stack96<true>(p, (int)grid, false, s)
+  return fp8 ? launch_stack96<true>(p, (int)grid, sweep, s)
              : launch_stack96<false>(p, (int)grid, sweep, s);
 }

@@ -85,11 +85,16 @@ def test_residual_stack_equals_one_launch_per_unit_bitwise(gpu, batch, length, d
     assert ref_x.abs().max().item() > 0.5  # the units change x
 
 
-def test_residual_stack_fp8_weights_equal_one_launch_per_unit_bitwise(gpu):
-    units, out_a, out_b = make_units((1, 3, 9), gpu, fp8=True, seed=3)
+@pytest.mark.parametrize("batch,length", [(4, 700), (64, 12), (3, 37), (1, 2000), (2, 1000)])
+@pytest.mark.parametrize("dilations", [(1, 3, 9), (2,)])
+def test_residual_stack_fp8_weights_equal_one_launch_per_unit_bitwise(gpu, batch, length,
+                                                                      dilations):
+    """E4M3 weights: the stack (tiled form for short rows, the sweep for long ones, the weights'
+    bytes staged by LDS DMA and widened when read) against one launch per unit."""
+    units, out_a, out_b = make_units(dilations, gpu, fp8=True, seed=3 + length)
     gen = torch.Generator().manual_seed(1)
-    x = (torch.randn(4, 700, C, generator=gen) * 0.3).to(gpu)
-    out = torch.empty(4, 700, C, dtype=torch.bfloat16, device=gpu)
+    x = (torch.randn(batch, length, C, generator=gen) * 0.3).to(gpu)
+    out = torch.empty(batch, length, C, dtype=torch.bfloat16, device=gpu)
     x_out = torch.empty_like(x)
     residual_stack(x, units, out, out_a, out_b, x_out=x_out)
     ref_u, ref_x = unit_by_unit(x, units, out_a, out_b)
