@@ -208,6 +208,11 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
   const f32x4 act_a = *reinterpret_cast<const f32x4*>(coef + kActA * BCO + q * 4);
   const f32x4 act_b = *reinterpret_cast<const f32x4*>(coef + kActB * BCO + q * 4);
   const float inv_l = 1.f / (float)L;
+  // Packed tensors (row stride = length x position stride, the decoders' usual layout) address a
+  // position by its flat index m alone; otherwise m splits into (row, position). Element offsets
+  // fit 32 bits (the byte extents are below 2 GiB).
+  const bool packed = p.r_sb == (int64_t)L * p.r_st && p.o_sb == (int64_t)L * p.o_st;
+  const uint32_t r_st = (uint32_t)p.r_st, o_st = (uint32_t)p.o_st;
   for (int pass = 0; pass * EPI_WAVES < WAVES_P; ++pass) {
     __syncthreads();
     const int wl = wave_p - pass * EPI_WAVES;  // this wave's slot in the pass
@@ -236,13 +241,21 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
       for (int u = 0; u < U; ++u) {
         const int r = min(r0 + u * RSTEP, prow - 1);
         const int m = mp + r;
-        int b = (int)((float)m * inv_l);  // m / L, corrected below
-        int i = m - b * L;
-        if (i < 0) { --b; i += L; }
-        if (i >= L) { ++b; i -= L; }
+        uint32_t re, oe;
+        if (packed) {
+          re = (uint32_t)m * r_st + n_q;
+          oe = (uint32_t)m * o_st + n_q;
+        } else {
+          int b = (int)((float)m * inv_l);  // m / L, corrected below
+          int i = m - b * L;
+          if (i < 0) { --b; i += L; }
+          if (i >= L) { ++b; i -= L; }
+          re = (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q);
+          oe = (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q);
+        }
         const bool ok = live && r0 + u * RSTEP < prow;
-        roff[u] = ok ? (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q) * 4 : kOutOfRange;
-        ooff[u] = ok ? (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q) : kOutOfRange;
+        roff[u] = ok ? re * 4 : kOutOfRange;
+        ooff[u] = ok ? oe : kOutOfRange;
         v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
       }
       if (p.residual) {
