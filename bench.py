@@ -15,7 +15,8 @@ Prints one JSON line: audio-seconds decoded per wall-second (xRT), plus
   cpu_baseline  the float32 CPU restatement of the reference path (oracle/codec_oracle.py) timed
                 on this host's cores on a bounded sample of the same workload;
   other_configs the xRT of the other decoder configurations: the single 20 s utterance, the
-                HiFiGAN mel vocoder (16 x 10 s) and the fp8-weight long form (8 x 120 s);
+                HiFiGAN mel vocoder (16 x 10 s) and the fp8-weight long form (8 x 120 s), with
+                the same long form on bf16 weights beside it;
   hift_transforms  HiFT's source spectrum and fused iSTFT tail at the HiFiGAN size, in HBM GB/s;
   qwen3_code2wav the Qwen3-Omni code2wav (pre-transformer + ConvNeXt + decoder) streaming 64
                 streams x 12-frame chunks, eager and HIP-graph replayed, per-kind kernel times;
@@ -207,6 +208,7 @@ def bench_streaming(args, device) -> dict:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": PMC_TRAFFIC_BYTES.get(dom_kind),
+                     "traffic_source": PMC_TRAFFIC_SOURCE.get(dom_kind),
                      "kernel": KERNEL_NAMES.get(dom_kind, dom_kind),
                      "launches_per_step": dom["launches"] / inst_steps,
                      "flops_per_launch": dom_flops_launch, "mean_launch_ms": dom_ms_launch},
@@ -225,10 +227,13 @@ def bench_streaming(args, device) -> dict:
 
 
 # HBM bytes per launch of the roofline kernel, from two rocprofv3 --pmc runs of
-# `bench.py --only stack96` (FETCH_SIZE, then WRITE_SIZE), each scaled by the same counter's
-# reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB, WRITE_SIZE =
-# 1024 MiB: fetch x 2, write x 1).
-PMC_TRAFFIC_BYTES = {"stack96": (385682 * 2 + 5836) * 1024}
+# `bench.py --only stack96` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by the
+# same counter's reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB,
+# WRITE_SIZE = 1024 MiB: fetch x 2, write x 1). Measured, not computed here: re-measure after a
+# change to the kernel (profiles/residual_stack96_pmc.md holds the runs and their commands).
+PMC_TRAFFIC_BYTES = {"stack96": (307375 * 2 + 7952) * 1024}
+PMC_TRAFFIC_SOURCE = {"stack96": "profiles/residual_stack96_pmc.md: rocprofv3 FETCH_SIZE + "
+                                 "WRITE_SIZE of `bench.py --only stack96`, copy-calibrated"}
 
 
 def run_only(args, device) -> None:
