@@ -11,10 +11,9 @@ from __future__ import annotations
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import codec_oracle as O
-from sglang_omni_amd import _native as N
-from sglang_omni_amd.kernels.conv import fused_conv, pack_conv1d
 from sglang_omni_amd.kernels.rvq import rvq_gather_sum
 from sglang_omni_amd.models import (
     DacCodecDecoder,
@@ -25,6 +24,8 @@ from sglang_omni_amd.models import (
 )
 from sglang_omni_amd.models.configs import CODEC_24K, CODEC_24K_LONG, HIFIGAN_24K
 from sglang_omni_amd.quantization import reference_weights
+from sglang_omni_amd.utils.channels_last_conv import channels_last_conv1d
+from sglang_omni_amd.utils.snake_beta import snake1d
 
 pytestmark = pytest.mark.gpu
 
@@ -55,9 +56,11 @@ def tiny(gpu, request):
 
 
 def test_single_conv_block_workload(gpu):
-    """RVQ (K=8, 1024 x 256 tables ~ N(0, 0.02), int32 codes, T=50) -> causal conv 256->256 k=7 ->
-    Snake(alpha=1) -> + x. The gather-sum is bit-exact in fp32; the block runs the bf16 MFMA
-    conv with the Snake + residual epilogue."""
+    """The fp32 single-block workload: RVQ (K=8, 1024 x 256 tables ~ N(0, 0.02), int32 codes,
+    T=50) -> causal conv 256->256 k=7 -> Snake(alpha=1) -> + x, all in float32 on the GPU. The
+    gather-sum is bit-exact; the conv is the direct-sum float32 kernel (the layer is fp32, so no
+    bf16 operand is formed) and Snake the float32 kernel, held to float32-summation tolerance
+    against the float32 oracle."""
     torch.manual_seed(0)
     tables = torch.randn(8, 1024, 256) * 0.02
     codes = torch.randint(0, 1024, (1, 8, 50), dtype=torch.int32)
@@ -67,17 +70,16 @@ def test_single_conv_block_workload(gpu):
     x_ref, y_ref = O.conv_block(codes, tables, w, b, alpha)
     x = rvq_gather_sum(codes.to(gpu), tables.to(gpu))  # [1, 50, 256] fp32
     assert torch.equal(x.cpu(), x_ref.transpose(1, 2))
-    packed = pack_conv1d(w, b).to(gpu)
-    y = torch.empty(1, 50, 256, dtype=torch.float32, device=gpu)
-    # y = x + Snake(conv(x)): the conv's epilogue applies Snake, then the residual adds x
-    snake = torch.empty(1, 50, 256, dtype=torch.float32, device=gpu)
-    fused_conv(x.to(torch.bfloat16), packed, snake, activation=N.ACT_SNAKE,
-               act_a=alpha.to(gpu), act_b=(alpha + 1e-9).reciprocal().to(gpu))
-    y = x + snake
-    # bf16 rounding of x and W is the only approximation: relative error ~ 2^-8 of the conv term
+    # the causal conv's input carries its left context (6 zero rows), as the reference's
+    # channels-last API takes it
+    padded = F.pad(x, (0, 0, 6, 0))
+    c = channels_last_conv1d(padded, conv, w.to(gpu), b.to(gpu), 50)
+    assert c.dtype == torch.float32 and c.shape == (1, 50, 256)
+    y = x + snake1d(c, alpha.to(gpu))
     conv_ref = O.causal_conv1d(x_ref, w, b)
     scale = conv_ref.abs().max().item()
-    torch.testing.assert_close(y.cpu().transpose(1, 2), y_ref, rtol=0, atol=2e-2 * scale)
+    torch.testing.assert_close(c.cpu().transpose(1, 2), conv_ref, rtol=1e-5, atol=1e-5 * scale)
+    torch.testing.assert_close(y.cpu().transpose(1, 2), y_ref, rtol=1e-5, atol=1e-5 * scale)
 
 
 def test_tiny_decoder_matches_the_oracle(gpu, tiny):
