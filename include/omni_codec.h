@@ -100,7 +100,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 6: omni_conv1d_plan / omni_conv1d_fused_with */
+int omni_codec_abi_version(void); /* 7: omni_conv1d_splitk */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -231,6 +231,23 @@ enum {
 
 int omni_conv1d_fused_with(const omni_conv_args* args, int kernel, int config,
                            omni_stream_t stream);
+
+/*
+ * Split-K form of a k = 1 conv used as a GEMM (replaces the plain GEMMs of the code2wav
+ * pre-transformer, `F.linear` in sglang_omni/models/qwen3_omni/components/code2wav.py:266,311,
+ * 318,322, and of the ConvNeXt blocks' pointwise convs, incremental_codec.py:174-175): the
+ * LDS-DMA kernel runs k_splits slices of the 32-channel chunks of each tile, each writing its
+ * float32 partial tile [positions][n_cols] into `workspace` (k_splits * batch * length * n_cols
+ * floats, 16-byte aligned), then a reduction sums the slices in slice order and applies the bias
+ * and the bf16 / float32 store. The summation order depends on (c_in, k_splits) only, never on
+ * the row count, so a caller that fixes k_splits per layer gets the same bits for a row whatever
+ * batch it runs in. Takes: taps = 1, a bf16 operand without in_activation, bf16 weights, no
+ * weight2, history, residual, mix, sum_out or activation; c_in a multiple of 32 * k_splits.
+ * k_splits = 1 is omni_conv1d_fused. kernel / config as in omni_conv1d_fused_with
+ * (OMNI_CONV_KERNEL_AUTO / 0, or OMNI_CONV_KERNEL_DMA and an entry of its list).
+ */
+int omni_conv1d_splitk(const omni_conv_args* args, int64_t k_splits, float* workspace,
+                       int64_t workspace_bytes, int kernel, int config, omni_stream_t stream);
 int omni_conv1d_plan(const omni_conv_args* args, int kernel, int config, int* kernel_out,
                      int* config_out, int* configs_in_list, int64_t* workgroups);
 

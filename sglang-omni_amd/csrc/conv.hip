@@ -206,19 +206,55 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
   p.hist_bytes = (uint32_t)hist_bytes;
   p.r_bytes = (uint32_t)r_bytes;
   p.o_bytes = (uint32_t)o_bytes;
+  p.k_splits = 1;
+  p.partial = nullptr;
   return OMNI_OK;
+}
+
+// The split-K reduction: out[m][n] = (sum over slices s = 0, 1, .. of partial[s][m][n], in slice
+// order) * scale[n] + bias[n % c_out], stored as the conv epilogue stores it (bf16 rounded to
+// nearest even, or float32). One thread per 4 columns of one position.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(
+    const float* partial, int splits, int64_t slice, int n_cols, int c_out, int length,
+    int quads, const float* scale, const float* bias, void* out, int out_bf16, int64_t o_sb,
+    int64_t o_st) {
+  const int e = blockIdx.x * 256 + threadIdx.x;  // a slice holds below 2^31 bytes
+  if (e >= quads) return;
+  const int nq = n_cols / 4;
+  const int m = e / nq;
+  const int n = (e - m * nq) * 4;
+  const float* src = partial + (int64_t)m * n_cols + n;
+  f32x4 v = *reinterpret_cast<const f32x4*>(src);
+  for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4*>(src + s * slice);
+  f32x4 sc = f32x4{1.f, 1.f, 1.f, 1.f}, bi = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (scale) sc = *reinterpret_cast<const f32x4*>(scale + n);
+  if (bias) {
+    const int co = n % c_out;  // c_out is a multiple of 4: the 4 columns share a phase
+    bi = f32x4{bias[co], bias[co + 1], bias[co + 2], bias[co + 3]};
+  }
+  v = v * sc + bi;
+  const int b = m / length;
+  const int64_t off = b * o_sb + (int64_t)(m - b * length) * o_st + n;
+  if (out_bf16) {
+    *reinterpret_cast<u32x2*>(static_cast<u16*>(out) + off) =
+        u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  } else {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + off) = v;
+  }
 }
 
 }  // namespace omni_conv
 
 namespace {
 
-// Validate, then choose (and launch unless `launch` is false) through dispatch.
+// Validate, then choose (and launch unless `launch` is false) through dispatch. k_splits > 1: the
+// split-K form (see omni_conv1d_splitk) with its float32 partials in `workspace`.
 int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int* kernel_out,
-               int* config_out, int* count_out, int64_t* workgroups_out, omni_stream_t stream) {
+               int* config_out, int* count_out, int64_t* workgroups_out, omni_stream_t stream,
+               int64_t k_splits = 1, float* workspace = nullptr, int64_t workspace_bytes = 0) {
   using namespace omni_conv;
   if (kernel < OMNI_CONV_KERNEL_AUTO || kernel > OMNI_CONV_KERNEL_FUSED_UNIT || config < 0 ||
-      (kernel == OMNI_CONV_KERNEL_AUTO && config != 0))
+      (kernel == OMNI_CONV_KERNEL_AUTO && config != 0) || k_splits < 1)
     return OMNI_ERR_INVALID_ARG;
   ConvParams p;
   bool x_f32 = false, fp8 = false, fuse2 = false;
@@ -227,11 +263,38 @@ int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int
     if (status < 0 && kernel_out) *kernel_out = OMNI_CONV_KERNEL_AUTO;  // nothing to launch
     return status < 0 ? OMNI_OK : status;
   }
+  const int64_t positions = a->batch * a->length;
+  if (k_splits > 1) {
+    // the GEMM form: a k = 1 conv of a bf16 operand with bf16 weights, bias only, no history,
+    // residual, mix, float32 sum or activation; whole chunks per slice
+    if (a->taps != 1 || fp8 || fuse2 || x_f32 || a->in_activation != OMNI_ACTIVATION_NONE ||
+        a->hist_pool || a->residual || a->mix_a || a->sum_out || !a->out ||
+        a->activation != OMNI_ACTIVATION_NONE)
+      return OMNI_ERR_UNSUPPORTED;
+    if (a->c_in % (32 * k_splits) || k_splits > 64) return OMNI_ERR_UNSUPPORTED;
+    if (kernel != OMNI_CONV_KERNEL_AUTO && kernel != OMNI_CONV_KERNEL_DMA)
+      return OMNI_ERR_UNSUPPORTED;
+    const int64_t slice = positions * a->n_cols;
+    if (slice * 4 > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
+    if (launch && (!workspace || !aligned16(workspace) || workspace_bytes < k_splits * slice * 4))
+      return OMNI_ERR_INVALID_ARG;
+    p.k_splits = (int)k_splits;
+    p.partial = workspace;
+  }
   Choice ch;
   ch.force = config;
   ch.launch = launch;
   int family = kernel;
-  const int r = dispatch(p, x_f32, fp8, fuse2, family, ch, reinterpret_cast<hipStream_t>(stream));
+  int r = dispatch(p, x_f32, fp8, fuse2, family, ch, reinterpret_cast<hipStream_t>(stream));
+  if (r == OMNI_OK && launch && k_splits > 1) {
+    const int quads = (int)(positions * a->n_cols / 4);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), p.partial, p.k_splits,
+                       positions * a->n_cols, p.n_cols, p.c_out, p.length, quads, p.wscale,
+                       p.bias, p.out, p.out_bf16, p.o_sb, p.o_st);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) r = OMNI_ERR_LAUNCH;
+  }
   if (r == OMNI_OK) {
     if (kernel_out) *kernel_out = family;
     if (config_out) *config_out = ch.chosen;
@@ -251,6 +314,14 @@ extern "C" int omni_conv1d_fused_with(const omni_conv_args* a, int kernel, int c
                                       omni_stream_t stream) {
   if (kernel == OMNI_CONV_KERNEL_AUTO || config < 1) return OMNI_ERR_INVALID_ARG;
   return conv_entry(a, kernel, config, true, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int omni_conv1d_splitk(const omni_conv_args* a, int64_t k_splits, float* workspace,
+                                  int64_t workspace_bytes, int kernel, int config,
+                                  omni_stream_t stream) {
+  if ((kernel == OMNI_CONV_KERNEL_AUTO) != (config == 0)) return OMNI_ERR_INVALID_ARG;
+  return conv_entry(a, kernel, config, true, nullptr, nullptr, nullptr, nullptr, stream, k_splits,
+                    workspace, workspace_bytes);
 }
 
 extern "C" int omni_conv1d_plan(const omni_conv_args* a, int kernel, int config, int* kernel_out,

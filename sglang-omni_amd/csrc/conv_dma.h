@@ -66,7 +66,8 @@ struct DmaTile {
 
 // The ring takes most of a CU's LDS, so one workgroup runs per CU: WAVES_CO * WAVES_P / 4 waves
 // per SIMD, which the register allocation may assume.
-template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8>
+template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8,
+          bool SPLIT>
 __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     __attribute__((amdgpu_waves_per_eu(WAVES_CO * WAVES_P / 4, WAVES_CO * WAVES_P / 4)))
     conv_dma_kernel(const ConvParams p) {
@@ -88,8 +89,14 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   // round-robin (workgroup b to XCD b % 8), each XCD with its own L2: renumbered so that XCD x
   // runs the contiguous range x of logical tiles, and with the column tile fastest in that order
   // the workgroups sharing an input tile run on one XCD, back to back, and read it from its L2.
-  const int n_tile = xcd_tile(blockIdx.x, gridDim.x) % p.n_tiles;
-  const int p_tile = xcd_tile(blockIdx.x, gridDim.x) / p.n_tiles;
+  // With split-K the K slice is the slowest index: slice s covers chunks [s * chunks / splits,
+  // (s + 1) * chunks / splits) of every tile.
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int splits = SPLIT ? p.k_splits : 1;
+  const int split = SPLIT ? tile / (p.p_tiles * p.n_tiles) : 0;
+  const int in_split = SPLIT ? tile - split * (p.p_tiles * p.n_tiles) : tile;
+  const int n_tile = in_split % p.n_tiles;
+  const int p_tile = in_split / p.n_tiles;
   const int n0 = n_tile * BCO;
 
   const int dil = p.dil;
@@ -100,7 +107,8 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   const int H = lpad;
   const int c_in = p.c_in;
   const int n_cols = p.n_cols;
-  const int chunks = c_in / kChunk;  // the launcher requires c_in % (32 KC) == 0
+  const int chunks = c_in / kChunk / splits;  // the launcher requires c_in % (32 KC splits) == 0
+  const int c_first = split * chunks;          // the slice's first chunk
   const int stages = chunks / KC;
 
   // The tile's positions [m0, m_end) of the flattened (row, position) space and its row segments
@@ -187,8 +195,24 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     woff[u] = (n < BCO && piece < Tile::WSLOTS) ? (uint32_t)(n * Tile::WSLOTS + piece) * 16 : 0u;
   }
 
+  // A split-K slice stores its raw float32 partial tile: the epilogue without scale, bias,
+  // residual or activation, into the slice's part of the partial buffer.
+  ConvParams q = p;
+  if constexpr (SPLIT) {
+    q.wscale = nullptr;
+    q.bias = nullptr;
+    q.residual = nullptr;
+    q.mix_a = nullptr;
+    q.mix_b = nullptr;
+    q.out = nullptr;
+    q.act = OMNI_ACT_NONE;
+    q.sum_out = p.partial + (int64_t)split * M * n_cols;
+    q.r_st = n_cols;
+    q.r_sb = (int64_t)L * n_cols;
+    q.r_bytes = (uint32_t)((int64_t)M * n_cols * 4);
+  }
   float* coef = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds) + Tile::coef_offset);
-  stage_coefficients<BCO, NT, false>(p, coef, n0);
+  stage_coefficients<BCO, NT, false>(q, coef, n0);
 
   auto xs_of = [&](int buf, int c) __attribute__((always_inline)) -> u16* {
     return lds + buf * Tile::BUF + c * (Tile::XCHUNK + Tile::WCHUNK);
@@ -217,7 +241,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     const int buf = s & 1;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-      const int kc = s * KC + c;
+      const int kc = c_first + s * KC + c;
       {
         u16* xs = xs_of(buf, c);
         u16* ws = xs + Tile::XCHUNK;
@@ -253,7 +277,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     const int buf = s & 1;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-      const int kc = s * KC + c;
+      const int kc = c_first + s * KC + c;
       {
         const u16* xs = xs_of(buf, c);
 #pragma unroll
@@ -335,11 +359,12 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     }
   }
 
-  conv_epilogue<typename Tile::Base, WAVES_P, TCO, TP>(p, acc, lds, coef, kScale, kBias, n0, m0,
+  conv_epilogue<typename Tile::Base, WAVES_P, TCO, TP>(q, acc, lds, coef, kScale, kBias, n0, m0,
                                                        m_end, wave_p, wco0);
 }
 
-template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false>
+template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false,
+          bool SPLIT = false>
 struct DmaConfig {
   using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
 
@@ -357,24 +382,26 @@ struct DmaConfig {
   // conv_mfma_kernel's narrower tiles).
   static bool fits(const ConvParams& p) {
     const int64_t padded = (p.n_cols + Tile::BCO - 1) / Tile::BCO * Tile::BCO;
-    return p.taps == TAPS && p.c_in % (kChunk * KC) == 0 && rows_needed(p) <= MAX_ROWS &&
+    return p.taps == TAPS && (p.k_splits > 1) == SPLIT &&
+           p.c_in % (kChunk * KC * p.k_splits) == 0 && rows_needed(p) <= MAX_ROWS &&
            (padded - p.n_cols) * 8 <= p.n_cols;
   }
 
   static int64_t workgroups(const ConvParams& p) {
     const int64_t positions = (int64_t)p.batch * p.length;
-    return ((positions + Tile::BP - 1) / Tile::BP) * ((p.n_cols + Tile::BCO - 1) / Tile::BCO);
+    return ((positions + Tile::BP - 1) / Tile::BP) * ((p.n_cols + Tile::BCO - 1) / Tile::BCO) *
+           p.k_splits;
   }
 
   static int launch(ConvParams p, hipStream_t stream) {
     const int64_t positions = (int64_t)p.batch * p.length;
     p.p_tiles = (int)((positions + Tile::BP - 1) / Tile::BP);
     p.n_tiles = (int)((p.n_cols + Tile::BCO - 1) / Tile::BCO);
-    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
+    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, SPLIT>;
     // raised once per instantiation, on its first launch (no attribute calls inside a capture)
     static const bool raised = raise_lds_limit((const void*)k);
     (void)raised;
-    hipLaunchKernelGGL(k, dim3((unsigned)(p.p_tiles * p.n_tiles)), dim3(Tile::NT),
+    hipLaunchKernelGGL(k, dim3((unsigned)(p.p_tiles * p.n_tiles * p.k_splits)), dim3(Tile::NT),
                        Tile::lds_bytes, stream, p);
     OMNI_LAUNCH_CHECK();
     return OMNI_OK;

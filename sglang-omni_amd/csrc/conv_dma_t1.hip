@@ -13,6 +13,11 @@ int launch_dma_taps1(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stre
                             DmaConfig<2, 4, 6, 3, 192, 1, 2, true>,
                             DmaConfig<2, 4, 3, 3, 192, 1, 3, true>,
                             DmaConfig<1, 8, 6, 2, 256, 1, 2, true>>(p, ch, stream);
+  if (p.k_splits > 1)  // split-K (bf16 weights): the same tiles, each a K slice of a tile
+    return launch_first_fit<DmaConfig<4, 4, 3, 3, 192, 1, 2, false, true>,
+                            DmaConfig<2, 4, 6, 3, 192, 1, 2, false, true>,
+                            DmaConfig<2, 4, 3, 3, 192, 1, 3, false, true>,
+                            DmaConfig<1, 8, 6, 2, 256, 1, 2, false, true>>(p, ch, stream);
   return launch_first_fit<DmaConfig<4, 4, 3, 3, 192, 1, 2>,
                             DmaConfig<2, 4, 6, 3, 192, 1, 2>,
                             DmaConfig<2, 4, 3, 3, 192, 1, 3>,

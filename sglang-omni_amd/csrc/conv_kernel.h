@@ -78,6 +78,10 @@ struct ConvParams {
   const float* act_b;
   float slope;
   int p_tiles, n_tiles;
+  // split-K (LDS-DMA k = 1 convs only): k_splits slices of whole 32-channel chunks, slice s
+  // writing its float32 partial tile [positions][n_cols] at partial + s * positions * n_cols
+  int k_splits;
+  float* partial;
   // byte extents of the buffers the kernel reads and writes (each below 2 GiB)
   uint32_t x_bytes, w_bytes, w2_bytes, hist_bytes, r_bytes, o_bytes;
 };

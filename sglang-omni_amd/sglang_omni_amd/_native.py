@@ -41,7 +41,7 @@ class OmniCodecError(RuntimeError):
 
 INVALID_ARG = 1
 UNSUPPORTED = 2
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # kernel families of omni_conv1d_fused (omni_conv1d_plan / omni_conv1d_fused_with)
 CONV_KERNEL_AUTO, CONV_KERNEL_DMA, CONV_KERNEL_STAGED, CONV_KERNEL_STAGED11, CONV_KERNEL_FUSED_UNIT = range(5)
@@ -179,6 +179,7 @@ SIGNATURES: dict[str, list] = {
                             _PTR, _INT, _I64, _I64, _I64, _INT, _PTR],
     "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
     "omni_conv1d_fused_with": [ctypes.POINTER(ConvArgs), _INT, _INT, _PTR],
+    "omni_conv1d_splitk": [ctypes.POINTER(ConvArgs), _I64, _PTR, _I64, _INT, _INT, _PTR],
     "omni_conv1d_plan": [ctypes.POINTER(ConvArgs), _INT, _INT, ctypes.POINTER(_INT),
                          ctypes.POINTER(_INT), ctypes.POINTER(_INT), ctypes.POINTER(_I64)],
     "omni_residual_stack": [ctypes.POINTER(ResidualStackArgs), _PTR],

@@ -12,7 +12,7 @@ A decode step on channels-last activations:
     rvq_gather_sum (mean form)            codes -> h (float32 residual stream)
     per layer (8):
       rms_norm_residual                   h -> normed (bf16)
-      GEMM qkv (hipBLASLt)                normed -> qkv
+      GEMM qkv (k = 1 conv kernel)        normed -> qkv
       rope_kv_write                       rotary on q, k in place; new K / V into the rings
       window_attention                    q over the 72-frame window -> attn
       GEMM o                              attn -> o
@@ -26,6 +26,13 @@ A decode step on channels-last activations:
                                           r += gamma * (...); the next operand (bf16)
     the causal conv stack of ``DacCodecDecoder`` with SnakeBeta coefficients, transposed convs
     trimmed on both sides and the final clamp.
+
+The GEMMs run on the LDS-DMA conv kernel as k = 1 convs (the linear weight [out, in] packed once
+as a conv weight [out, in, 1]): bf16 operands, float32 accumulation in a fixed order (32-input
+chunks ascending; for the layers with long inputs and few outputs, split-K: slices of the input
+chunks summed in slice order, the slice count fixed per layer by its shape), rounded once to the
+bf16 output. The order does not depend on the row count, so a stream decoded in chunks gives the
+bits of its whole decode.
 """
 
 from __future__ import annotations
@@ -36,7 +43,7 @@ from typing import Any
 import torch
 
 from ..kernels import code2wav_front as F
-from ..kernels.conv import fused_conv, pack_conv1d, pack_conv_transpose1d
+from ..kernels.conv import fused_conv, gemm, pack_conv1d, pack_conv_transpose1d
 from ..kernels.rvq import rvq_gather_sum
 from .configs import Qwen3Code2WavConfig, Qwen3TTSCodecConfig
 from .dac_codec import CodecStatePool, DacCodecDecoder, _Workspace
@@ -104,9 +111,34 @@ class Code2WavStatePool(CodecStatePool):
         self.frame_positions.index_fill_(0, slots, 0)
 
 
+def _k_splits(k: int, n: int) -> int:
+    """The split-K slice count of a [rows, k] x [k, n] GEMM, from its shape alone (never the row
+    count, which the summation order must not depend on): the layers with few output columns per
+    input take more slices, so that their few column tiles spread over more workgroups."""
+    splits = 1 if n >= 4096 else (4 if k >= 3072 else (2 if n >= 3072 else 4))
+    while splits > 1 and k % (64 * splits):  # each slice whole pairs of 32-channel chunks
+        splits //= 2
+    return splits
+
+
+def _linear(weight: torch.Tensor, device: torch.device):
+    """A linear layer's weight [out, in] as a packed k = 1 conv (bf16, no bias), with the split-K
+    slice count of its shape (``k_splits``)."""
+    packed = pack_conv1d(weight.float()[..., None], None).to(device)
+    packed.k_splits = _k_splits(weight.shape[1], weight.shape[0])
+    return packed
+
+
+def _gemm(x: torch.Tensor, packed, out: torch.Tensor, workspace: torch.Tensor) -> None:
+    """out [rows, out] (bf16) = x [rows, in] (bf16) @ W^T on the k = 1 conv kernel."""
+    rows = x.shape[0]
+    gemm(x.view(1, rows, x.shape[1]), packed, out.view(1, rows, out.shape[1]),
+         k_splits=packed.k_splits, workspace=workspace)
+
+
 class Qwen3Code2WavDecoder(DacCodecDecoder):
-    """Qwen3-Omni code2wav, every op but the transformer's and ConvNeXt's plain GEMMs on gfx950
-    HIP kernels (the GEMMs are hipBLASLt through torch.mm, on the same stream). ``state`` is a
+    """Qwen3-Omni code2wav on gfx950 HIP kernels (the transformer's and ConvNeXt's GEMMs as k = 1
+    convs on the LDS-DMA conv kernel). ``state`` is a
     ``Qwen3OmniMoeCode2Wav.state_dict()``-named float32 dict (``configs.make_qwen3_code2wav_
     weights``); conv weights are bf16 (``weight_format`` "fp8" quantizes the decoder convs)."""
 
@@ -164,15 +196,15 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             qkv = torch.cat([state[f"{p}.self_attn.{n}_proj.weight"] for n in "qkv"], dim=0)
             gate_up = torch.cat([state[f"{p}.mlp.gate_proj.weight"],
                                  state[f"{p}.mlp.up_proj.weight"]], dim=0)
-            # GEMM operands as [in, out] row-major: x @ W with no transposed views
+            # GEMM weights [out, in] packed as k = 1 convs (bf16)
             self.layers.append({
                 "in_norm": f32(state[f"{p}.input_layernorm.weight"]),
-                "qkv": bf16(qkv.t()),
-                "o": bf16(state[f"{p}.self_attn.o_proj.weight"].t()),
+                "qkv": _linear(qkv, dev),
+                "o": _linear(state[f"{p}.self_attn.o_proj.weight"], dev),
                 "attn_scale": f32(state[f"{p}.self_attn_layer_scale.scale"]),
                 "post_norm": f32(state[f"{p}.post_attention_layernorm.weight"]),
-                "gate_up": bf16(gate_up.t()),
-                "down": bf16(state[f"{p}.mlp.down_proj.weight"].t()),
+                "gate_up": _linear(gate_up, dev),
+                "down": _linear(state[f"{p}.mlp.down_proj.weight"], dev),
                 "mlp_scale": f32(state[f"{p}.mlp_layer_scale.scale"]),
             })
         self.final_norm = f32(state["pre_transformer.norm.weight"])
@@ -193,9 +225,9 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                 "dw_bias": f32(state[f"{p}.dwconv.conv.bias"]),
                 "ln_weight": f32(state[f"{p}.norm.weight"]),
                 "ln_bias": f32(state[f"{p}.norm.bias"]),
-                "w1": bf16(state[f"{p}.pwconv1.weight"].t()),
+                "w1": _linear(state[f"{p}.pwconv1.weight"], dev),
                 "b1": f32(state[f"{p}.pwconv1.bias"]),
-                "w2": bf16(state[f"{p}.pwconv2.weight"].t()),
+                "w2": _linear(state[f"{p}.pwconv2.weight"], dev),
                 "b2": f32(state[f"{p}.pwconv2.bias"]),
                 "gamma": f32(state[f"{p}.gamma"]),
             })
@@ -255,6 +287,15 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             buf[f"p1_{i}"] = torch.empty(batch * length, 4 * u, dtype=bf, device=dev)
             buf[f"p2_{i}"] = torch.empty(batch * length, u, dtype=bf, device=dev)
             buf[f"z{i}"] = torch.empty(batch, length, u, dtype=bf, device=dev)
+        # the split-K GEMMs' float32 partials: the largest slices x rows x columns of any site
+        sites = [(m, layer[name]) for layer in self.layers for name in ("qkv", "o", "gate_up", "down")]
+        length = frames
+        for up in self.upsamplers:
+            length *= up["factor"]
+            sites += [(batch * length, up["w1"]), (batch * length, up["w2"])]
+        need = max((p.k_splits * rows * p.n_cols for rows, p in sites if p.k_splits > 1),
+                   default=0)
+        buf["splitk"] = torch.empty(max(need, 4), dtype=torch.float32, device=dev)
         ws.front.update(buf)
         return ws.front
 
@@ -310,7 +351,7 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                         "key_ring": pool.keys[i], "value_ring": pool.values[i],
                         "ring_frames": pool.ring_frames}
             with timer.launch("front_gemm", 2.0 * m * c * qkv.shape[1]):
-                torch.mm(normed, layer["qkv"], out=qkv)
+                _gemm(normed, layer["qkv"], qkv, buf["splitk"])
             with timer.launch("front_elementwise", 0.0):
                 F.rope_kv_write(qkv, batch, heads, kv_heads, hd, self.inv_freq, cold=cold, **ring)
             # a first decode attends to its own frames: the keys are in qkv already
@@ -319,16 +360,16 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                 F.window_attention(qkv, batch, heads, kv_heads, hd, cfg.sliding_window,
                                    hd ** -0.5, attn, cold=cold, **attend_ring)
             with timer.launch("front_gemm", 2.0 * m * self.q_width * c):
-                torch.mm(attn, layer["o"], out=proj)
+                _gemm(attn, layer["o"], proj, buf["splitk"])
             with timer.launch("front_elementwise", 0.0):
                 F.rms_norm_residual(h, layer["post_norm"], eps, normed, delta=proj,
                                     scale=layer["attn_scale"])
             with timer.launch("front_gemm", 2.0 * m * c * gate_up.shape[1]):
-                torch.mm(normed, layer["gate_up"], out=gate_up)
+                _gemm(normed, layer["gate_up"], gate_up, buf["splitk"])
             with timer.launch("front_elementwise", 0.0):
                 F.silu_mul(gate_up, act)
             with timer.launch("front_gemm", 2.0 * m * act.shape[1] * c):
-                torch.mm(act, layer["down"], out=proj)
+                _gemm(act, layer["down"], proj, buf["splitk"])
             nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
             with timer.launch("front_elementwise", 0.0):
                 F.rms_norm_residual(h, nxt, eps, normed, delta=proj, scale=layer["mlp_scale"])
@@ -359,11 +400,11 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             u = self.latent
             p1, p2 = buf[f"p1_{i}"], buf[f"p2_{i}"]
             with timer.launch("front_gemm", 2.0 * rows * u * 4 * u):
-                torch.mm(n.view(rows, u), up["w1"], out=p1)
+                _gemm(n.view(rows, u), up["w1"], p1, buf["splitk"])
             with timer.launch("front_elementwise", 0.0):
                 F.bias_gelu(p1, up["b1"])
             with timer.launch("front_gemm", 2.0 * rows * 4 * u * u):
-                torch.mm(p1, up["w2"], out=p2)
+                _gemm(p1, up["w2"], p2, buf["splitk"])
             z = buf[f"z{i}"]
             with timer.launch("front_elementwise", 0.0):
                 F.bias_scale_residual(r.view(rows, u), p2, up["b2"], up["gamma"],

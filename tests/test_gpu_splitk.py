@@ -1,0 +1,84 @@
+"""Split-K k = 1 convs (``omni_conv1d_splitk``), the GEMMs of the code2wav pre-transformer and
+ConvNeXt blocks (the reference's ``F.linear`` calls, sglang_omni/models/qwen3_omni/components/
+code2wav.py:266,311,318,322):
+
+* every tile of the LDS-DMA k = 1 list, forced, at 2 and 4 slices, against the float64 GEMM of
+  the same bf16 operands (float32 output: float32-summation tolerance);
+* a row gives the same bits whatever batch it runs in (the summation order depends on C_in and
+  the slice count only): rows decoded 3, 36 and 36 at a time equal the 75-row launch;
+* the split form refuses what it does not take, and a workspace that is too small.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from sglang_omni_amd import _native as N
+from sglang_omni_amd.kernels.conv import _conv_args, gemm, pack_conv1d, splitk_workspace_elements
+
+pytestmark = pytest.mark.gpu
+
+SPLIT_TILES = 4  # entries of the k = 1 LDS-DMA list
+
+
+def operands(rows, c_in, c_out, seed, gpu):
+    gen = torch.Generator().manual_seed(seed)
+    x = (torch.randn(1, rows, c_in, generator=gen)).to(torch.bfloat16)
+    w = (torch.randn(c_out, c_in, 1, generator=gen) / c_in ** 0.5).to(torch.bfloat16).float()
+    b = (torch.randn(c_out, generator=gen) * 0.1).to(torch.bfloat16).float()
+    return x.to(gpu), w, b
+
+
+@pytest.mark.parametrize("splits", [2, 4])
+@pytest.mark.parametrize("config", range(1, SPLIT_TILES + 1))
+def test_each_split_tile_matches_the_float64_gemm(gpu, config, splits):
+    rows, c_in, c_out = 300, 768, 384
+    x, w, b = operands(rows, c_in, c_out, 10 * config + splits, gpu)
+    packed = pack_conv1d(w, b).to(gpu)
+    ws = torch.empty(splitk_workspace_elements(x, packed, splits), device=gpu)
+    out = torch.empty(1, rows, c_out, device=gpu)
+    gemm(x, packed, out, k_splits=splits, workspace=ws, kernel=N.CONV_KERNEL_DMA, config=config)
+    ref = x.double().cpu()[0] @ w[:, :, 0].double().t() + b.double()
+    scale = ref.abs().max().item()
+    torch.testing.assert_close(out[0].cpu().double(), ref, rtol=1e-5, atol=1e-5 * scale)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_a_row_gives_the_same_bits_in_any_batch(gpu, splits):
+    x, w, b = operands(75, 1024, 1024, 3, gpu)
+    packed = pack_conv1d(w, b).to(gpu)
+    ws = torch.empty(splitk_workspace_elements(x, packed, splits), device=gpu)
+    whole = torch.empty(1, 75, 1024, dtype=torch.bfloat16, device=gpu)
+    gemm(x, packed, whole, k_splits=splits, workspace=ws)
+    parts = []
+    for a, c in ((0, 3), (3, 39), (39, 75)):
+        o = torch.empty(1, c - a, 1024, dtype=torch.bfloat16, device=gpu)
+        gemm(x[:, a:c].contiguous(), packed, o, k_splits=splits, workspace=ws)
+        parts.append(o)
+    assert torch.equal(torch.cat(parts, dim=1), whole)
+
+
+def test_split_form_refusals(gpu):
+    x, w, b = operands(40, 256, 128, 5, gpu)
+    packed = pack_conv1d(w, b).to(gpu)
+    out = torch.empty(1, 40, 128, dtype=torch.bfloat16, device=gpu)
+    need = splitk_workspace_elements(x, packed, 2)
+    with pytest.raises(ValueError):  # workspace too small
+        gemm(x, packed, out, k_splits=2, workspace=torch.empty(need - 1, device=gpu))
+    lib = N.load_library()
+    ws = torch.empty(need, device=gpu)
+    resid = torch.zeros(1, 40, 128, device=gpu)
+    args = _conv_args(x, packed, out, residual=resid)
+    status = lib.omni_conv1d_splitk(ctypes.byref(args), 2, ws.data_ptr(), ws.numel() * 4,
+                                    N.CONV_KERNEL_AUTO, 0, N.stream_handle(gpu))
+    assert status == N.UNSUPPORTED  # a residual is not part of the split form
+    args = _conv_args(x, packed, out)
+    status = lib.omni_conv1d_splitk(ctypes.byref(args), 3, ws.data_ptr(), ws.numel() * 4,
+                                    N.CONV_KERNEL_AUTO, 0, N.stream_handle(gpu))
+    assert status == N.UNSUPPORTED  # 256 input channels are not 3 slices of whole chunks
+    status = lib.omni_conv1d_splitk(ctypes.byref(args), 2, ws.data_ptr(), 16,
+                                    N.CONV_KERNEL_AUTO, 0, N.stream_handle(gpu))
+    assert status == N.INVALID_ARG  # workspace_bytes below the partials' size
