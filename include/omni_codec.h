@@ -248,6 +248,21 @@ int omni_conv1d_fused_with(const omni_conv_args* args, int kernel, int config,
  */
 int omni_conv1d_splitk(const omni_conv_args* args, int64_t k_splits, float* workspace,
                        int64_t workspace_bytes, int kernel, int config, omni_stream_t stream);
+
+/*
+ * omni_conv1d_splitk without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. The float32 partials go to a static device array of 64 MiB
+ * per GPU (OMNI_SPLITK_SCRATCH_BYTES; the current device's, whose address is looked up once per
+ * device), held until the process ends; the call allocates and frees nothing. Partials beyond
+ * the array (k_splits * batch * length * n_cols * 4 bytes) return OMNI_ERR_UNSUPPORTED before
+ * any launch. Every call on one GPU shares its array: calls that overlap on one GPU (other
+ * streams, other threads) race; the stream must belong to the current device. Same arithmetic,
+ * hence the same bits, as omni_conv1d_splitk.
+ */
+#define OMNI_SPLITK_SCRATCH_BYTES (64ll << 20)
+int omni_conv1d_splitk_noalloc(const omni_conv_args* args, int64_t k_splits, int kernel, int config,
+                               omni_stream_t stream);
 int omni_conv1d_plan(const omni_conv_args* args, int kernel, int config, int* kernel_out,
                      int* config_out, int* configs_in_list, int64_t* workgroups);
 

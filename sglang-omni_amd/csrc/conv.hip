@@ -1,7 +1,16 @@
 // C ABI of the fused convolution: argument validation and the choice of kernel configuration.
 // The kernel template and its tile configurations are in conv_kernel.h.
+#include <mutex>
+
 #include "conv_dma.h"
 #include "conv_kernel.h"
+
+// The split-K partials of omni_conv1d_splitk_noalloc: one array per GPU (each device holds its own
+// copy at its own address), kept until the process ends. In host code `scratch` names a host-side
+// stand-in, never the device memory: kernels and copies take the address scratch_address()
+// looked up with hipGetSymbolAddress.
+constexpr int64_t kScratchBytes = OMNI_SPLITK_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kScratchBytes / 4];
 
 namespace omni_conv {
 namespace {
@@ -322,6 +331,57 @@ extern "C" int omni_conv1d_splitk(const omni_conv_args* a, int64_t k_splits, flo
   if ((kernel == OMNI_CONV_KERNEL_AUTO) != (config == 0)) return OMNI_ERR_INVALID_ARG;
   return conv_entry(a, kernel, config, true, nullptr, nullptr, nullptr, nullptr, stream, k_splits,
                     workspace, workspace_bytes);
+}
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::once_flag scratch_once[kScratchDevices];
+float* scratch_device_ptr[kScratchDevices];
+int scratch_lookup_status[kScratchDevices];
+
+// This GPU's scratch array (the current device): its device address is looked up once per
+// device, with that device current, and kept.
+int scratch_address(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return OMNI_ERR_DEVICE;
+  }
+  if (dev < 0 || dev >= kScratchDevices) return OMNI_ERR_UNSUPPORTED;
+  std::call_once(scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      scratch_lookup_status[dev] = OMNI_ERR_DEVICE;
+      return;
+    }
+    scratch_device_ptr[dev] = static_cast<float*>(ptr);
+    scratch_lookup_status[dev] = OMNI_OK;
+  });
+  *out = scratch_device_ptr[dev];
+  return scratch_lookup_status[dev];
+}
+
+}  // namespace
+
+extern "C" int omni_conv1d_splitk_noalloc(const omni_conv_args* a, int64_t k_splits, int kernel,
+                                          int config, omni_stream_t stream) {
+  if (!a || k_splits < 1 || (kernel == OMNI_CONV_KERNEL_AUTO) != (config == 0))
+    return OMNI_ERR_INVALID_ARG;
+  if (k_splits > 64) return OMNI_ERR_UNSUPPORTED;
+  if (a->batch < 0 || a->length < 0 || a->n_cols < 1) return OMNI_ERR_INVALID_ARG;
+  // the partials must fit the array (each slice is written whole before the reduction reads it,
+  // so nothing in it has to start at zero)
+  if (k_splits > 1 && a->batch > 0 && a->length > 0 &&
+      (a->batch > kScratchBytes || a->length > kScratchBytes / a->batch ||
+       a->n_cols * k_splits > kScratchBytes / 4 / (a->batch * a->length)))
+    return OMNI_ERR_UNSUPPORTED;
+  float* ws = nullptr;
+  const int st = scratch_address(&ws);
+  if (st != OMNI_OK) return st;
+  return conv_entry(a, kernel, config, true, nullptr, nullptr, nullptr, nullptr, stream, k_splits,
+                    ws, kScratchBytes);
 }
 
 extern "C" int omni_conv1d_plan(const omni_conv_args* a, int kernel, int config, int* kernel_out,

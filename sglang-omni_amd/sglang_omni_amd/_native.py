@@ -180,6 +180,7 @@ SIGNATURES: dict[str, list] = {
     "omni_conv1d_fused": [ctypes.POINTER(ConvArgs), _PTR],
     "omni_conv1d_fused_with": [ctypes.POINTER(ConvArgs), _INT, _INT, _PTR],
     "omni_conv1d_splitk": [ctypes.POINTER(ConvArgs), _I64, _PTR, _I64, _INT, _INT, _PTR],
+    "omni_conv1d_splitk_noalloc": [ctypes.POINTER(ConvArgs), _I64, _INT, _INT, _PTR],
     "omni_conv1d_plan": [ctypes.POINTER(ConvArgs), _INT, _INT, ctypes.POINTER(_INT),
                          ctypes.POINTER(_INT), ctypes.POINTER(_INT), ctypes.POINTER(_I64)],
     "omni_residual_stack": [ctypes.POINTER(ResidualStackArgs), _PTR],
