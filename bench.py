@@ -287,7 +287,14 @@ def bench_other_configs(device) -> dict:
     """xRT of the other decoder configurations (one call each, inputs resident in HBM)."""
     from sglang_omni_amd.models import (DacCodecDecoder, HifiGanVocoder, make_dac_weights,
                                         make_hifigan_weights)
-    from sglang_omni_amd.models.configs import CODEC_24K, CODEC_24K_LONG, HIFIGAN_24K
+    from sglang_omni_amd.models.configs import (CODEC_24K, CODEC_24K_LONG, HIFIGAN_24K,
+                                                dac_macs_per_frame, hifigan_macs_per_frame)
+
+    def mfma(frames: int, macs_per_frame: int, dt: float) -> dict:
+        """The whole decoder's algorithmic FLOPs over its time, against the bf16 MFMA peak (the
+        fp8-weight form multiplies in bf16 too)."""
+        tflops = 2.0 * frames * macs_per_frame / dt / 1e12
+        return {"TFLOPs": round(tflops, 1), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
 
     out = {}
     gen = torch.Generator().manual_seed(0)
@@ -295,13 +302,15 @@ def bench_other_configs(device) -> dict:
     codes = torch.randint(0, 2048, (1, 16, 250), generator=gen).to(device)
     dt = timed_call(lambda: dec.from_indices(codes))
     out["single_utterance"] = {"workload": "24 kHz codec, 1 x 250 frames (20 s), bf16",
-                               "xRT": round(20.0 / dt, 1), "ms": round(dt * 1e3, 3)}
+                               "xRT": round(20.0 / dt, 1), "ms": round(dt * 1e3, 3),
+                               **mfma(250, dac_macs_per_frame(CODEC_24K), dt)}
     del dec
     voc = HifiGanVocoder(make_hifigan_weights(HIFIGAN_24K, seed=0), HIFIGAN_24K, device=device)
     mel = (torch.randn(16, 80, 500, generator=gen) * 2 - 5).to(device)
     dt = timed_call(lambda: voc(mel))
     out["hifigan"] = {"workload": "HiFiGAN mel->wave, 16 x 500 mel frames (160 s), bf16",
-                      "xRT": round(160.0 / dt, 1), "ms": round(dt * 1e3, 3)}
+                      "xRT": round(160.0 / dt, 1), "ms": round(dt * 1e3, 3),
+                      **mfma(16 * 500, hifigan_macs_per_frame(HIFIGAN_24K), dt)}
     del voc
     codes = torch.randint(0, 1024, (8, 32, 1500), generator=gen).to(device)
     long_weights = make_dac_weights(CODEC_24K_LONG, seed=0)
@@ -311,7 +320,8 @@ def bench_other_configs(device) -> dict:
         name = "fp8 e4m3" if fmt == "fp8" else "bf16"
         out[f"{fmt}_long_form"] = {"workload": f"24 kHz codec, {name} weights, 8 x 1500 frames "
                                                "(960 s), whole utterances",
-                                   "xRT": round(960.0 / dt, 1), "ms": round(dt * 1e3, 3)}
+                                   "xRT": round(960.0 / dt, 1), "ms": round(dt * 1e3, 3),
+                                   **mfma(8 * 1500, dac_macs_per_frame(CODEC_24K_LONG), dt)}
         del dec
     return out
 
