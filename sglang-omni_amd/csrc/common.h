@@ -47,6 +47,14 @@ OMNI_DEVICE u16 float_to_bits_f16(float x) {
   return *reinterpret_cast<u16*>(&h);
 }
 
+// A copy of v the compiler cannot see through. Addresses of rarely run code derived from it are
+// computed where they are used instead of being hoisted out of the hot loops and held in
+// registers for the whole kernel.
+OMNI_DEVICE int opaque_copy(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Snake v + b * sin(2 pi ar v)^2 with the frequency in revolutions, ar = alpha / (2 pi): the
 // hardware v_sin_f32 takes revolutions, and v_fract_f32 reduces the phase to [0, 1) (the
 // activations are bounded, so no Payne-Hanek style reduction is needed). The kernels stage

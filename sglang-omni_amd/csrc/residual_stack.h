@@ -201,7 +201,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wave_co = wave % WCO;
   const int wave_p = wave / WCO;
   const int lrow = lane & 15;
@@ -365,28 +365,30 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 
   // This lane's staged row t in the accumulator layout, its segment, stream row and position
   // (recomputed where needed rather than held in registers; in the sweep every row is of row b0)
-  auto row_of = [&](int t) __attribute__((always_inline)) -> int {
-    return wave_p * TP * 16 + t * 16 + lrow;
+  // (lr: the lane's row within its 16-row groups, lane % 16)
+  auto row_of = [&](int t, int lr) __attribute__((always_inline)) -> int {
+    return wave_p * TP * 16 + t * 16 + lr;
   };
-  auto seg_of = [&](int t) __attribute__((always_inline)) -> int {
-    return SWEEP ? 0 : row_of(t) / span;
+  auto seg_of = [&](int t, int lr) __attribute__((always_inline)) -> int {
+    return SWEEP ? 0 : row_of(t, lr) / span;
   };
-  auto pos_of = [&](int t) __attribute__((always_inline)) -> int {
-    const int r = row_of(t);
-    return r < rows ? i0 - H + (r - seg_of(t) * span) : -(1 << 30);
+  auto pos_of = [&](int t, int lr) __attribute__((always_inline)) -> int {
+    const int r = row_of(t, lr);
+    return r < rows ? i0 - H + (r - seg_of(t, lr) * span) : -(1 << 30);
   };
   if (tile > 0) __syncthreads();  // the previous tile's reads of the tile, guard and ring are done
   {
     const auto xr = buffer_rsrc(p.x, p.x_bytes);
+    const int ln = opaque_copy(lane);
 #pragma unroll
     for (int c = 0; c < TCO; ++c) {
-      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+      const int n = wco0 + c * 16 + (ln >> 4) * 4;
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
-        const int pos = pos_of(t);
+        const int pos = pos_of(t, ln & 15);
         const bool ok = pos >= 0 && pos < L;
         const uint32_t off =
-            ok ? (uint32_t)((b0 + seg_of(t)) * p.x_sb + pos * p.x_st + n) * 4 : kOutOfRange;
+            ok ? (uint32_t)((b0 + seg_of(t, ln & 15)) * p.x_sb + pos * p.x_st + n) * 4 : kOutOfRange;
         xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
       }
     }
@@ -404,7 +406,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       const int w0 = wave_p * TP * 16;
       const int lo = first > w0 ? first : w0;
       const int n = (w0 + TP * 16 - lo) * PIECES_PER_ROW;
-      for (int e = lane; e < n; e += 64) {
+      for (int e = opaque_copy(lane); e < n; e += 64) {
         const int r = lo + e / PIECES_PER_ROW;
         const int piece = e - (r - lo) * PIECES_PER_ROW;
         u32x4* st = reinterpret_cast<u32x4*>(halo + (p.halo_off[k] + r - first) * C + piece * 8);
@@ -448,7 +450,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     // (a) operand rows left of position 0 (segments that start a stream row): the history copy
     // of the row's slot, or zeros
     if (i0 == 0 && h > 0) {
-      for (int e = tid; e < nseg * h * PIECES_PER_ROW; e += NT) {
+      for (int e = opaque_copy(tid); e < nseg * h * PIECES_PER_ROW; e += NT) {
         const int s = e / (h * PIECES_PER_ROW);
         const int rem = e - s * h * PIECES_PER_ROW;
         const int j = rem / PIECES_PER_ROW;  // sample j of the history: position j - h
@@ -470,7 +472,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     // (b) the new history: the last h operand samples of each stream row, written by the
     // workgroup holding them (those left of 0 by the one holding position 0)
     if (hist != nullptr) {
-      for (int e = tid; e < nseg * h * PIECES_PER_ROW; e += NT) {
+      for (int e = opaque_copy(tid); e < nseg * h * PIECES_PER_ROW; e += NT) {
         const int s = e / (h * PIECES_PER_ROW);
         const int rem = e - s * h * PIECES_PER_ROW;
         const int j = rem / PIECES_PER_ROW;
@@ -493,37 +495,98 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 #pragma unroll
       for (int t = 0; t < TP; ++t) acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     {
+      // One weight stage of NTAPS taps, software-pipelined in a fixed issue order. The stage's
+      // weight tiles (tap-major, then column tile) pass through a ring of three registers: tile
+      // i + 3 is read as soon as tile i's TP MFMAs have issued, two column tiles ahead of its
+      // use; the next tap's TP operand tiles go to the second of two buffers while the current
+      // tap's MFMAs run. So only the stage's first reads wait on LDS latency, with no more
+      // operand registers than a tap's tiles (scheduling barriers keep the compiler from
+      // regrouping the reads). E4M3 weights stay as loaded bytes until their MFMAs. The MFMAs
+      // of each accumulator keep the order of the taps, so the sums are those of the plain loop.
+      auto conv_stage = [&](auto ntaps, const u16* wtap, const u16* ukc, int t0)
+          __attribute__((always_inline)) {
+        constexpr int NTAPS = decltype(ntaps)::value;
+        constexpr int NTILES = NTAPS * TCO;
+        // u16 elements per weight row of the stage
+        constexpr int P8 = (W_FP8 ? Tile::P_LO : NTAPS * 4 + 1) * 8;
+        using WRaw = typename std::conditional<W_FP8, u32x2, bf16x8>::type;
+        auto load_a = [&](int i) __attribute__((always_inline)) -> WRaw {
+          const int jj = i / TCO;
+          const int c = i - jj * TCO;
+          return *reinterpret_cast<const WRaw*>(wtap + jj * (kChunk * Tile::WE / 2) + c * 16 * P8);
+        };
+        auto widen = [&](const WRaw& w) __attribute__((always_inline)) -> bf16x8 {
+          if constexpr (W_FP8)
+            return __builtin_bit_cast(bf16x8, fp8x8_to_bf16x8(w));
+          else
+            return w;
+        };
+        auto load_b = [&](int jj, bf16x8 (&b)[TP]) __attribute__((always_inline)) {
+          const int rj = row0 + (t0 + jj) * d - h;
+          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+#pragma unroll
+          for (int t = 0; t < TP; ++t)
+            b[t] = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
+        };
+        WRaw ring[3];
+        bf16x8 bb[2][TP];
+        load_b(0, bb[0]);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) ring[i] = load_a(i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int jj = 0; jj < NTAPS; ++jj) {
+#pragma unroll
+          for (int c = 0; c < TCO; ++c) {
+            const int i = jj * TCO + c;
+            const bf16x8 av = widen(ring[i % 3]);
+#pragma unroll
+            for (int t = 0; t < TP; ++t)
+              acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bb[jj & 1][t], acc[c][t], 0, 0, 0);
+            if (i + 3 < NTILES) ring[i % 3] = load_a(i + 3);
+            if (c == 1 && jj + 1 < NTAPS) load_b(jj + 1, bb[(jj + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      };
       for (int r = 0; r < Tile::CONV_STAGES; ++r) {
         const int g = k * Tile::STAGES + r;
         if (r > 0) stage_begin(g);  // stage 0 began at the top of the unit
         const int kc = W_FP8 ? r : r >> 1;
-        const int t0 = (!W_FP8 && (r & 1)) ? 4 : 0;
-        const int nt = W_FP8 ? kTaps : ((r & 1) ? 3 : 4);
-        const int P8 = (W_FP8 ? Tile::P_LO : nt * 4 + 1) * 8;  // u16 elements per weight row
-        // the lane's 8 weights of tap t0 + jj: 16 bytes (bf16) or 8 (E4M3, widened when read)
-        const u16* wtap = ws + (g & 1) * Tile::RING_ELEMS + (wco0 + lrow) * P8 + (W_FP8 ? lk / 2 : lk);
         const u16* ukc = us + kc * UROWS * kChunk;
+        const u16* wbuf = ws + (g & 1) * Tile::RING_ELEMS;
+        if constexpr (W_FP8) {
+          // the lane's 8 weights of a tap: 8 bytes, widened when read
+          conv_stage(std::integral_constant<int, kTaps>{},
+                     wbuf + (wco0 + lrow) * Tile::P_LO * 8 + lk / 2, ukc, 0);
+        } else {
+          // bf16 weights (taps 0-3 or 4-6 of the chunk; the lane's 8 weights of a tap: 16
+          // bytes): one loop over the stage's taps, each reading its TP operand tiles and TCO
+          // weight tiles before its first MFMA, one LDS wait per tap (a pipelined, unrolled stage
+          // needs more registers than two waves per SIMD have beside the bf16 stages' addresses)
+          const int t0 = (r & 1) ? 4 : 0;
+          const int nt = (r & 1) ? 3 : 4;
+          const int P8 = (nt * 4 + 1) * 8;  // u16 elements per weight row
+          const u16* wtap = wbuf + (wco0 + lrow) * P8 + lk;
 #pragma unroll 1
-        for (int jj = 0; jj < nt; ++jj) {
-          bf16x8 a[TCO];
+          for (int jj = 0; jj < nt; ++jj) {
+            const int rj = row0 + (t0 + jj) * d - h;
+            const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+            bf16x8 bv[TP], a[TCO];
 #pragma unroll
-          for (int c = 0; c < TCO; ++c) {
-            if constexpr (W_FP8)
-              a[c] = __builtin_bit_cast(
-                  bf16x8, fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(wtap + c * 16 * P8)));
-            else
-              a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * P8);
-          }
-          const int rj = row0 + (t0 + jj) * d - h;
-          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+            for (int t = 0; t < TP; ++t)
+              bv[t] = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
 #pragma unroll
-          for (int t = 0; t < TP; ++t) {
-            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
+            for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * P8);
 #pragma unroll
             for (int c = 0; c < TCO; ++c)
-              acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
+#pragma unroll
+              for (int t = 0; t < TP; ++t)
+                acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv[t], acc[c][t], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, TP + TCO, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, TP * TCO, 0);
+            wtap += kChunk;  // one tap: 32 weights
           }
-          wtap += kChunk * Tile::WE / 2;  // one tap: 32 weights
         }
       }
     }
@@ -602,7 +665,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   // ---- the output operand rows of the tile's positions, 16 contiguous bytes per thread
   if (p.out != nullptr) {
     const auto orsrc = buffer_rsrc(p.out, p.o_bytes);
-    for (int e = tid; e < nseg * len * PIECES_PER_ROW; e += NT) {
+    for (int e = opaque_copy(tid); e < nseg * len * PIECES_PER_ROW; e += NT) {
       const int s = e / (len * PIECES_PER_ROW);
       const int rem = e - s * len * PIECES_PER_ROW;
       const int q = rem / PIECES_PER_ROW;
@@ -621,7 +684,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     // (a) context rows left of position 0 (segments that start a stream row): the history copy
     // of the row's slot, or zeros
     if (i0 == 0 && fh > 0) {
-      for (int e = tid; e < nseg * fh * PIECES_PER_ROW; e += NT) {
+      for (int e = opaque_copy(tid); e < nseg * fh * PIECES_PER_ROW; e += NT) {
         const int s = e / (fh * PIECES_PER_ROW);
         const int rem = e - s * fh * PIECES_PER_ROW;
         const int j = rem / PIECES_PER_ROW;  // sample j of the history: position j - fh
@@ -643,7 +706,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     // (b) its new history: the last fh operand samples of each stream row, written by the
     // workgroup holding them (those left of 0 by the one holding position 0)
     if (p.fin_hist != nullptr) {
-      for (int e = tid; e < nseg * fh * PIECES_PER_ROW; e += NT) {
+      for (int e = opaque_copy(tid); e < nseg * fh * PIECES_PER_ROW; e += NT) {
         const int s = e / (fh * PIECES_PER_ROW);
         const int rem = e - s * fh * PIECES_PER_ROW;
         const int j = rem / PIECES_PER_ROW;
@@ -666,17 +729,18 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     // operand tile read at the taps' row shifts exactly as the units' dilated conv reads it
     // (dilation 1). The weights go to LDS first (the ring is free now): [fin_taps][C] bf16.
     u16* wf = ws;
-    for (int e = tid; e < p.fin_taps * C; e += NT) wf[e] = float_to_bits_bf16(p.fin_w[e]);
+    for (int e = opaque_copy(tid); e < p.fin_taps * C; e += NT) wf[e] = float_to_bits_bf16(p.fin_w[e]);
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < TP; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int ln = opaque_copy(lane);
     for (int j = 0; j <= fh; ++j) {
-      const int rj = row0 + j - fh;
-      const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+      const int rj = GUARD + wave_p * TP * 16 + (ln & 15) + j - fh;
+      const int bj = rj * kChunk + (((ln >> 4) ^ ((rj >> 2) & 3)) << 3);
 #pragma unroll
       for (int kc = 0; kc < CH; ++kc) {
         bf16x8 a = bf16x8{};
-        if (lrow == 0) a = *reinterpret_cast<const bf16x8*>(wf + j * C + kc * kChunk + lk);
+        if ((ln & 15) == 0) a = *reinterpret_cast<const bf16x8*>(wf + j * C + kc * kChunk + (ln >> 4) * 8);
 #pragma unroll
         for (int t = 0; t < TP; ++t) {
           const bf16x8 bv =
@@ -687,27 +751,29 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     }
     // column 0 of each accumulator block: lanes 0..15, element 0, row lrow + 16 t
     const float bias = p.fin_b ? p.fin_b[0] : 0.f;
-    if (lane < 16) {
+    if (ln < 16) {
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
-        const int q = row_of(t) - seg_of(t) * span;
-        if (row_of(t) < rows && q >= H)
-          p.fin_out[(int64_t)(b0 + seg_of(t)) * p.fin_o_sb + pos_of(t)] =
+        const int q = row_of(t, ln) - seg_of(t, ln) * span;
+        if (row_of(t, ln) < rows && q >= H)
+          p.fin_out[(int64_t)(b0 + seg_of(t, ln)) * p.fin_o_sb + pos_of(t, ln)] =
               apply_act(p.fin_act, acc[0][t][0] + bias, 0.f, 0.f, 0.f);
       }
     }
   }
   if (p.x_out != nullptr) {
     const auto xo = buffer_rsrc(p.x_out, p.xo_bytes);
+    const int ln = opaque_copy(lane);
+    const int lr = ln & 15;
 #pragma unroll
     for (int c = 0; c < TCO; ++c) {
-      const int n = wco0 + c * 16 + (lane >> 4) * 4;
+      const int n = wco0 + c * 16 + (ln >> 4) * 4;
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
-        const int q = row_of(t) - seg_of(t) * span;
-        const bool ok = row_of(t) < rows && q >= H;
+        const int q = row_of(t, lr) - seg_of(t, lr) * span;
+        const bool ok = row_of(t, lr) < rows && q >= H;
         const uint32_t off =
-            ok ? (uint32_t)((b0 + seg_of(t)) * p.xo_sb + pos_of(t) * p.xo_st + n) * 4
+            ok ? (uint32_t)((b0 + seg_of(t, lr)) * p.xo_sb + pos_of(t, lr) * p.xo_st + n) * 4
                : kOutOfRange;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xv[c][t]), xo, off, 0, 0);
       }
