@@ -833,27 +833,6 @@ using ResidualUnit96Short = Config<1, 2, 6, 1, 32 + 4 * kMaxHalo, 7>;   // short
 using ResidualUnit192 = Config<4, 4, 3, 3, 192 + 3 * kMaxHalo, 7>;      // fused, 192 channels
 using ResidualUnit192Short = Config<2, 2, 6, 1, 32 + 4 * kMaxHalo, 7>;  // short rows
 
-// The fused residual-unit launch for one channel count: the full tile, or the short-row tile
-// when the full one's staged rows do not fit (entries 1 and 2 of a forced choice).
-template <bool W_FP8, typename Full, typename Short>
-int launch_fused_pair(const ConvParams& p, int in_mode, Choice& ch, hipStream_t stream) {
-  const bool fits[2] = {Full::fits(p, true), Short::fits(p, true)};
-  const int64_t wgs[2] = {Full::workgroups(p), Short::workgroups(p)};
-  int (*run[2])(ConvParams, hipStream_t);
-  if (in_mode == IN_RAW) {
-    run[0] = &Full::template launch<IN_RAW, W_FP8, true>;
-    run[1] = &Short::template launch<IN_RAW, W_FP8, true>;
-  } else if (in_mode == IN_ACT) {
-    run[0] = &Full::template launch<IN_ACT, W_FP8, true>;
-    run[1] = &Short::template launch<IN_ACT, W_FP8, true>;
-  } else {
-    run[0] = &Full::template launch<IN_F32, W_FP8, true>;
-    run[1] = &Short::template launch<IN_F32, W_FP8, true>;
-  }
-  const int pick = fits[0] ? 0 : (fits[1] ? 1 : -1);
-  return choose_and_launch(ch, 2, fits, wgs, run, pick, p, stream);
-}
-
 // Launchers, one translation unit each (they compile in parallel): taps <= 7 for each input and
 // weight dtype, taps <= 11 for bf16 weights, and the fused residual-unit forms.
 template <int IN, bool W_FP8>

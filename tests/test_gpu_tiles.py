@@ -34,7 +34,7 @@ pytestmark = pytest.mark.gpu
 DMA_LIST = {1: 4, 2: 4, 7: 4}
 STAGED_LIST = 10
 STAGED11_LIST = 10
-FUSED_LIST = 2
+FUSED_LIST = 3
 
 SHAPES = [(2, 300), (3, 100), (64, 12), (1, 700), (8, 40), (2, 20)]  # (rows, positions)
 
@@ -268,10 +268,17 @@ def test_staged11_tile_matches_float64_and_the_chosen_tile(gpu, config, mode):
 # ------------------------------------------------------------------------------ fused unit
 
 
-@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
-@pytest.mark.parametrize("mode", ["raw", "f32-snake"])
-@pytest.mark.parametrize("channels", [96, 192])
-@pytest.mark.parametrize("config", range(1, FUSED_LIST + 1), ids=["full", "short"])
+# (entry, channels, operand, fp8 weights): entry 1 is the LDS-DMA unit, which takes 192-channel
+# bf16 operands as they are with bf16 weights; entries 2 and 3 (the register-staged full and
+# short-row tiles) take every case
+FUSED_CASES = [(config, channels, mode, fp8) for config in range(1, FUSED_LIST + 1)
+               for channels in (96, 192) for mode in ("raw", "f32-snake") for fp8 in (False, True)
+               if config > 1 or (channels == 192 and mode == "raw" and not fp8)]
+
+
+@pytest.mark.parametrize("config,channels,mode,fp8", FUSED_CASES,
+                         ids=[f"{('dma', 'full', 'short')[c - 1]}-{n}-{m}-{'fp8' if f else 'bf16'}"
+                              for c, n, m, f in FUSED_CASES])
 def test_fused_unit_tile_matches_its_two_launch_form(gpu, config, channels, mode, fp8):
     """conv k7 (d = 9) -> Snake -> conv k1 -> + x in one launch equals, bit for bit, the same
     unit as two launches (h through HBM as bf16); the two-launch form's convs are then held to
