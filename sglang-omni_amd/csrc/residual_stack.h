@@ -356,6 +356,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   // taking each operand's halo from the previous tile (the halo store, copied into the guard)
   f32x4 xv[TCO][TP];
   f32x4 acc[TCO][TP];
+  bool x_ready = false;  // xv already holds this tile's x (loaded during the previous tile)
   for (int tile = 0;; ++tile) {
   const int H = (SWEEP && tile > 0) ? 0 : p.H;
   if constexpr (SWEEP) len = min(Tile::R - H, seg_end - i0);
@@ -377,7 +378,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     return r < rows ? i0 - H + (r - seg_of(t, lr) * span) : -(1 << 30);
   };
   if (tile > 0) __syncthreads();  // the previous tile's reads of the tile, guard and ring are done
-  {
+  if (!x_ready) {
     const auto xr = buffer_rsrc(p.x, p.x_bytes);
     const int ln = opaque_copy(lane);
 #pragma unroll
@@ -660,6 +661,31 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       }
     }
     halo_move(k + 1);
+  }
+  // In the sweep, the next tile's x (no halo rows ahead of it) is loaded now, while this tile's
+  // final conv and output stores run, instead of at the start of the next tile where the first
+  // operand waits for it; only when x_last is not stored, so the residual stream is free.
+  x_ready = false;
+  if constexpr (SWEEP) {
+    if (has_next && p.x_out == nullptr) {
+      const int ni0 = i0 + len;
+      const int nrows = min(Tile::R, seg_end - ni0);
+      const auto xr = buffer_rsrc(p.x, p.x_bytes);
+      const int ln = opaque_copy(lane);
+#pragma unroll
+      for (int c = 0; c < TCO; ++c) {
+        const int n = wco0 + c * 16 + (ln >> 4) * 4;
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+          const int r = wave_p * TP * 16 + t * 16 + (ln & 15);
+          const int pos = ni0 + r;
+          const bool ok = r < nrows && pos < L;
+          const uint32_t off = ok ? (uint32_t)(b0 * p.x_sb + pos * p.x_st + n) * 4 : kOutOfRange;
+          xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        }
+      }
+      x_ready = true;
+    }
   }
   __syncthreads();
   // ---- the output operand rows of the tile's positions, 16 contiguous bytes per thread
