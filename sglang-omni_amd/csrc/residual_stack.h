@@ -229,6 +229,17 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     len = p.length;
   }
   const int L = p.length;
+  // The final conv's weights ([fin_taps][C] float32, at most 8 * 96 = 768 <= 2 * NT), rounded to
+  // bf16 once per workgroup and held in registers, two per thread, for the LDS copy each tile
+  // makes of them (instead of a global load and a wait per tile).
+  static_assert(8 * C <= 2 * NT, "the final conv's weights are two per thread");
+  uint32_t fin_wb = 0;  // bf16 weights tid and tid + NT, packed low / high
+  if (p.fin_w != nullptr) {
+    const int nfw = p.fin_taps * C;
+    const u16 w0 = tid < nfw ? float_to_bits_bf16(p.fin_w[tid]) : (u16)0;
+    const u16 w1 = tid + NT < nfw ? float_to_bits_bf16(p.fin_w[tid + NT]) : (u16)0;
+    fin_wb = (uint32_t)w0 | ((uint32_t)w1 << 16);
+  }
   // ---- set-up, once per workgroup: coefficients, zero guard rows (and halo store) in LDS
   const int ncoef = (p.nunits * kCoefRows + 2) * C;
   if (p.coef_table != nullptr) {
@@ -755,7 +766,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     // operand tile read at the taps' row shifts exactly as the units' dilated conv reads it
     // (dilation 1). The weights go to LDS first (the ring is free now): [fin_taps][C] bf16.
     u16* wf = ws;
-    for (int e = opaque_copy(tid); e < p.fin_taps * C; e += NT) wf[e] = float_to_bits_bf16(p.fin_w[e]);
+    {
+      const int nfw = p.fin_taps * C;
+      if (tid < nfw) wf[tid] = (u16)(fin_wb & 0xffffu);
+      if (tid + NT < nfw) wf[tid + NT] = (u16)(fin_wb >> 16);
+    }
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < TP; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
