@@ -482,8 +482,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       __syncthreads();
     }
     // (b) the new history: the last h operand samples of each stream row, written by the
-    // workgroup holding them (those left of 0 by the one holding position 0)
-    if (hist != nullptr) {
+    // workgroup holding them (those left of 0 by the one holding position 0); a tile that holds
+    // neither a row's last h positions nor its start skips the loop (and its slot loads)
+    if (hist != nullptr && (i0 == 0 || i0 + len > L - h)) {
       for (int e = opaque_copy(tid); e < nseg * h * PIECES_PER_ROW; e += NT) {
         const int s = e / (h * PIECES_PER_ROW);
         const int rem = e - s * h * PIECES_PER_ROW;
@@ -741,8 +742,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     }
     __syncthreads();
     // (b) its new history: the last fh operand samples of each stream row, written by the
-    // workgroup holding them (those left of 0 by the one holding position 0)
-    if (p.fin_hist != nullptr) {
+    // workgroup holding them (those left of 0 by the one holding position 0); as the units', only
+    // in a tile that holds a row's last fh positions or its start
+    if (p.fin_hist != nullptr && (i0 == 0 || i0 + len > L - fh)) {
       for (int e = opaque_copy(tid); e < nseg * fh * PIECES_PER_ROW; e += NT) {
         const int s = e / (fh * PIECES_PER_ROW);
         const int rem = e - s * fh * PIECES_PER_ROW;
