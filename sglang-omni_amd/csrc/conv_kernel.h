@@ -217,7 +217,121 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
   // fit 32 bits (the byte extents are below 2 GiB).
   const bool packed = p.r_sb == (int64_t)L * p.r_st && p.o_sb == (int64_t)L * p.o_st;
   const uint32_t r_st = (uint32_t)p.r_st, o_st = (uint32_t)p.o_st;
-  for (int pass = 0; pass * EPI_WAVES < WAVES_P; ++pass) {
+  const bool live = walker && n_q < n_cols;
+  // element offsets of flat position m in the residual-shaped tensors and in out
+  auto offsets = [&](int m, uint32_t& re, uint32_t& oe) __attribute__((always_inline)) {
+    if (packed) {
+      re = (uint32_t)m * r_st + n_q;
+      oe = (uint32_t)m * o_st + n_q;
+    } else {
+      int b = (int)((float)m * inv_l);  // m / L, corrected below
+      int i = m - b * L;
+      if (i < 0) { --b; i += L; }
+      if (i >= L) { ++b; i -= L; }
+      re = (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q);
+      oe = (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q);
+    }
+  };
+  // Finish the NU rows r0 + u * RSTEP of a pass (positions from mp, prow rows; r0 < prow): read
+  // them from LDS, add the residual (`res`, loaded beforehand when `have_res`, else loaded here)
+  // and the mix, store sum_out, apply the activation and store out.
+  auto finish = [&](auto nu, int mp, int prow, int r0, bool have_res, auto& res)
+      __attribute__((always_inline)) {
+    constexpr int NU = decltype(nu)::value;
+    uint32_t roff[NU], ooff[NU];
+    f32x4 v[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int r = min(r0 + u * RSTEP, prow - 1);
+      uint32_t re, oe;
+      offsets(mp + r, re, oe);
+      const bool ok = live && r0 + u * RSTEP < prow;
+      roff[u] = ok ? re * 4 : kOutOfRange;
+      ooff[u] = ok ? oe : kOutOfRange;
+      v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
+    }
+    if (p.residual) {
+      if (!have_res) {
+        const auto rr = buffer_rsrc(p.residual, p.r_bytes);
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          res[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, roff[u], 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) v[u] += res[u];
+    }
+    if (p.mix_a) {
+      const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
+      const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const f32x4 ma = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, roff[u], 0, 0));
+        const f32x4 mb = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, roff[u], 0, 0));
+        v[u] = ((ma + mb) + v[u]) * p.mix_scale;
+      }
+    }
+    if (p.sum_out) {
+      const auto rs = buffer_rsrc(p.sum_out, p.r_bytes);
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rs, roff[u], 0, 0);
+    }
+    if (p.out != nullptr) {
+      const int act = p.act;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        f32x4 y = v[u];
+        if (act == OMNI_ACT_SNAKE) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = snake_rev(y[e], act_a[e], act_b[e]);
+        } else if (act == OMNI_ACT_LEAKY_RELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;
+        } else if (act != OMNI_ACT_NONE) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = apply_act(act, y[e], 0.f, 0.f, p.slope);
+        }
+        const auto ro = buffer_rsrc(p.out, p.o_bytes);
+        if (p.out_bf16) {
+          const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 2;
+          __builtin_amdgcn_raw_buffer_store_b64(
+              u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, oo, 0, 0);
+        } else {
+          const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 4;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, oo, 0, 0);
+        }
+      }
+    }
+  };
+  // When a walker's rows of a pass fit in registers (UR of them), the pass's residual rows are
+  // loaded before its LDS exchange (the first pass's before the first barrier, a later pass's
+  // right after the previous pass's stores were issued): their HBM latency then overlaps the
+  // exchange instead of costing a round trip per group of rows after it.
+  constexpr int NPASS = (WAVES_P + EPI_WAVES - 1) / EPI_WAVES;
+  constexpr int UR = (Tile::EPI_ROWS + RSTEP - 1) / RSTEP;  // rows per walker and pass
+  constexpr bool PREFETCH = UR <= 10 && NT <= 512;
+  f32x4 pre[PREFETCH ? UR : 1];
+  auto prefetch = [&](int pass) __attribute__((always_inline)) {
+    if constexpr (PREFETCH) {
+      if (p.residual) {
+        const auto rr = buffer_rsrc(p.residual, p.r_bytes);
+        const int mp = m0 + pass * Tile::EPI_ROWS;
+        const int prow = min(Tile::EPI_ROWS, m_end - mp);
+#pragma unroll
+        for (int u = 0; u < UR; ++u) {
+          const int r = r_first + u * RSTEP;
+          uint32_t re, oe;
+          offsets(mp + min(r, prow - 1), re, oe);
+          const uint32_t off = live && r < prow ? re * 4 : kOutOfRange;
+          pre[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0));
+        }
+      }
+    }
+  };
+  prefetch(0);
+#pragma unroll
+  for (int pass = 0; pass < NPASS; ++pass) {
+    if (pass > 0) prefetch(pass);
     __syncthreads();
     const int wl = wave_p - pass * EPI_WAVES;  // this wave's slot in the pass
     if (wl >= 0 && wl < EPI_WAVES) {
@@ -236,82 +350,13 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
     __syncthreads();
     const int mp = m0 + pass * Tile::EPI_ROWS;  // first position of the pass
     const int prow = min(Tile::EPI_ROWS, m_end - mp);
-    const bool live = walker && n_q < n_cols;
-    constexpr int U = 4;  // rows in flight per thread
-    for (int r0 = r_first; r0 < prow; r0 += U * RSTEP) {
-      uint32_t roff[U], ooff[U];
-      f32x4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int r = min(r0 + u * RSTEP, prow - 1);
-        const int m = mp + r;
-        uint32_t re, oe;
-        if (packed) {
-          re = (uint32_t)m * r_st + n_q;
-          oe = (uint32_t)m * o_st + n_q;
-        } else {
-          int b = (int)((float)m * inv_l);  // m / L, corrected below
-          int i = m - b * L;
-          if (i < 0) { --b; i += L; }
-          if (i >= L) { ++b; i -= L; }
-          re = (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q);
-          oe = (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q);
-        }
-        const bool ok = live && r0 + u * RSTEP < prow;
-        roff[u] = ok ? re * 4 : kOutOfRange;
-        ooff[u] = ok ? oe : kOutOfRange;
-        v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
-      }
-      if (p.residual) {
-        const auto rr = buffer_rsrc(p.residual, p.r_bytes);
+    if constexpr (PREFETCH) {
+      if (r_first < prow) finish(std::integral_constant<int, UR>{}, mp, prow, r_first, true, pre);
+    } else {
+      constexpr int U = 4;  // rows in flight per thread
+      for (int r0 = r_first; r0 < prow; r0 += U * RSTEP) {
         f32x4 res[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          res[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, roff[u], 0, 0));
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] += res[u];
-      }
-      if (p.mix_a) {
-        const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
-        const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const f32x4 ma = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, roff[u], 0, 0));
-          const f32x4 mb = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, roff[u], 0, 0));
-          v[u] = ((ma + mb) + v[u]) * p.mix_scale;
-        }
-      }
-      if (p.sum_out) {
-        const auto rs = buffer_rsrc(p.sum_out, p.r_bytes);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rs, roff[u], 0, 0);
-      }
-      if (p.out != nullptr) {
-        const int act = p.act;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          f32x4 y = v[u];
-          if (act == OMNI_ACT_SNAKE) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = snake_rev(y[e], act_a[e], act_b[e]);
-          } else if (act == OMNI_ACT_LEAKY_RELU) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;
-          } else if (act != OMNI_ACT_NONE) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = apply_act(act, y[e], 0.f, 0.f, p.slope);
-          }
-          const auto ro = buffer_rsrc(p.out, p.o_bytes);
-          if (p.out_bf16) {
-            const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 2;
-            __builtin_amdgcn_raw_buffer_store_b64(
-                u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, oo, 0, 0);
-          } else {
-            const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 4;
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, oo, 0, 0);
-          }
-        }
+        finish(std::integral_constant<int, U>{}, mp, prow, r0, false, res);
       }
     }
   }
