@@ -10,7 +10,9 @@
 // rows left of position 0, the new history written from LDS, causal zero rows) this kernel
 // repeats. One column tile holds all 192 channels, since the k1 conv needs every channel of h: a
 // chunk's weights for 192 columns and 7 taps (89 KB) would not double-buffer, so a ring stage
-// holds one chunk's input rows and taps 0-3 or 4-6 of its weights (72 KB), two stages per chunk.
+// holds taps 0-3 or 4-6 of a chunk's weights, two stages per chunk, and each ring buffer also
+// holds the input rows of every other chunk (chunk kc in buffer kc % 2, staged once for both of
+// its stages).
 // After the last stage the W2 weights (DMA'd into the free ring buffer during it) and h =
 // Snake(acc * scale + bias) (into the other) feed the k1 conv, whose accumulators go through
 // conv_epilogue (residual, float32 residual stream, the next operand's activation).
@@ -198,13 +200,14 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
   const auto w2_rsrc = buffer_rsrc(p.weight2, p.w2_bytes);
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-  // Stage s: chunk s / 2, taps 0-3 (s even) or 4-6 (s odd), into ring buffer s % 2: the chunk's
-  // input rows, then the taps' weights.
+  // Stage s: chunk kc = s / 2, taps 0-3 (s even) or 4-6 (s odd): the taps' weights into ring
+  // buffer s % 2 and, for the chunk's first stage, its input rows into buffer kc % 2 (where both
+  // of the chunk's stages read them: the other chunk's rows there were last read two stages back).
   auto issue = [&](int s) __attribute__((always_inline)) {
     const int kc = s >> 1;
     const int g = s & 1;
-    u16* xs = buf_of(s & 1);
-    u16* ws = xs + Tile::XCHUNK;
+    u16* xs = buf_of(kc & 1);
+    u16* ws = buf_of(s & 1) + Tile::XCHUNK;
     const uint32_t wbase = (uint32_t)((kc * p.n_cols * 7 + g * 4) * kChunk * 2);
     if (g == 0) {
 #pragma unroll
@@ -223,6 +226,7 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
                                                    (int)woff3[u], (int)wbase, 0, 0);
       }
     }
+    if (g != 0) return;
     const uint32_t xbase = (uint32_t)(kc * kChunk * 2);
 #pragma unroll
     for (int u = 0; u < Tile::X_PIECES; ++u) {
@@ -291,17 +295,18 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
     __syncthreads();
     if (s + 1 < STAGES) issue(s + 1);
     else issue_w2((s + 1) & 1);
-    if (p.hist != nullptr && (s & 1) == 0) write_history(s >> 1, s & 1);
+    if (p.hist != nullptr && (s & 1) == 0) write_history(s >> 1, (s >> 1) & 1);
     const int g = s & 1;
     const int t0 = g * 4;
-    const u16* xs = buf_of(s & 1);
+    const u16* xs = buf_of((s >> 1) & 1);         // the chunk's input rows
+    const u16* wsb = buf_of(s & 1) + Tile::XCHUNK;  // the stage's weights
     // the stage's taps, software-pipelined: tap i + 1's operands are read from LDS before tap
     // i's MFMAs
     auto stage_taps = [&](auto ntc) __attribute__((always_inline)) {
       constexpr int NTAPS = decltype(ntc)::value;
       constexpr int P8 = (NTAPS == 4 ? Tile::P4 : Tile::P3) * 8;  // u16 elements per weight row
       auto load_tap = [&](int i, bf16x8 (&a)[TCO], bf16x8 (&bv)[TP]) __attribute__((always_inline)) {
-        const u16* wtap = xs + Tile::XCHUNK + (wco0 + lrow) * P8 + lk + i * kChunk;
+        const u16* wtap = wsb + (wco0 + lrow) * P8 + lk + i * kChunk;
 #pragma unroll
         for (int cc = 0; cc < TCO; ++cc)
           a[cc] = *reinterpret_cast<const bf16x8*>(wtap + cc * 16 * P8);
