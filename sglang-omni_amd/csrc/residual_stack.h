@@ -229,16 +229,22 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     len = p.length;
   }
   const int L = p.length;
-  // The final conv's weights ([fin_taps][C] float32, at most 8 * 96 = 768 <= 2 * NT), rounded to
-  // bf16 once per workgroup and held in registers, two per thread, for the LDS copy each tile
-  // makes of them (instead of a global load and a wait per tile).
-  static_assert(8 * C <= 2 * NT, "the final conv's weights are two per thread");
-  uint32_t fin_wb = 0;  // bf16 weights tid and tid + NT, packed low / high
-  if (p.fin_w != nullptr) {
-    const int nfw = p.fin_taps * C;
-    const u16 w0 = tid < nfw ? float_to_bits_bf16(p.fin_w[tid]) : (u16)0;
-    const u16 w1 = tid + NT < nfw ? float_to_bits_bf16(p.fin_w[tid + NT]) : (u16)0;
-    fin_wb = (uint32_t)w0 | ((uint32_t)w1 << 16);
+  // The final conv's weights ([fin_taps][C] float32, at most 8 taps), rounded to bf16 once per
+  // workgroup and held in registers as this lane's A operand of its taps-as-columns MFMA: tap
+  // lane % 16 (zeros past the taps), channels 8 (lane / 16) .. + 7 of each 32-channel chunk.
+  static_assert(kTaps + 1 <= 16, "a tap per A-operand row");
+  bf16x8 fin_a[CH];
+#pragma unroll
+  for (int kc = 0; kc < CH; ++kc) fin_a[kc] = bf16x8{};
+  if (p.fin_w != nullptr && (lane & 15) < p.fin_taps) {
+    const float* wrow = p.fin_w + (lane & 15) * C + (lane >> 4) * 8;
+#pragma unroll
+    for (int kc = 0; kc < CH; ++kc) {
+      const float* wk = wrow + kc * kChunk;
+      fin_a[kc] = __builtin_bit_cast(
+          bf16x8, u32x4{pack_bf16x2(wk[0], wk[1]), pack_bf16x2(wk[2], wk[3]),
+                        pack_bf16x2(wk[4], wk[5]), pack_bf16x2(wk[6], wk[7])});
+    }
   }
   // ---- set-up, once per workgroup: coefficients, zero guard rows (and halo store) in LDS
   const int ncoef = (p.nunits * kCoefRows + 2) * C;
@@ -763,44 +769,57 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         }
       }
     }
-    // (c) the conv on the matrix cores, as a conv with one real column: column 0 of the A
-    // operand holds the weights (rounded to bf16), columns 1..15 zeros, and the B operand is the
-    // operand tile read at the taps' row shifts exactly as the units' dilated conv reads it
-    // (dilation 1). The weights go to LDS first (the ring is free now): [fin_taps][C] bf16.
-    u16* wf = ws;
-    {
-      const int nfw = p.fin_taps * C;
-      if (tid < nfw) wf[tid] = (u16)(fin_wb & 0xffffu);
-      if (tid + NT < nfw) wf[tid + NT] = (u16)(fin_wb >> 16);
-    }
-    __syncthreads();
+    // (c) the conv on the matrix cores with the taps as the columns: column j of the A operand
+    // holds tap j's weights (fin_a), the B operand is the operand tile at the rows' own
+    // positions, so one MFMA per 32-channel chunk and 16 rows gives D[j][row] = sum_c w[j][c]
+    // u[row][c] for every tap; then out[row] = sum_j D[j][row - fh + j] (taps ascending) + bias,
+    // from D through LDS ([16 + R][8] floats in the ring, which is free now). Wave 0 also
+    // computes the 16 rows ahead of row 0 (the guard, where the sweep keeps the previous tile's
+    // last operand rows).
+    float* dl = reinterpret_cast<float*>(ws);
+    static_assert((16 + Tile::R) * 8 * 4 <= Tile::W_ELEMS * 2, "D fits the ring");
+    const int ln = opaque_copy(lane);
+    f32x4 dg = f32x4{0.f, 0.f, 0.f, 0.f};  // wave 0: the guard rows -16 .. -1
 #pragma unroll
     for (int t = 0; t < TP; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int ln = opaque_copy(lane);
-    for (int j = 0; j <= fh; ++j) {
-      const int rj = GUARD + wave_p * TP * 16 + (ln & 15) + j - fh;
-      const int bj = rj * kChunk + (((ln >> 4) ^ ((rj >> 2) & 3)) << 3);
+    {
+      const int rt = GUARD + wave_p * TP * 16 + (ln & 15);
+      const int bt = rt * kChunk + (((ln >> 4) ^ ((rt >> 2) & 3)) << 3);
+      const int rg = GUARD - 16 + (ln & 15);
+      const int bg = rg * kChunk + (((ln >> 4) ^ ((rg >> 2) & 3)) << 3);
 #pragma unroll
       for (int kc = 0; kc < CH; ++kc) {
-        bf16x8 a = bf16x8{};
-        if ((ln & 15) == 0) a = *reinterpret_cast<const bf16x8*>(wf + j * C + kc * kChunk + (ln >> 4) * 8);
+        const bf16x8 a = fin_a[kc];
+        const u16* ukc = us + kc * UROWS * kChunk;
 #pragma unroll
         for (int t = 0; t < TP; ++t) {
-          const bf16x8 bv =
-              *reinterpret_cast<const bf16x8*>(us + kc * UROWS * kChunk + bj + t * 16 * kChunk);
+          const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bt + t * 16 * kChunk);
           acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[0][t], 0, 0, 0);
+        }
+        if (wave_p == 0) {
+          const bf16x8 bv = *reinterpret_cast<const bf16x8*>(ukc + bg);
+          dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, dg, 0, 0, 0);
         }
       }
     }
-    // column 0 of each accumulator block: lanes 0..15, element 0, row lrow + 16 t
-    const float bias = p.fin_b ? p.fin_b[0] : 0.f;
-    if (ln < 16) {
+    // lane l holds D[4 (l / 16) + e][row l % 16 of the block]: taps 0..7 in lanes 0..31
+    if ((ln >> 4) < 2) {
 #pragma unroll
-      for (int t = 0; t < TP; ++t) {
-        const int q = row_of(t, ln) - seg_of(t, ln) * span;
-        if (row_of(t, ln) < rows && q >= H)
-          p.fin_out[(int64_t)(b0 + seg_of(t, ln)) * p.fin_o_sb + pos_of(t, ln)] =
-              apply_act(p.fin_act, acc[0][t][0] + bias, 0.f, 0.f, 0.f);
+      for (int t = 0; t < TP; ++t)
+        *reinterpret_cast<f32x4*>(dl + (16 + row_of(t, ln & 15)) * 8 + (ln >> 4) * 4) = acc[0][t];
+      if (wave_p == 0) *reinterpret_cast<f32x4*>(dl + (ln & 15) * 8 + (ln >> 4) * 4) = dg;
+    }
+    __syncthreads();
+    const float bias = p.fin_b ? p.fin_b[0] : 0.f;
+    for (int r = opaque_copy(tid); r < rows; r += NT) {
+      const int sg = SWEEP ? 0 : r / span;
+      const int q = r - sg * span;
+      if (q >= H) {
+        const float* dr = dl + (16 + r - fh) * 8;
+        float v = dr[0];
+        for (int j = 1; j <= fh; ++j) v += dr[j * 8 + j];
+        p.fin_out[(int64_t)(b0 + sg) * p.fin_o_sb + (i0 - H + q)] =
+            apply_act(p.fin_act, v + bias, 0.f, 0.f, 0.f);
       }
     }
   }
