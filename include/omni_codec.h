@@ -100,7 +100,7 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 7: omni_conv1d_splitk */
+int omni_codec_abi_version(void); /* 8: omni_conv1d_splitk takes k = 7, history and activations */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -235,16 +235,20 @@ int omni_conv1d_fused_with(const omni_conv_args* args, int kernel, int config,
 /*
  * Split-K form of a k = 1 conv used as a GEMM (replaces the plain GEMMs of the code2wav
  * pre-transformer, `F.linear` in sglang_omni/models/qwen3_omni/components/code2wav.py:266,311,
- * 318,322, and of the ConvNeXt blocks' pointwise convs, incremental_codec.py:174-175): the
- * LDS-DMA kernel runs k_splits slices of the 32-channel chunks of each tile, each writing its
- * float32 partial tile [positions][n_cols] into `workspace` (k_splits * batch * length * n_cols
- * floats, 16-byte aligned), then a reduction sums the slices in slice order and applies the bias
- * and the bf16 / float32 store. The summation order depends on (c_in, k_splits) only, never on
- * the row count, so a caller that fixes k_splits per layer gets the same bits for a row whatever
- * batch it runs in. Takes: taps = 1, a bf16 operand without in_activation, bf16 weights, no
- * weight2, history, residual, mix, sum_out or activation; c_in a multiple of 32 * k_splits.
- * k_splits = 1 is omni_conv1d_fused. kernel / config as in omni_conv1d_fused_with
- * (OMNI_CONV_KERNEL_AUTO / 0, or OMNI_CONV_KERNEL_DMA and an entry of its list).
+ * 318,322, and of the ConvNeXt blocks' pointwise convs, incremental_codec.py:174-175), or of a
+ * k = 7 conv with few output positions (a decoder's input conv over a streaming step, the
+ * `CausalConvNet` of modded_dac.py:566-572): the LDS-DMA kernel runs k_splits slices of the
+ * 32-channel chunks of each tile (the k = 7 form staging its history rows per slice and writing
+ * the new history of its own chunks), each writing its float32 partial tile [positions][n_cols]
+ * into `workspace` (k_splits * batch * length * n_cols floats, 16-byte aligned), then a
+ * reduction sums the slices in slice order and applies the bias, the output activation and the
+ * bf16 / float32 store. The summation order depends on (c_in, taps, k_splits) only, never on the
+ * row count, so a caller that fixes k_splits per layer gets the same bits for a row whatever
+ * batch it runs in. Takes: taps = 1 or 7, a bf16 operand without in_activation, bf16 weights,
+ * history (k = 7), activation NONE, SNAKE or LEAKY_RELU; no weight2, residual, mix or sum_out;
+ * c_in a multiple of 32 * k_splits. k_splits = 1 is omni_conv1d_fused. kernel / config as in
+ * omni_conv1d_fused_with (OMNI_CONV_KERNEL_AUTO / 0, or OMNI_CONV_KERNEL_DMA and an entry of its
+ * list).
  */
 int omni_conv1d_splitk(const omni_conv_args* args, int64_t k_splits, float* workspace,
                        int64_t workspace_bytes, int kernel, int config, omni_stream_t stream);

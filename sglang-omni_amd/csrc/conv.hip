@@ -220,13 +220,14 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
   return OMNI_OK;
 }
 
-// The split-K reduction: out[m][n] = (sum over slices s = 0, 1, .. of partial[s][m][n], in slice
-// order) * scale[n] + bias[n % c_out], stored as the conv epilogue stores it (bf16 rounded to
-// nearest even, or float32). One thread per 4 columns of one position.
+// The split-K reduction: out[m][n] = act((sum over slices s = 0, 1, .. of partial[s][m][n], in
+// slice order) * scale[n] + bias[n % c_out]), the activation (none, Snake with per-channel
+// act_a / act_b, LeakyReLU) and the store (bf16 rounded to nearest even, or float32) as the conv
+// epilogue applies them. One thread per 4 columns of one position.
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(
     const float* partial, int splits, int64_t slice, int n_cols, int c_out, int length,
-    int quads, const float* scale, const float* bias, void* out, int out_bf16, int64_t o_sb,
-    int64_t o_st) {
+    int quads, const float* scale, const float* bias, int act, const float* act_a,
+    const float* act_b, float slope, void* out, int out_bf16, int64_t o_sb, int64_t o_st) {
   const int e = blockIdx.x * 256 + threadIdx.x;  // a slice holds below 2^31 bytes
   if (e >= quads) return;
   const int nq = n_cols / 4;
@@ -242,6 +243,14 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(
     bi = f32x4{bias[co], bias[co + 1], bias[co + 2], bias[co + 3]};
   }
   v = v * sc + bi;
+  if (act == OMNI_ACT_SNAKE) {
+    const int co = n % c_out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = snake_rev(v[e], act_a[co + e] * kInvTwoPi, act_b[co + e]);
+  } else if (act == OMNI_ACT_LEAKY_RELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] >= 0.f ? v[e] : v[e] * slope;
+  }
   const int b = m / length;
   const int64_t off = b * o_sb + (int64_t)(m - b * length) * o_st + n;
   if (out_bf16) {
@@ -274,11 +283,13 @@ int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int
   }
   const int64_t positions = a->batch * a->length;
   if (k_splits > 1) {
-    // the GEMM form: a k = 1 conv of a bf16 operand with bf16 weights, bias only, no history,
-    // residual, mix, float32 sum or activation; whole chunks per slice
-    if (a->taps != 1 || fp8 || fuse2 || x_f32 || a->in_activation != OMNI_ACTIVATION_NONE ||
-        a->hist_pool || a->residual || a->mix_a || a->sum_out || !a->out ||
-        a->activation != OMNI_ACTIVATION_NONE)
+    // a k = 1 or k = 7 conv of a bf16 operand (its history rows staged per slice) with bf16
+    // weights; bias and an output activation (none, Snake, LeakyReLU) in the reduction; no
+    // residual, mix or float32 sum; whole chunks per slice
+    if ((a->taps != 1 && a->taps != 7) || fp8 || fuse2 || x_f32 ||
+        a->in_activation != OMNI_ACTIVATION_NONE || a->residual || a->mix_a || a->sum_out ||
+        !a->out || (p.act != OMNI_ACT_NONE && p.act != OMNI_ACT_SNAKE &&
+                    p.act != OMNI_ACT_LEAKY_RELU))
       return OMNI_ERR_UNSUPPORTED;
     if (a->c_in % (32 * k_splits) || k_splits > 64) return OMNI_ERR_UNSUPPORTED;
     if (kernel != OMNI_CONV_KERNEL_AUTO && kernel != OMNI_CONV_KERNEL_DMA)
@@ -300,7 +311,8 @@ int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), p.partial, p.k_splits,
                        positions * a->n_cols, p.n_cols, p.c_out, p.length, quads, p.wscale,
-                       p.bias, p.out, p.out_bf16, p.o_sb, p.o_st);
+                       p.bias, p.act, p.act_a, p.act_b, p.slope, p.out, p.out_bf16, p.o_sb,
+                       p.o_st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) r = OMNI_ERR_LAUNCH;
   }

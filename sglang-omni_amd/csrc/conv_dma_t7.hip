@@ -14,6 +14,9 @@ int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stre
                             DmaConfig<1, 8, 6, 3, 496, 7, 1, true>,
                             DmaConfig<2, 4, 3, 3, 368, 7, 1, true>,
                             DmaConfig<1, 4, 6, 3, 368, 7, 1, true>>(p, ch, stream);
+  if (p.k_splits > 1)  // split-K (bf16 weights): K slices of the 96 x 192 tiles (8 / 4 waves)
+    return launch_first_fit<DmaConfig<2, 4, 3, 3, 368, 7, 1, false, true>,
+                            DmaConfig<1, 4, 6, 3, 368, 7, 1, false, true>>(p, ch, stream);
   return launch_first_fit<DmaConfig<2, 8, 3, 3, 496, 7, 1>,
                             DmaConfig<1, 8, 6, 3, 496, 7, 1>,
                             DmaConfig<2, 4, 3, 3, 368, 7, 1>,

@@ -308,29 +308,39 @@ def splitk_workspace_elements(x: torch.Tensor, conv: PackedConv, k_splits: int) 
     return k_splits * x.shape[0] * x.shape[1] * conv.n_cols
 
 
-def gemm(x: torch.Tensor, conv: PackedConv, out: torch.Tensor, *, k_splits: int = 1,
-         workspace: torch.Tensor | None = None, kernel: int = N.CONV_KERNEL_AUTO,
-         config: int = 0) -> torch.Tensor:
-    """out [B, L, n_cols] = x [B, L, C_in] (bf16) times a packed k = 1 conv (bias included), as
-    ``omni_conv1d_splitk``: ``k_splits`` slices of the input channels, their float32 partials
-    in ``workspace`` (at least ``splitk_workspace_elements`` float32 elements on x's GPU),
-    summed in slice order. The summation order depends on C_in and k_splits only, so a row gives
-    the same bits whatever batch it runs in."""
-    if k_splits == 1:
-        return fused_conv(x, conv, out, kernel=kernel, config=config)
-    if conv.taps != 1:
-        raise ValueError("the split-K form takes k = 1 convs")
+def splitk_conv(x: torch.Tensor, conv: PackedConv, out: torch.Tensor, *, k_splits: int,
+                workspace: torch.Tensor, kernel: int = N.CONV_KERNEL_AUTO, config: int = 0,
+                **kw) -> torch.Tensor:
+    """``omni_conv1d_splitk``: the conv (k = 1, or k = 7 with its slot history) in ``k_splits``
+    slices of the input channels, their float32 partials in ``workspace`` (at least
+    ``splitk_workspace_elements`` contiguous float32 elements on x's GPU), summed in slice order,
+    then the bias, the output activation (``activation`` / ``act_a`` / ``act_b`` as for
+    ``fused_conv``) and the store. The summation order depends on the layer and k_splits only,
+    so a row gives the same bits whatever batch or chunk of its stream it runs in."""
     need = splitk_workspace_elements(x, conv, k_splits)
     if (workspace is None or workspace.dtype != torch.float32 or not workspace.is_contiguous()
             or workspace.numel() < need or workspace.device != x.device):
         raise ValueError(f"split-K over {k_splits} slices needs a contiguous float32 workspace of "
                          f"{need} elements on {x.device}")
-    args = _conv_args(x, conv, out)
+    args = _conv_args(x, conv, out, **kw)
     lib = N.load_library()
     N.check(lib.omni_conv1d_splitk(ctypes.byref(args), k_splits, workspace.data_ptr(),
                                    workspace.numel() * 4, kernel, config,
                                    N.stream_handle(x.device)), "omni_conv1d_splitk")
     return out
+
+
+def gemm(x: torch.Tensor, conv: PackedConv, out: torch.Tensor, *, k_splits: int = 1,
+         workspace: torch.Tensor | None = None, kernel: int = N.CONV_KERNEL_AUTO,
+         config: int = 0) -> torch.Tensor:
+    """out [B, L, n_cols] = x [B, L, C_in] (bf16) times a packed k = 1 conv (bias included), in
+    ``k_splits`` slices of the input channels (``splitk_conv``) when k_splits > 1."""
+    if k_splits == 1:
+        return fused_conv(x, conv, out, kernel=kernel, config=config)
+    if conv.taps != 1:
+        raise ValueError("the split-K GEMM takes k = 1 convs")
+    return splitk_conv(x, conv, out, k_splits=k_splits, workspace=workspace, kernel=kernel,
+                       config=config)
 
 
 def fused_conv(x: torch.Tensor, conv: PackedConv, out: torch.Tensor | None, *,

@@ -51,6 +51,7 @@ from ..kernels.conv import (
     pack_conv1d,
     pack_conv_transpose1d,
     residual_stack,
+    splitk_conv,
     stack_coefficients,
 )
 from ..kernels.rvq import rvq_gather_sum
@@ -97,6 +98,8 @@ FUSED_UNIT_CHANNELS = (96, 192)
 FUSED_UNIT_CHANNELS_BF16 = (96, 192)
 # channel counts the residual-stack kernel (every unit of a block in one launch) handles
 STACK_CHANNELS = (96,)
+# K slices of the input conv with bf16 weights (kept when its input channels divide into them)
+IN_CONV_SPLITS = 4
 
 
 def _snake_coefficients(alpha: torch.Tensor | dict[str, torch.Tensor],
@@ -268,6 +271,13 @@ class DacCodecDecoder:
         self.final_in_stack = (bool(self.blocks) and self.blocks[-1].stack is not None
                                and self.blocks[-1].c_out == self.final_channels
                                and self.final_taps <= 8)
+        # the input conv in K slices (omni_conv1d_splitk) with bf16 weights: at a streaming
+        # step's few positions (64 streams x 12 frames) its unsplit tiles fill a quarter of the
+        # GPU; the slice count is the layer's, never the batch's, so every decode of a stream
+        # sums alike (streamed == whole, bit for bit)
+        ic_conv = self.in_conv.conv
+        self.in_conv_splits = (IN_CONV_SPLITS if ic_conv.scale is None and ic_conv.taps in (1, 7)
+                               and ic_conv.c_in % (32 * IN_CONV_SPLITS) == 0 else 1)
         self._workspaces: dict[tuple[int, int], _Workspace] = {}
         self._checked_index: tuple[weakref.ref, int] | None = None
         # a utils.timing.LaunchTimer installed here records every launch with its work
@@ -298,7 +308,8 @@ class DacCodecDecoder:
         if ws is None:
             dev = self.device
             length = frames * self.front_upsample
-            largest = length * self.in_conv.conv.n_cols
+            # x also holds the input conv's split-K partials
+            largest = length * self.in_conv.conv.n_cols * self.in_conv_splits
             for blk in self.blocks:
                 length *= blk.stride
                 largest = max(largest, length * blk.c_out)
@@ -353,8 +364,13 @@ class DacCodecDecoder:
         u = self._view(ws.u[cur], batch, length, self.in_conv.conv.n_cols)
         ic = self.in_conv
         with timer.launch("conv", 2.0 * batch * length * ic.conv.macs_per_position, ic.name):
-            fused_conv(z, ic.conv, u, activation=snake, act_a=ic.out_a, act_b=ic.out_b,
-                       **hist(ic.name))
+            if self.in_conv_splits > 1:
+                # the partials go to the residual-stream buffer, unused until the first up conv
+                splitk_conv(z, ic.conv, u, k_splits=self.in_conv_splits, workspace=ws.x,
+                            activation=snake, act_a=ic.out_a, act_b=ic.out_b, **hist(ic.name))
+            else:
+                fused_conv(z, ic.conv, u, activation=snake, act_a=ic.out_a, act_b=ic.out_b,
+                           **hist(ic.name))
         for bi, blk in enumerate(self.blocks):
             up = blk.up
             out_len = length * blk.stride

@@ -1,12 +1,15 @@
-"""Split-K k = 1 convs (``omni_conv1d_splitk``), the GEMMs of the code2wav pre-transformer and
+"""Split-K convs (``omni_conv1d_splitk``): k = 1, the GEMMs of the code2wav pre-transformer and
 ConvNeXt blocks (the reference's ``F.linear`` calls, sglang_omni/models/qwen3_omni/components/
-code2wav.py:266,311,318,322):
+code2wav.py:266,311,318,322), and k = 7 with its slot history and output Snake, a decoder's input
+conv over a streaming step (``CausalConvNet``, modded_dac.py:566-572):
 
 * every tile of the LDS-DMA k = 1 list, forced, at 2 and 4 slices, against the float64 GEMM of
   the same bf16 operands (float32 output: float32-summation tolerance);
 * a row gives the same bits whatever batch it runs in (the summation order depends on C_in and
   the slice count only): rows decoded 3, 36 and 36 at a time equal the 75-row launch;
-* the split form refuses what it does not take, and a workspace that is too small.
+* the split form refuses what it does not take, and a workspace that is too small;
+* k = 7: every tile of its split list, forced, against the float64 causal conv + bias + Snake;
+  a stream decoded in chunks through its slot history equals the whole stream bit for bit.
 """
 
 from __future__ import annotations
@@ -17,7 +20,13 @@ import pytest
 import torch
 
 from sglang_omni_amd import _native as N
-from sglang_omni_amd.kernels.conv import _conv_args, gemm, pack_conv1d, splitk_workspace_elements
+from sglang_omni_amd.kernels.conv import (
+    _conv_args,
+    gemm,
+    pack_conv1d,
+    splitk_conv,
+    splitk_workspace_elements,
+)
 
 pytestmark = pytest.mark.gpu
 
@@ -82,3 +91,74 @@ def test_split_form_refusals(gpu):
     status = lib.omni_conv1d_splitk(ctypes.byref(args), 2, ws.data_ptr(), 16,
                                     N.CONV_KERNEL_AUTO, 0, N.stream_handle(gpu))
     assert status == N.INVALID_ARG  # workspace_bytes below the partials' size
+
+
+SPLIT7_TILES = 2  # entries of the k = 7 LDS-DMA split list
+
+
+def conv7_operands(batch, length, c_in, c_out, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = (torch.randn(batch, length, c_in, generator=gen)).to(torch.bfloat16)
+    w = (torch.randn(c_out, c_in, 7, generator=gen) / (7 * c_in) ** 0.5).to(torch.bfloat16).float()
+    b = (torch.randn(c_out, generator=gen) * 0.1).float()
+    alpha = (torch.rand(c_out, generator=gen) + 0.5).float()
+    return x, w, b, alpha
+
+
+def causal_conv_snake_f64(x, w, b, alpha):
+    """float64 causal conv (left pad 6) + bias, then Snake(alpha): [B, L, C_out]."""
+    xd = torch.nn.functional.pad(x.double().transpose(1, 2), (6, 0))
+    y = torch.nn.functional.conv1d(xd, w.double(), b.double()).transpose(1, 2)
+    a = alpha.double()
+    return y + (a + 1e-9).reciprocal() * torch.sin(a * y) ** 2
+
+
+@pytest.mark.parametrize("splits", [2, 4])
+@pytest.mark.parametrize("config", range(1, SPLIT7_TILES + 1))
+def test_each_k7_split_tile_matches_the_float64_conv(gpu, config, splits):
+    batch, length, c_in, c_out = 6, 40, 512, 384
+    x, w, b, alpha = conv7_operands(batch, length, c_in, c_out, 20 * config + splits)
+    packed = pack_conv1d(w, b).to(gpu)
+    xg = x.to(gpu)
+    ws = torch.empty(splitk_workspace_elements(xg, packed, splits), device=gpu)
+    out = torch.empty(batch, length, c_out, device=gpu)
+    a = alpha.to(gpu)
+    splitk_conv(xg, packed, out, k_splits=splits, workspace=ws, kernel=N.CONV_KERNEL_DMA,
+                config=config, activation=N.ACT_SNAKE, act_a=a, act_b=(a + 1e-9).reciprocal())
+    ref = causal_conv_snake_f64(x, w, b, alpha)
+    scale = ref.abs().max().item()
+    torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5, atol=1e-5 * scale)
+
+
+@pytest.mark.parametrize("splits", [2, 4])
+def test_k7_split_stream_in_chunks_equals_the_whole(gpu, splits):
+    """Rows decoded in chunks through the slot history (chunks shorter than the six-sample context
+    included) give the whole rows' bits; the rows sit in shuffled slots of a larger pool."""
+    batch, c_in, c_out = 5, 512, 256
+    chunks = (12, 3, 12, 25)
+    length = sum(chunks)
+    x, w, b, alpha = conv7_operands(batch, length, c_in, c_out, 31 + splits)
+    packed = pack_conv1d(w, b).to(gpu)
+    xg = x.to(gpu)
+    a = alpha.to(gpu)
+    act = dict(activation=N.ACT_SNAKE, act_a=a, act_b=(a + 1e-9).reciprocal())
+    ws = torch.empty(splitk_workspace_elements(xg, packed, splits), device=gpu)
+    whole = torch.empty(batch, length, c_out, dtype=torch.bfloat16, device=gpu)
+    splitk_conv(xg, packed, whole, k_splits=splits, workspace=ws, **act)
+    slots = 9
+    hist = torch.randn(slots, 2, 6, c_in, device=gpu).to(torch.bfloat16)  # a cold start ignores it
+    parity = torch.zeros(slots, dtype=torch.int64, device=gpu)
+    slot_index = torch.tensor([7, 2, 0, 5, 3], device=gpu)
+    parts, start = [], 0
+    for n, size in enumerate(chunks):
+        xc = xg[:, start:start + size].contiguous()
+        o = torch.empty(batch, size, c_out, dtype=torch.bfloat16, device=gpu)
+        splitk_conv(xc, packed, o, k_splits=splits, workspace=ws, history=hist,
+                    slot_index=slot_index, slot_parity=parity, history_cold=n == 0, **act)
+        parity[slot_index] += 1
+        parts.append(o)
+        start += size
+    assert torch.equal(torch.cat(parts, dim=1), whole)
+    ref = causal_conv_snake_f64(x, w, b, alpha)
+    err = (whole.cpu().double() - ref).abs().max().item()
+    assert err <= 2 ** -7 * ref.abs().max().item()  # the bf16 output's rounding
