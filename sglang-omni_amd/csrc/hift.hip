@@ -63,7 +63,8 @@ __global__ void __launch_bounds__(kThreads) short_time_spectrum_kernel(const Stf
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.y;
   const int64_t f0 = (int64_t)blockIdx.x * kFramesPerBlock;
-  for (int e = tid; e < comps * n_fft; e += kThreads) basis[e] = p.basis[e];
+  if constexpr (NF == 0)
+    for (int e = tid; e < comps * n_fft; e += kThreads) basis[e] = p.basis[e];
   // the block's signal span: frames f0 .. f0 + kFramesPerBlock - 1 read padded samples
   // f0 * hop .. (f0 + kFramesPerBlock - 1) * hop + n_fft - 1
   const int64_t nframes = min((int64_t)kFramesPerBlock, p.frames - f0);
@@ -79,12 +80,16 @@ __global__ void __launch_bounds__(kThreads) short_time_spectrum_kernel(const Stf
   if (tid >= nframes) return;
   float* o = p.out + (row * comps) * p.frames + f0 + tid;
   if constexpr (NF != 0) {
+    // the bases are the same for every thread: read through the constant address space, they
+    // arrive by scalar loads and feed the FMAs as scalar operands (no LDS traffic)
+    typedef __attribute__((address_space(4))) const float cfloat;
+    cfloat* gbasis = (cfloat*)(p.basis);
     float s[NF];
 #pragma unroll
     for (int k = 0; k < NF; ++k) s[k] = seg[tid * hop + k];
 #pragma unroll 2
     for (int c = 0; c < comps; ++c) {
-      const float* b = basis + c * NF;
+      cfloat* b = gbasis + c * NF;
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < NF; ++k) acc = __builtin_fmaf(s[k], b[k], acc);
@@ -209,6 +214,100 @@ __global__ void __launch_bounds__(kThreads) overlap_add_inverse_kernel(const Ist
   p.out[row * p.out_stride + i] = y;
 }
 
+// HiFT's geometry (n_fft 16, hop 4, 9 bins): each thread finishes 4 samples of one window phase
+// r = sample % 4 (samples i0 + tid + 256 k), so its 4 x 18 basis values and 4 squared-window
+// values stay in registers for all of them (2 or 8 samples per thread measured slower: 8 leaves
+// each workgroup's exp / sin / sincos staging too long a serial chain); the workgroup's frames sit in LDS as rows of 20
+// floats (18 components, 2 pad) read 16 bytes at a time. Every output takes the generic kernel's
+// terms in its order (overlaps ascending, then bins), so the two give the same bits.
+constexpr int kInv16Samples = 4 * kThreads;  // samples per workgroup
+constexpr int kInv16Pitch = 20;              // floats per frame row in LDS
+constexpr int inverse16_frames() { return (kInv16Samples - 1) / 4 + 16 / 4 + 1; }
+constexpr size_t inverse16_lds_bytes() { return (size_t)inverse16_frames() * kInv16Pitch * 4; }
+
+__global__ void __launch_bounds__(kThreads) overlap_add_inverse16_kernel(const IstftParams p) {
+  constexpr int NF = 16, HP = 4, BINS = 9, COMPS = 18, OV = NF / HP, HALF = NF / 2;
+  extern __shared__ float smem[];
+  float* spec = smem;  // [frames of the window][kInv16Pitch]
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.y;
+  const int64_t i0 = (int64_t)blockIdx.x * kInv16Samples;
+  const int64_t fa = (i0 + HALF) / HP - (OV - 1);
+  const int64_t fb = (i0 + kInv16Samples - 1 + HALF) / HP;
+  const int nf = (int)(fb - fa + 1);
+  if (p.tail) {
+    for (int e = tid; e < nf * BINS; e += kThreads) {
+      const int j = e / BINS;
+      const int b = e - j * BINS;
+      const int64_t f = fa + j;
+      float re = 0.f, im = 0.f;
+      if (f >= 0 && f < p.frames) {
+        const float* hf = p.h + row * p.h_row_stride + f * p.h_frame_stride;
+        const float mag = fminf(expf(hf[b]), p.mag_clip);
+        const float phase = sinf(hf[BINS + b]);
+        float sn, cs;
+        sincosf(phase, &sn, &cs);
+        re = mag * cs;
+        im = mag * sn;
+      }
+      spec[j * kInv16Pitch + b] = re;
+      spec[j * kInv16Pitch + BINS + b] = im;
+    }
+  } else {
+    for (int e = tid; e < nf * COMPS; e += kThreads) {
+      const int j = e / COMPS;
+      const int c = e - j * COMPS;
+      const int64_t f = fa + j;
+      float v = 0.f;
+      if (f >= 0 && f < p.frames) {
+        const float* src = c < BINS ? p.re : p.im;
+        const int b = c < BINS ? c : c - BINS;
+        v = src[(row * BINS + b) * p.frames + f];
+      }
+      spec[j * kInv16Pitch + c] = v;
+    }
+  }
+  // this thread's window phase (i0 is a multiple of HP): t = r + HP o for overlap o
+  const int r = (tid + HALF) % HP;
+  float bas[OV][COMPS], w2[OV];
+#pragma unroll
+  for (int o = 0; o < OV; ++o) {
+    w2[o] = p.win2[r + HP * o];
+#pragma unroll
+    for (int c = 0; c < COMPS; ++c) bas[o][c] = p.basis[c * NF + r + HP * o];
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int k = 0; k < kInv16Samples / kThreads; ++k) {
+    const int64_t i = i0 + tid + (int64_t)k * kThreads;
+    if (i >= p.samples) break;
+    const int64_t pos = i + HALF;
+    float signal = 0.f, envelope = 0.f;
+#pragma unroll
+    for (int o = 0; o < OV; ++o) {
+      const int64_t f = pos / HP - o;
+      if (f < 0 || f >= p.frames) continue;
+      const f32x4* sv = reinterpret_cast<const f32x4*>(spec + (int)(f - fa) * kInv16Pitch);
+      float s[kInv16Pitch];
+#pragma unroll
+      for (int q = 0; q < kInv16Pitch / 4; ++q) {
+        const f32x4 v = sv[q];
+        s[4 * q] = v[0];
+        s[4 * q + 1] = v[1];
+        s[4 * q + 2] = v[2];
+        s[4 * q + 3] = v[3];
+      }
+#pragma unroll
+      for (int b = 0; b < BINS; ++b)
+        signal += __builtin_fmaf(s[b], bas[o][b], s[BINS + b] * bas[o][BINS + b]);
+      envelope += w2[o];
+    }
+    float y = signal / envelope;
+    if (p.tail) y = fminf(fmaxf(y, -p.audio_limit), p.audio_limit);
+    p.out[row * p.out_stride + i] = y;
+  }
+}
+
 bool valid_fft(int64_t n_fft, int64_t hop, int64_t bins) {
   return n_fft >= 2 && n_fft <= kMaxFft && hop >= 1 && hop <= n_fft && n_fft % hop == 0 &&
          bins == n_fft / 2 + 1;
@@ -262,10 +361,13 @@ int launch_inverse(IstftParams& p, int64_t rows, omni_stream_t stream) {
   dim3 grid((unsigned)((p.samples + kSamplesPerBlock - 1) / kSamplesPerBlock), (unsigned)rows);
   const size_t lds = inverse_lds_bytes(p.n_fft, p.hop, p.bins);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (p.n_fft == 16 && p.hop == 4)
-    hipLaunchKernelGGL((overlap_add_inverse_kernel<16, 4>), grid, dim3(kThreads), lds, s, p);
-  else
+  if (p.n_fft == 16 && p.hop == 4) {
+    dim3 grid16((unsigned)((p.samples + kInv16Samples - 1) / kInv16Samples), (unsigned)rows);
+    hipLaunchKernelGGL(overlap_add_inverse16_kernel, grid16, dim3(kThreads), inverse16_lds_bytes(),
+                       s, p);
+  } else {
     hipLaunchKernelGGL((overlap_add_inverse_kernel<0, 0>), grid, dim3(kThreads), lds, s, p);
+  }
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
 }
