@@ -25,7 +25,8 @@ ARCH = "gfx950"
 
 SOURCES = ["capi.hip", "rvq.hip", "conv.hip", "conv_k7_raw_wbf16.hip", "conv_k7_raw_wfp8.hip",
            "conv_k7_act_wbf16.hip", "conv_k7_act_wfp8.hip", "conv_k11.hip", "conv_ru_wbf16.hip",
-           "conv_dma_t1.hip", "conv_dma_t2.hip", "conv_dma_t7.hip",
+           "conv_dma_t1.hip", "conv_dma_t2.hip", "conv_dma_t3.hip", "conv_dma_t7.hip",
+           "conv_dma_t11.hip",
            "conv_ru_wfp8.hip", "residual_stack.hip", "residual_stack_wbf16.hip",
            "residual_stack_wfp8.hip", "single_output_conv.hip", "codec_state.hip", "snake.hip", "hift.hip",
            "egress.hip", "code2wav_front.hip", "channel_embedding.hip", "conv_general.hip"]

@@ -30,6 +30,8 @@ int dispatch(const ConvParams& p, bool x_f32, bool fp8, bool fuse2, int& kernel,
     if (p.taps == 7) status = launch_dma_taps7(p, fp8, ch, stream);
     else if (p.taps == 2) status = launch_dma_taps2(p, fp8, ch, stream);
     else if (p.taps == 1) status = launch_dma_taps1(p, fp8, ch, stream);
+    else if (p.taps == 3) status = launch_dma_taps3(p, fp8, ch, stream);
+    else if (p.taps == 11) status = launch_dma_taps11(p, fp8, ch, stream);
     if (status != OMNI_ERR_UNSUPPORTED || want == OMNI_CONV_KERNEL_DMA) {
       kernel = OMNI_CONV_KERNEL_DMA;
       return status;

@@ -430,10 +430,13 @@ int launch_first_fit(const ConvParams& p, Choice& ch, hipStream_t stream) {
 }
 
 // Launchers by tap count (1: k = 1 convs, 2: transposed convs of kernel 2 * stride, 7: k = 7
-// convs), one translation unit each.
+// convs; 3 and 11: narrow layers' k = 3 and k = 11 convs), one translation unit each.
 // `fp8`: the packed weights are E4M3 (one byte per weight, per-column scales in the epilogue).
 int launch_dma_taps1(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps2(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
+// narrow layers only (n_cols <= 64, bf16 weights): k = 3 and k = 11
+int launch_dma_taps3(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
+int launch_dma_taps11(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 
 }  // namespace omni_conv

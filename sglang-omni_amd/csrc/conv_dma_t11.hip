@@ -1,0 +1,14 @@
+// LDS-DMA convolution kernels for k = 11 convs of narrow layers (HiFiGAN's multi-receptive-
+// field ResBlocks at 64 and 32 channels; bf16 operand and weights).
+#include "conv_dma.h"
+
+namespace omni_conv {
+
+int launch_dma_taps11(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream) {
+  // 64 columns x 256 positions or 32 x 512 (an 11-tap weight stage of 64 columns takes 46 KB)
+  if (fp8 || p.k_splits > 1 || p.n_cols > 64) return OMNI_ERR_UNSUPPORTED;
+  return launch_first_fit<DmaConfig<1, 8, 4, 2, 384, 11, 1>,
+                          DmaConfig<1, 8, 2, 4, 640, 11, 1>>(p, ch, stream);
+}
+
+}  // namespace omni_conv

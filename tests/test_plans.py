@@ -10,7 +10,13 @@ import pytest
 
 from sglang_omni_amd import _native as N
 from sglang_omni_amd.kernels.conv import plan_shapes
-from tests.test_gpu_tiles import DMA_LIST, FUSED_LIST, STAGED11_LIST, STAGED_LIST
+from tests.test_gpu_tiles import (
+    DMA_LIST,
+    FUSED_LIST,
+    NARROW_DMA_LIST,
+    STAGED11_LIST,
+    STAGED_LIST,
+)
 
 
 def test_list_lengths_match_the_forced_tile_sweep():
@@ -25,8 +31,13 @@ def test_list_lengths_match_the_forced_tile_sweep():
                          in_activation=N.ACT_SNAKE)
     assert staged.kernel == N.CONV_KERNEL_STAGED and staged.configs == STAGED_LIST
     s11 = plan_shapes(batch=2, length=300, c_in=64, n_cols=64, c_out=64, taps=11, dilation=5,
-                      left_pad=25)
+                      left_pad=25, in_activation=N.ACT_LEAKY_RELU)
     assert s11.kernel == N.CONV_KERNEL_STAGED11 and s11.configs == STAGED11_LIST
+    for taps, n in NARROW_DMA_LIST.items():  # narrow layers with a ready bf16 operand
+        for cols in (64, 32):
+            plan = plan_shapes(batch=2, length=300, c_in=cols, n_cols=cols, c_out=cols,
+                               taps=taps, dilation=5, left_pad=(taps - 1) * 5 // 2)
+            assert plan.kernel == N.CONV_KERNEL_DMA and plan.configs == n
     fused = plan_shapes(batch=2, length=300, c_in=96, n_cols=96, c_out=96, taps=7, dilation=9,
                         fused_unit=True)
     assert fused.kernel == N.CONV_KERNEL_FUSED_UNIT and fused.configs == FUSED_LIST
