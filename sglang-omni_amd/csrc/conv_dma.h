@@ -38,7 +38,10 @@
 
 namespace omni_conv {
 
-template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false>
+// ONE: layers of a single stage (c_in == 32 KC) take a ring of one buffer, which lets two
+// workgroups share a CU: one's DMA and epilogue run under the other's matrix work.
+template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false,
+          bool ONE = false>
 struct DmaTile {
   using Base = ConvTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS>;  // epilogue geometry
   static constexpr int NT = Base::NT;
@@ -55,23 +58,29 @@ struct DmaTile {
   static constexpr int XCHUNK = MAX_ROWS * kChunk;  // elements of a chunk's input rows
   static constexpr int WCHUNK = NIW * 64 * 8;       // elements of a chunk's weights
   static constexpr int BUF = KC * (XCHUNK + WCHUNK);
-  static constexpr size_t ring_bytes = 2 * (size_t)BUF * 2;
+  static constexpr int RING = ONE ? 1 : 2;       // ring buffers
+  static constexpr int WGS_PER_CU = ONE ? 2 : 1;  // workgroups the LDS and registers are sized for
+  static constexpr size_t ring_bytes = RING * (size_t)BUF * 2;
   static constexpr size_t epi_bytes = (size_t)Base::EPI_ROWS * Base::EPITCH * 4;
   static constexpr size_t coef_offset = ring_bytes > epi_bytes ? ring_bytes : epi_bytes;
   static constexpr size_t lds_bytes = coef_offset + Base::coef_bytes();
   static_assert(MAX_ROWS % 16 == 0, "input rows are staged 16 per DMA instruction");
   static_assert(X_PIECES <= 16, "two mode bits per input piece in 32 bits");
-  static_assert(lds_bytes <= 160 * 1024, "the ring, epilogue and coefficients fit the CU's LDS");
+  static_assert(lds_bytes * WGS_PER_CU <= 160 * 1024,
+                "the ring, epilogue and coefficients of each resident workgroup fit the CU's LDS");
 };
 
-// The ring takes most of a CU's LDS, so one workgroup runs per CU: WAVES_CO * WAVES_P / 4 waves
-// per SIMD, which the register allocation may assume.
+// The two-buffer ring takes most of a CU's LDS, so one workgroup runs per CU: WAVES_CO * WAVES_P / 4
+// waves per SIMD, which the register allocation may assume (twice that with ONE's one-buffer
+// ring, two workgroups per CU).
 template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8,
-          bool SPLIT>
+          bool SPLIT, bool ONE>
 __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
-    __attribute__((amdgpu_waves_per_eu(WAVES_CO * WAVES_P / 4, WAVES_CO * WAVES_P / 4)))
+    __attribute__((amdgpu_waves_per_eu(WAVES_CO * WAVES_P / 4 * (ONE ? 2 : 1),
+                                       WAVES_CO * WAVES_P / 4 * (ONE ? 2 : 1))))
     conv_dma_kernel(const ConvParams p) {
-  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
+  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, ONE>;
+  static_assert(!(ONE && SPLIT), "a one-stage layer has no K slices");
   constexpr int NT = Tile::NT;
   constexpr int NW = Tile::NW;
   constexpr int BCO = Tile::BCO;
@@ -218,12 +227,12 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     return lds + buf * Tile::BUF + c * (Tile::XCHUNK + Tile::WCHUNK);
   };
 
-  // Zero padding rows: written once into every chunk of both buffers (no DMA writes them).
+  // Zero padding rows: written once into every chunk of the ring's buffers (no DMA writes them).
 #pragma unroll
   for (int u = 0; u < Tile::X_PIECES; ++u) {
     if (((xmode >> (2 * u)) & 3u) == 0u) {
       const int r = (tid >> 2) + u * (NT / 4);
-      for (int bc = 0; bc < 2 * KC; ++bc)
+      for (int bc = 0; bc < Tile::RING * KC; ++bc)
         *reinterpret_cast<u32x4*>(xs_of(bc / KC, bc % KC) + r * kChunk + q8) = u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -364,9 +373,9 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 }
 
 template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false,
-          bool SPLIT = false>
+          bool SPLIT = false, bool ONE = false>
 struct DmaConfig {
-  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8>;
+  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, ONE>;
 
   // Staged rows of the fullest tile: BP positions over at most nseg row segments, each with its
   // own halo.
@@ -383,7 +392,8 @@ struct DmaConfig {
   static bool fits(const ConvParams& p) {
     const int64_t padded = (p.n_cols + Tile::BCO - 1) / Tile::BCO * Tile::BCO;
     return p.taps == TAPS && (p.k_splits > 1) == SPLIT &&
-           p.c_in % (kChunk * KC * p.k_splits) == 0 && rows_needed(p) <= MAX_ROWS &&
+           p.c_in % (kChunk * KC * p.k_splits) == 0 && (!ONE || p.c_in == kChunk * KC) &&
+           rows_needed(p) <= MAX_ROWS &&
            (padded - p.n_cols) * 8 <= p.n_cols;
   }
 
@@ -397,7 +407,7 @@ struct DmaConfig {
     const int64_t positions = (int64_t)p.batch * p.length;
     p.p_tiles = (int)((positions + Tile::BP - 1) / Tile::BP);
     p.n_tiles = (int)((p.n_cols + Tile::BCO - 1) / Tile::BCO);
-    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, SPLIT>;
+    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, SPLIT, ONE>;
     // raised once per instantiation, on its first launch (no attribute calls inside a capture)
     static const bool raised = raise_lds_limit((const void*)k);
     (void)raised;

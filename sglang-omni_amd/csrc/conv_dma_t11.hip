@@ -1,13 +1,19 @@
 // LDS-DMA convolution kernels for k = 11 convs of narrow layers (HiFiGAN's multi-receptive-
-// field ResBlocks at 64 and 32 channels; bf16 operand and weights).
+// field ResBlocks at 128, 64 and 32 channels; bf16 operand and weights).
 #include "conv_dma.h"
 
 namespace omni_conv {
 
 int launch_dma_taps11(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream) {
-  // 64 columns x 256 positions or 32 x 512 (an 11-tap weight stage of 64 columns takes 46 KB)
-  if (fp8 || p.k_splits > 1 || p.n_cols > 64) return OMNI_ERR_UNSUPPORTED;
-  return launch_first_fit<DmaConfig<1, 8, 4, 2, 384, 11, 1>,
+  if (fp8 || p.k_splits > 1 || (p.n_cols > 64 && p.n_cols != 128)) return OMNI_ERR_UNSUPPORTED;
+  // 128 columns: two column tiles of 64 x 256 (an 11-tap weight stage of 128 columns would take
+  // 92 KB, twice over in the ring)
+  if (p.n_cols == 128) return launch_first_fit<DmaConfig<1, 8, 4, 2, 384, 11, 1>>(p, ch, stream);
+  // 32 columns x 512 positions for a layer of one stage (c_in 32) on a one-buffer ring, two
+  // workgroups per CU; 64 columns x 256 positions or 32 x 512 (an 11-tap weight stage of 64
+  // columns takes 46 KB)
+  return launch_first_fit<DmaConfig<1, 8, 2, 4, 640, 11, 1, false, false, true>,
+                          DmaConfig<1, 8, 4, 2, 384, 11, 1>,
                           DmaConfig<1, 8, 2, 4, 640, 11, 1>>(p, ch, stream);
 }
 

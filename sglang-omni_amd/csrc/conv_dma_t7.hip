@@ -17,9 +17,15 @@ int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stre
   // narrow layers (HiFiGAN's 64- and 32-channel stages): 64 or 32 columns x 512 positions
   // (64 first: 13.99 against 14.18 ms per HiFiGAN call with 32 first, 14.48 on the
   // register-staged kernel)
+  // (a layer of one stage, c_in 32, first: two workgroups per CU on a one-buffer ring)
   if (p.n_cols <= 64 && p.k_splits == 1 && !fp8)
-    return launch_first_fit<DmaConfig<1, 8, 4, 4, 640, 7, 1>,
+    return launch_first_fit<DmaConfig<1, 8, 2, 4, 640, 7, 1, false, false, true>,
+                            DmaConfig<1, 8, 4, 4, 640, 7, 1>,
                             DmaConfig<1, 8, 2, 4, 640, 7, 1>>(p, ch, stream);
+  // HiFiGAN's 128-channel stage: 128 columns x 192 positions, 8 waves of 64 x 48 (the ring fills
+  // the 160 KiB)
+  if (p.n_cols == 128 && p.k_splits == 1 && !fp8)
+    return launch_first_fit<DmaConfig<2, 4, 4, 3, 320, 7, 1>>(p, ch, stream);
   if (p.k_splits > 1)  // split-K (bf16 weights): K slices of the 96 x 192 tiles (8 / 4 waves)
     return launch_first_fit<DmaConfig<2, 4, 3, 3, 368, 7, 1, false, true>,
                             DmaConfig<1, 4, 6, 3, 368, 7, 1, false, true>>(p, ch, stream);

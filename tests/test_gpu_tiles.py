@@ -33,7 +33,9 @@ pytestmark = pytest.mark.gpu
 # entries per list (tests/test_plans.py checks these against the library's own counts)
 DMA_LIST = {1: 4, 2: 4, 7: 4}
 # the narrow layers' LDS-DMA lists (n_cols <= 64, bf16 weights: HiFiGAN's 64 / 32-channel stages)
-NARROW_DMA_LIST = {3: 2, 7: 2, 11: 2}
+NARROW_DMA_LIST = {3: 4, 7: 3, 11: 3}
+# and for its 128-channel stage (n_cols == 128)
+NARROW128_DMA_LIST = {3: 1, 7: 1, 11: 1}
 STAGED_LIST = 10
 STAGED11_LIST = 10
 FUSED_LIST = 3
@@ -174,14 +176,14 @@ def test_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, config, fp8):
         check_float64(forced, conv64(x.float().cpu(), w, b, dilation=packed.dilation))
 
 
-NARROW_CASES = [(taps, cols, k) for taps in (3, 7, 11) for cols in (64, 32)
-                for k in range(1, NARROW_DMA_LIST[taps] + 1)]
+NARROW_CASES = [(taps, cols, k) for taps in (3, 7, 11) for cols in (128, 64, 32)
+                for k in range(1, (NARROW128_DMA_LIST if cols == 128 else NARROW_DMA_LIST)[taps] + 1)]
 
 
 @pytest.mark.parametrize("taps,cols,config", NARROW_CASES, ids=lambda v: str(v))
 def test_narrow_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, cols, config):
-    """HiFiGAN's ResBlock convs ('same' padding, dilation 5) at 64 and 32 channels on the narrow
-    LDS-DMA tiles: each entry against the float64 conv and the size-chosen entry's bits."""
+    """HiFiGAN's ResBlock convs ('same' padding, dilation 5) at 128, 64 and 32 channels on the
+    narrow LDS-DMA tiles: each entry against the float64 conv and the size-chosen entry's bits."""
     gen = torch.Generator().manual_seed(1000 * taps + 10 * cols + config)
     c_in = c_out = cols
     d = 5
@@ -192,7 +194,8 @@ def test_narrow_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, cols, co
                    left_pad=packed.left_pad)
     shape = pick_shape(plan_kw, N.CONV_KERNEL_DMA, config, streamed=False)
     if shape is None:
-        pytest.skip(f"entry {config} takes {cols} columns only through the wider entry's padding")
+        pytest.skip(f"entry {config} does not take {cols} columns (column padding or a one-stage "
+                    f"entry's c_in)")
     batch, length = shape
     x = bf(torch.randn(batch, length, c_in, generator=gen)).to(gpu, torch.bfloat16)
     forced = torch.empty(batch, length, c_out, dtype=torch.float32, device=gpu)

@@ -13,6 +13,7 @@ from sglang_omni_amd.kernels.conv import plan_shapes
 from tests.test_gpu_tiles import (
     DMA_LIST,
     FUSED_LIST,
+    NARROW128_DMA_LIST,
     NARROW_DMA_LIST,
     STAGED11_LIST,
     STAGED_LIST,
@@ -33,8 +34,9 @@ def test_list_lengths_match_the_forced_tile_sweep():
     s11 = plan_shapes(batch=2, length=300, c_in=64, n_cols=64, c_out=64, taps=11, dilation=5,
                       left_pad=25, in_activation=N.ACT_LEAKY_RELU)
     assert s11.kernel == N.CONV_KERNEL_STAGED11 and s11.configs == STAGED11_LIST
-    for taps, n in NARROW_DMA_LIST.items():  # narrow layers with a ready bf16 operand
-        for cols in (64, 32):
+    for taps in NARROW_DMA_LIST:  # narrow layers with a ready bf16 operand
+        for cols in (128, 64, 32):
+            n = (NARROW128_DMA_LIST if cols == 128 else NARROW_DMA_LIST)[taps]
             plan = plan_shapes(batch=2, length=300, c_in=cols, n_cols=cols, c_out=cols,
                                taps=taps, dilation=5, left_pad=(taps - 1) * 5 // 2)
             assert plan.kernel == N.CONV_KERNEL_DMA and plan.configs == n
