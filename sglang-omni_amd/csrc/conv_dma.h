@@ -445,7 +445,7 @@ int launch_first_fit(const ConvParams& p, Choice& ch, hipStream_t stream) {
 int launch_dma_taps1(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps2(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
-// narrow layers only (n_cols <= 64, bf16 weights): k = 3 and k = 11
+// narrow layers only (n_cols <= 64 or 128, bf16 weights): k = 3 and k = 11
 int launch_dma_taps3(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps11(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 
