@@ -236,6 +236,22 @@ PMC_TRAFFIC_SOURCE = {"stack96": "profiles/residual_stack96_pmc.md: rocprofv3 FE
                                  "WRITE_SIZE of `bench.py --only stack96`, copy-calibrated"}
 
 
+def bench_hifigan(device) -> dict:
+    """HiFiGAN mel -> wave, 16 clips of 500 mel frames (10 s each at 24 kHz), bf16."""
+    from sglang_omni_amd.models import HifiGanVocoder, make_hifigan_weights
+    from sglang_omni_amd.models.configs import HIFIGAN_24K, hifigan_macs_per_frame
+
+    gen = torch.Generator().manual_seed(0)
+    voc = HifiGanVocoder(make_hifigan_weights(HIFIGAN_24K, seed=0), HIFIGAN_24K, device=device)
+    mel = (torch.randn(16, 80, 500, generator=gen) * 2 - 5).to(device)
+    dt = timed_call(lambda: voc(mel))
+    macs = hifigan_macs_per_frame(HIFIGAN_24K)
+    return {"workload": "HiFiGAN mel->wave, 16 x 500 mel frames (160 s), bf16",
+            "xRT": round(160.0 / dt, 1), "ms": round(dt * 1e3, 3),
+            "TFLOPs": round(2.0 * macs * 16 * 500 / dt / 1e12, 1),
+            "mfma_frac": round(2.0 * macs * 16 * 500 / dt / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+
 def run_only(args, device) -> None:
     from sglang_omni_amd import _native as N
     from sglang_omni_amd.kernels.conv import FinalConv, residual_stack
@@ -285,10 +301,8 @@ def timed_call(fn, reps: int = 3) -> float:
 
 def bench_other_configs(device) -> dict:
     """xRT of the other decoder configurations (one call each, inputs resident in HBM)."""
-    from sglang_omni_amd.models import (DacCodecDecoder, HifiGanVocoder, make_dac_weights,
-                                        make_hifigan_weights)
-    from sglang_omni_amd.models.configs import (CODEC_24K, CODEC_24K_LONG, HIFIGAN_24K,
-                                                dac_macs_per_frame, hifigan_macs_per_frame)
+    from sglang_omni_amd.models import DacCodecDecoder, make_dac_weights
+    from sglang_omni_amd.models.configs import CODEC_24K, CODEC_24K_LONG, dac_macs_per_frame
 
     def mfma(frames: int, macs_per_frame: int, dt: float) -> dict:
         """The whole decoder's algorithmic FLOPs over its time, against the bf16 MFMA peak (the
@@ -305,13 +319,7 @@ def bench_other_configs(device) -> dict:
                                "xRT": round(20.0 / dt, 1), "ms": round(dt * 1e3, 3),
                                **mfma(250, dac_macs_per_frame(CODEC_24K), dt)}
     del dec
-    voc = HifiGanVocoder(make_hifigan_weights(HIFIGAN_24K, seed=0), HIFIGAN_24K, device=device)
-    mel = (torch.randn(16, 80, 500, generator=gen) * 2 - 5).to(device)
-    dt = timed_call(lambda: voc(mel))
-    out["hifigan"] = {"workload": "HiFiGAN mel->wave, 16 x 500 mel frames (160 s), bf16",
-                      "xRT": round(160.0 / dt, 1), "ms": round(dt * 1e3, 3),
-                      **mfma(16 * 500, hifigan_macs_per_frame(HIFIGAN_24K), dt)}
-    del voc
+    out["hifigan"] = bench_hifigan(device)
     codes = torch.randint(0, 1024, (8, 32, 1500), generator=gen).to(device)
     long_weights = make_dac_weights(CODEC_24K_LONG, seed=0)
     for fmt in ("fp8", "bf16"):  # the same shape with each weight format
@@ -539,9 +547,9 @@ def main() -> None:
     parser.add_argument("--workload", default="streaming64")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-rvq-large", action="store_true")
-    parser.add_argument("--only", choices=["stack96", "copy", "qwen3_code2wav"],
+    parser.add_argument("--only", choices=["stack96", "copy", "qwen3_code2wav", "hifigan"],
                         help="run one kernel alone (hardware-counter profiles; prints no JSON), "
-                             "or only the Qwen3-Omni code2wav leg (prints its JSON)")
+                             "or only the Qwen3-Omni code2wav or HiFiGAN leg (prints its JSON)")
     parser.add_argument("--launches", type=int, default=2)
     parser.add_argument("--no-other-configs", action="store_true",
                         help="skip the xRT of the other configurations and the peak calibration")
@@ -559,6 +567,9 @@ def main() -> None:
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.only == "qwen3_code2wav":
         print(json.dumps(bench_qwen3_code2wav(device)), flush=True)
+        return
+    if args.only == "hifigan":
+        print(json.dumps(bench_hifigan(device)), flush=True)
         return
     if args.only:
         run_only(args, device)

@@ -38,10 +38,10 @@
 
 namespace omni_conv {
 
-// ONE: layers of a single stage (c_in == 32 KC) take a ring of one buffer, which lets two
-// workgroups share a CU: one's DMA and epilogue run under the other's matrix work.
+// OCC > 0: layers of a single stage (c_in == 32 KC) take a ring of one buffer, which lets OCC
+// workgroups share a CU: one's DMA and epilogue run under another's matrix work.
 template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false,
-          bool ONE = false>
+          int OCC = 0>
 struct DmaTile {
   using Base = ConvTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS>;  // epilogue geometry
   static constexpr int NT = Base::NT;
@@ -58,8 +58,8 @@ struct DmaTile {
   static constexpr int XCHUNK = MAX_ROWS * kChunk;  // elements of a chunk's input rows
   static constexpr int WCHUNK = NIW * 64 * 8;       // elements of a chunk's weights
   static constexpr int BUF = KC * (XCHUNK + WCHUNK);
-  static constexpr int RING = ONE ? 1 : 2;       // ring buffers
-  static constexpr int WGS_PER_CU = ONE ? 2 : 1;  // workgroups the LDS and registers are sized for
+  static constexpr int RING = OCC > 0 ? 1 : 2;        // ring buffers
+  static constexpr int WGS_PER_CU = OCC > 0 ? OCC : 1;  // workgroups the LDS and registers are sized for
   static constexpr size_t ring_bytes = RING * (size_t)BUF * 2;
   static constexpr size_t epi_bytes = (size_t)Base::EPI_ROWS * Base::EPITCH * 4;
   static constexpr size_t coef_offset = ring_bytes > epi_bytes ? ring_bytes : epi_bytes;
@@ -71,16 +71,16 @@ struct DmaTile {
 };
 
 // The two-buffer ring takes most of a CU's LDS, so one workgroup runs per CU: WAVES_CO * WAVES_P / 4
-// waves per SIMD, which the register allocation may assume (twice that with ONE's one-buffer
-// ring, two workgroups per CU).
+// waves per SIMD, which the register allocation may assume (OCC times that with a one-buffer
+// ring, OCC workgroups per CU).
 template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8,
-          bool SPLIT, bool ONE>
+          bool SPLIT, int OCC>
 __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
-    __attribute__((amdgpu_waves_per_eu(WAVES_CO * WAVES_P / 4 * (ONE ? 2 : 1),
-                                       WAVES_CO * WAVES_P / 4 * (ONE ? 2 : 1))))
+    __attribute__((amdgpu_waves_per_eu((WAVES_CO * WAVES_P * (OCC > 0 ? OCC : 1) + 3) / 4,
+                                       (WAVES_CO * WAVES_P * (OCC > 0 ? OCC : 1) + 3) / 4)))
     conv_dma_kernel(const ConvParams p) {
-  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, ONE>;
-  static_assert(!(ONE && SPLIT), "a one-stage layer has no K slices");
+  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, OCC>;
+  static_assert(!(OCC > 0 && SPLIT), "a one-stage layer has no K slices");
   constexpr int NT = Tile::NT;
   constexpr int NW = Tile::NW;
   constexpr int BCO = Tile::BCO;
@@ -373,9 +373,9 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 }
 
 template <int WAVES_CO, int WAVES_P, int TCO, int TP, int MAX_ROWS, int TAPS, int KC, bool W8 = false,
-          bool SPLIT = false, bool ONE = false>
+          bool SPLIT = false, int OCC = 0>
 struct DmaConfig {
-  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, ONE>;
+  using Tile = DmaTile<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, OCC>;
 
   // Staged rows of the fullest tile: BP positions over at most nseg row segments, each with its
   // own halo.
@@ -392,7 +392,7 @@ struct DmaConfig {
   static bool fits(const ConvParams& p) {
     const int64_t padded = (p.n_cols + Tile::BCO - 1) / Tile::BCO * Tile::BCO;
     return p.taps == TAPS && (p.k_splits > 1) == SPLIT &&
-           p.c_in % (kChunk * KC * p.k_splits) == 0 && (!ONE || p.c_in == kChunk * KC) &&
+           p.c_in % (kChunk * KC * p.k_splits) == 0 && (OCC == 0 || p.c_in == kChunk * KC) &&
            rows_needed(p) <= MAX_ROWS &&
            (padded - p.n_cols) * 8 <= p.n_cols;
   }
@@ -407,7 +407,7 @@ struct DmaConfig {
     const int64_t positions = (int64_t)p.batch * p.length;
     p.p_tiles = (int)((positions + Tile::BP - 1) / Tile::BP);
     p.n_tiles = (int)((p.n_cols + Tile::BCO - 1) / Tile::BCO);
-    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, SPLIT, ONE>;
+    auto k = conv_dma_kernel<WAVES_CO, WAVES_P, TCO, TP, MAX_ROWS, TAPS, KC, W8, SPLIT, OCC>;
     // raised once per instantiation, on its first launch (no attribute calls inside a capture)
     static const bool raised = raise_lds_limit((const void*)k);
     (void)raised;
@@ -445,7 +445,8 @@ int launch_first_fit(const ConvParams& p, Choice& ch, hipStream_t stream) {
 int launch_dma_taps1(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps2(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
-// narrow layers only (n_cols <= 64 or 128, bf16 weights): k = 3 and k = 11
+// HiFiGAN's layers only (bf16 weights; n_cols <= 64, or a multiple of 128 for k = 3, or 128 for
+// k = 11): k = 3 and k = 11
 int launch_dma_taps3(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps11(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 

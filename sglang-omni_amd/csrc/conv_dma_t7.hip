@@ -17,9 +17,10 @@ int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stre
   // narrow layers (HiFiGAN's 64- and 32-channel stages): 64 or 32 columns x 512 positions
   // (64 first: 13.99 against 14.18 ms per HiFiGAN call with 32 first, 14.48 on the
   // register-staged kernel)
-  // (a layer of one stage, c_in 32, first: two workgroups per CU on a one-buffer ring)
+  // (a layer of one stage, c_in 32, first: 32 columns x 256 positions, 4 waves, on a one-buffer
+  // ring with four workgroups per CU)
   if (p.n_cols <= 64 && p.k_splits == 1 && !fp8)
-    return launch_first_fit<DmaConfig<1, 8, 2, 4, 640, 7, 1, false, false, true>,
+    return launch_first_fit<DmaConfig<1, 4, 2, 4, 384, 7, 1, false, false, 4>,
                             DmaConfig<1, 8, 4, 4, 640, 7, 1>,
                             DmaConfig<1, 8, 2, 4, 640, 7, 1>>(p, ch, stream);
   // HiFiGAN's 128-channel stage: 128 columns x 192 positions, 8 waves of 64 x 48 (the ring fills

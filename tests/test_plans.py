@@ -35,8 +35,8 @@ def test_list_lengths_match_the_forced_tile_sweep():
                       left_pad=25, in_activation=N.ACT_LEAKY_RELU)
     assert s11.kernel == N.CONV_KERNEL_STAGED11 and s11.configs == STAGED11_LIST
     for taps in NARROW_DMA_LIST:  # narrow layers with a ready bf16 operand
-        for cols in (128, 64, 32):
-            n = (NARROW128_DMA_LIST if cols == 128 else NARROW_DMA_LIST)[taps]
+        for cols in (256, 128, 64, 32) if taps == 3 else (128, 64, 32):
+            n = (NARROW128_DMA_LIST if cols > 64 else NARROW_DMA_LIST)[taps]
             plan = plan_shapes(batch=2, length=300, c_in=cols, n_cols=cols, c_out=cols,
                                taps=taps, dilation=5, left_pad=(taps - 1) * 5 // 2)
             assert plan.kernel == N.CONV_KERNEL_DMA and plan.configs == n
