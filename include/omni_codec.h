@@ -205,9 +205,12 @@ int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
 /*
  * Kernel families of omni_conv1d_fused, each with a list of tile configurations (output columns x
  * positions per workgroup, waves, staged rows) that the call picks from by problem size:
- *   OMNI_CONV_KERNEL_DMA         LDS-DMA staged; bf16 operand used as is (no in_activation), bf16
- *                                weights, taps 1, 2 or 7, c_in a multiple of 32, no weight2; a
- *                                list of 4 per tap count
+ *   OMNI_CONV_KERNEL_DMA         LDS-DMA staged; bf16 operand used as is (no in_activation), c_in
+ *                                a multiple of 32, no weight2; taps 1, 2 or 7 with bf16 or E4M3
+ *                                weights: a list of 4 per tap count (bf16 k = 7 at 128 columns:
+ *                                1, at 64 or fewer: 3); taps 3 and 11 with bf16 weights at 64
+ *                                columns or fewer (4 and 3), at a multiple of 128 columns (taps
+ *                                3: 2) or at 128 (taps 11: 2)
  *   OMNI_CONV_KERNEL_STAGED      register-staged, taps <= 7, any operand mode and weight dtype;
  *                                10 configurations
  *   OMNI_CONV_KERNEL_STAGED11    register-staged, taps <= 11, bf16 weights, x bf16; 10
