@@ -90,3 +90,28 @@ def test_forced_choice_contract():
 def test_an_empty_call_plans_nothing():
     plan = plan_shapes(batch=0, length=12, c_in=96, n_cols=96, c_out=96, taps=7)
     assert plan.kernel == N.CONV_KERNEL_AUTO and plan.config == 0
+
+
+@pytest.mark.parametrize("channels,length", [(256, 4000), (128, 20000), (64, 60000), (32, 240000)])
+@pytest.mark.parametrize("taps", [3, 7, 11])
+def test_hifigan_resblock_convs_plan_to_their_tiles(channels, length, taps):
+    """HiFiGAN's ResBlock convs at 16 clips x 500 mel frames ('same' padding, dilations 1 and 5)
+    take the families and entries their measurements chose: LDS-DMA for all but the 256-channel
+    k = 11 convs (register-staged), the one-buffer-ring entries first where c_in is one stage."""
+    for d in (1, 5):
+        plan = plan_shapes(batch=16, length=length, c_in=channels, n_cols=channels,
+                           c_out=channels, taps=taps, dilation=d, left_pad=(taps - 1) * d // 2)
+        if channels == 256 and taps == 11:
+            assert plan.kernel == N.CONV_KERNEL_STAGED11
+            continue
+        assert plan.kernel == N.CONV_KERNEL_DMA
+        if channels == 256 and taps == 7:
+            assert plan.configs == DMA_LIST[7]
+        elif channels >= 128:
+            assert plan.configs == NARROW128_DMA_LIST[taps]
+        else:
+            assert plan.configs == NARROW_DMA_LIST[taps]
+        # 64 channels: the two-chunk one-stage entry (k = 3) or the 64-column entry follows the
+        # 32-column one-stage entry, which needs c_in = 32
+        assert plan.config == (2 if channels == 64 else 1)
+        assert plan.workgroups >= 256
