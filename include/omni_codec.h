@@ -209,8 +209,8 @@ int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
  *                                a multiple of 32, no weight2; taps 1, 2 or 7 with bf16 or E4M3
  *                                weights: a list of 4 per tap count (bf16 k = 7 at 128 columns:
  *                                1, at 64 or fewer: 3); taps 3 and 11 with bf16 weights at 64
- *                                columns or fewer (4 and 3), at a multiple of 128 columns (taps
- *                                3: 2) or at 128 (taps 11: 2)
+ *                                columns or fewer (4 and 3), at a multiple of 128 or of 96
+ *                                columns (taps 3: 2 each) or at 128 (taps 11: 2)
  *   OMNI_CONV_KERNEL_STAGED      register-staged, taps <= 7, any operand mode and weight dtype;
  *                                10 configurations
  *   OMNI_CONV_KERNEL_STAGED11    register-staged, taps <= 11, bf16 weights, x bf16; 10

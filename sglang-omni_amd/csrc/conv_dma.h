@@ -445,8 +445,8 @@ int launch_first_fit(const ConvParams& p, Choice& ch, hipStream_t stream) {
 int launch_dma_taps1(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps2(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
-// HiFiGAN's layers only (bf16 weights; n_cols <= 64, or a multiple of 128 for k = 3, or 128 for
-// k = 11): k = 3 and k = 11
+// HiFiGAN's layers only (bf16 weights; n_cols <= 64, or a multiple of 128 or 96 for k = 3, or 128
+// for k = 11): k = 3 and k = 11
 int launch_dma_taps3(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 int launch_dma_taps11(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stream);
 

@@ -36,6 +36,8 @@ DMA_LIST = {1: 4, 2: 4, 7: 4}
 NARROW_DMA_LIST = {3: 4, 7: 3, 11: 3}
 # and for its 128-channel stage (n_cols == 128; k = 3 also at 256 columns)
 NARROW128_DMA_LIST = {3: 2, 7: 1, 11: 2}
+# k = 3 at other multiples of 96 columns (192: the three phases of HiFiGAN's 128 -> 64 up conv)
+NARROW96_DMA_LIST = {3: 2}
 STAGED_LIST = 10
 STAGED11_LIST = 10
 FUSED_LIST = 3
@@ -176,14 +178,20 @@ def test_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, config, fp8):
         check_float64(forced, conv64(x.float().cpu(), w, b, dilation=packed.dilation))
 
 
-NARROW_CASES = [(taps, cols, k) for taps in (3, 7, 11) for cols in (256, 128, 64, 32)
-                if taps == 3 or cols != 256
-                for k in range(1, (NARROW128_DMA_LIST if cols > 64 else NARROW_DMA_LIST)[taps] + 1)]
+def _narrow_list(cols: int) -> dict:
+    if cols == 192:
+        return NARROW96_DMA_LIST
+    return NARROW128_DMA_LIST if cols > 64 else NARROW_DMA_LIST
+
+
+NARROW_CASES = [(taps, cols, k) for taps in (3, 7, 11) for cols in (256, 192, 128, 64, 32)
+                if taps == 3 or cols not in (256, 192)
+                for k in range(1, _narrow_list(cols)[taps] + 1)]
 
 
 @pytest.mark.parametrize("taps,cols,config", NARROW_CASES, ids=lambda v: str(v))
 def test_narrow_dma_tile_matches_float64_and_the_chosen_tile(gpu, taps, cols, config):
-    """HiFiGAN's ResBlock convs ('same' padding, dilation 5) at 256 (k = 3), 128, 64 and 32
+    """HiFiGAN's convs ('same' padding, dilation 5) at 256 and 192 (k = 3), 128, 64 and 32
     channels on their LDS-DMA tiles: each entry against the float64 conv and the size-chosen
     entry's bits."""
     gen = torch.Generator().manual_seed(1000 * taps + 10 * cols + config)
