@@ -251,7 +251,10 @@ int omni_conv1d_fused_with(const omni_conv_args* args, int kernel, int config,
  * history (k = 7), activation NONE, SNAKE or LEAKY_RELU; no weight2, residual, mix or sum_out;
  * c_in a multiple of 32 * k_splits. k_splits = 1 is omni_conv1d_fused. kernel / config as in
  * omni_conv1d_fused_with (OMNI_CONV_KERNEL_AUTO / 0, or OMNI_CONV_KERNEL_DMA and an entry of its
- * list).
+ * list). k_splits > 1 runs on the LDS-DMA family only: a call that none of its split tiles can
+ * hold (e.g. k = 7 over many rows of a few positions each, whose history rows overflow the
+ * tile's staged rows) returns OMNI_ERR_UNSUPPORTED before any launch and leaves out untouched;
+ * the caller then runs the conv unsplit (omni_conv1d_fused).
  */
 int omni_conv1d_splitk(const omni_conv_args* args, int64_t k_splits, float* workspace,
                        int64_t workspace_bytes, int kernel, int config, omni_stream_t stream);

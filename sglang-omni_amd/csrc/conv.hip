@@ -306,7 +306,10 @@ int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int
   Choice ch;
   ch.force = config;
   ch.launch = launch;
-  int family = kernel;
+  // only the LDS-DMA tiles write split-K partials: a split call no DMA tile fits is refused
+  // here, never handed to a family that would write the whole conv into out and leave the
+  // reduction summing partials nobody wrote
+  int family = k_splits > 1 ? OMNI_CONV_KERNEL_DMA : kernel;
   int r = dispatch(p, x_f32, fp8, fuse2, family, ch, reinterpret_cast<hipStream_t>(stream));
   if (r == OMNI_OK && launch && k_splits > 1) {
     const int quads = (int)(positions * a->n_cols / 4);

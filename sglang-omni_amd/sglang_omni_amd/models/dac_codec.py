@@ -115,6 +115,22 @@ def _snake_coefficients(alpha: torch.Tensor | dict[str, torch.Tensor],
     return a.to(device).contiguous(), (a + 1e-9).reciprocal().to(device).contiguous()
 
 
+# the attribute that marks an index tensor whose ids were checked distinct on the host, holding
+# the tensor's version counter at the check (an in-place write to the tensor voids the mark)
+_DISTINCT_MARK = "_omni_distinct_slots_version"
+
+
+def mark_distinct_slots(index: torch.Tensor) -> torch.Tensor:
+    """Mark ``index`` as holding distinct slot ids, checked by the caller on its host list, so
+    a decode step takes it without reading it back from the device."""
+    setattr(index, _DISTINCT_MARK, index._version)
+    return index
+
+
+def _marked_distinct(index: torch.Tensor) -> bool:
+    return getattr(index, _DISTINCT_MARK, None) == index._version
+
+
 class CodecStatePool:
     """Per-slot decoder state resident in HBM: for every causal conv with left context, a
     [slots, 2, context, C_in] bf16 pool (two copies, selected by the slot's parity), then
@@ -158,9 +174,12 @@ class CodecStatePool:
         if any(s < 0 or s >= total for s in slots):
             raise ValueError(f"slot ids must lie in [0, {total}): {slots}")
         if self.device.type != "cuda":
-            return torch.tensor(slots, dtype=torch.long, device=self.device)
-        return torch.tensor(slots, dtype=torch.long, pin_memory=True).to(self.device,
-                                                                          non_blocking=True)
+            index = torch.tensor(slots, dtype=torch.long, device=self.device)
+        else:
+            index = torch.tensor(slots, dtype=torch.long, pin_memory=True).to(self.device,
+                                                                               non_blocking=True)
+        mark_distinct_slots(index)
+        return index
 
     def zero_slots(self, slots: torch.Tensor) -> None:
         """Clear the slots' state (both copies) and parity."""
@@ -179,6 +198,9 @@ class _Workspace:
     # wide halo): they run as two launches
     unfused_blocks: set[int] = field(default_factory=set)
     front: dict[str, torch.Tensor] = field(default_factory=dict)  # a front's own buffers
+    # False once the split-K input conv was refused at this shape (many rows of a few frames:
+    # no split tile holds their history rows); the input conv then runs unsplit
+    in_conv_split: bool = True
 
 
 class DacCodecDecoder:
@@ -274,7 +296,9 @@ class DacCodecDecoder:
         # the input conv in K slices (omni_conv1d_splitk) with bf16 weights: at a streaming
         # step's few positions (64 streams x 12 frames) its unsplit tiles fill a quarter of the
         # GPU; the slice count is the layer's, never the batch's, so every decode of a stream
-        # sums alike (streamed == whole, bit for bit)
+        # sums alike (streamed == whole, bit for bit) wherever a split tile holds the step; a
+        # step of many rows of a few frames each, which none holds, runs the conv unsplit (the
+        # same values to float32 summation order)
         ic_conv = self.in_conv.conv
         self.in_conv_splits = (IN_CONV_SPLITS if ic_conv.scale is None and ic_conv.taps in (1, 7)
                                and ic_conv.c_in % (32 * IN_CONV_SPLITS) == 0 else 1)
@@ -364,11 +388,20 @@ class DacCodecDecoder:
         u = self._view(ws.u[cur], batch, length, self.in_conv.conv.n_cols)
         ic = self.in_conv
         with timer.launch("conv", 2.0 * batch * length * ic.conv.macs_per_position, ic.name):
-            if self.in_conv_splits > 1:
+            split = self.in_conv_splits > 1 and ws.in_conv_split
+            if split:
                 # the partials go to the residual-stream buffer, unused until the first up conv
-                splitk_conv(z, ic.conv, u, k_splits=self.in_conv_splits, workspace=ws.x,
-                            activation=snake, act_a=ic.out_a, act_b=ic.out_b, **hist(ic.name))
-            else:
+                try:
+                    splitk_conv(z, ic.conv, u, k_splits=self.in_conv_splits, workspace=ws.x,
+                                activation=snake, act_a=ic.out_a, act_b=ic.out_b,
+                                **hist(ic.name))
+                except N.OmniCodecError as err:
+                    # refused before any launch: nothing was written, so the unsplit conv
+                    # below runs on the same inputs and history
+                    if err.status != N.UNSUPPORTED:
+                        raise
+                    ws.in_conv_split = split = False
+            if not split:
                 fused_conv(z, ic.conv, u, activation=snake, act_a=ic.out_a, act_b=ic.out_b,
                            **hist(ic.name))
         for bi, blk in enumerate(self.blocks):
@@ -542,11 +575,13 @@ class DacCodecDecoder:
         return torch.cat(parts, dim=-1)
 
     def _check_distinct_slots(self, slot_index: torch.Tensor) -> None:
-        """Rows naming one slot twice would race on its history and parity: refuse them. The
-        check reads the index on the host once per index tensor (and again after any in-place
-        change to it); under graph capture it is the caller's (``CodecStatePool.stage_index``
-        and the graph runner check their host lists)."""
-        if torch.cuda.is_current_stream_capturing():
+        """Rows naming one slot twice would race on its history and parity: refuse them. An
+        index from ``CodecStatePool.stage_index`` (or marked by ``mark_distinct_slots``) was
+        checked on its host list and is taken as it is, so a serving step never waits for the
+        GPU; any other index is read back once per tensor (and again after an in-place change
+        to it). Under graph capture the check is the caller's (the graph runner checks its host
+        lists)."""
+        if _marked_distinct(slot_index) or torch.cuda.is_current_stream_capturing():
             return
         ref = self._checked_index
         if ref is not None and ref[0]() is slot_index and ref[1] == slot_index._version:

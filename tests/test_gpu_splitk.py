@@ -162,3 +162,66 @@ def test_k7_split_stream_in_chunks_equals_the_whole(gpu, splits):
     ref = causal_conv_snake_f64(x, w, b, alpha)
     err = (whole.cpu().double() - ref).abs().max().item()
     assert err <= 2 ** -7 * ref.abs().max().item()  # the bf16 output's rounding
+
+
+def test_a_split_no_tile_holds_is_refused_and_leaves_out_untouched(gpu):
+    """k = 7 over 64 rows of 5 positions: a 192-position split tile would stage 192 rows plus 40
+    row segments' 6-row halos (432 > 368 rows), so no split tile holds the call. It must come
+    back UNSUPPORTED before any launch, out untouched, never as another family's full conv
+    followed by a reduction of unwritten partials. k = 1 at 96 channels in 3 slices (one
+    32-channel chunk per slice, below every split tile's two) is refused the same way."""
+    batch, length, c_in, c_out = 64, 5, 512, 384
+    x, w, b, alpha = conv7_operands(batch, length, c_in, c_out, 40)
+    packed = pack_conv1d(w, b).to(gpu)
+    xg = x.to(gpu)
+    ws = torch.full((splitk_workspace_elements(xg, packed, 4),), 7.0, device=gpu)
+    out = torch.full((batch, length, c_out), -3.0, device=gpu)
+    a = alpha.to(gpu)
+    act = dict(activation=N.ACT_SNAKE, act_a=a, act_b=(a + 1e-9).reciprocal())
+    with pytest.raises(N.OmniCodecError) as err:
+        splitk_conv(xg, packed, out, k_splits=4, workspace=ws, **act)
+    assert err.value.status == N.UNSUPPORTED
+    lib = N.load_library()
+    status = lib.omni_conv1d_splitk_noalloc(ctypes.byref(_conv_args(xg, packed, out, **act)), 4,
+                                            N.CONV_KERNEL_AUTO, 0, N.stream_handle(gpu))
+    assert status == N.UNSUPPORTED
+    torch.cuda.synchronize()
+    assert bool((out == -3.0).all()) and bool((ws == 7.0).all())
+    # the unsplit conv serves the same call
+    from sglang_omni_amd.kernels.conv import fused_conv
+    fused_conv(xg, packed, out, **act)
+    ref = causal_conv_snake_f64(x, w, b, alpha)
+    torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5,
+                               atol=1e-5 * ref.abs().max().item())
+    x1, w1, b1 = operands(40, 96, 128, 41, gpu)
+    p1 = pack_conv1d(w1, b1).to(gpu)
+    out1 = torch.full((1, 40, 128), -3.0, device=gpu)
+    ws1 = torch.empty(splitk_workspace_elements(x1, p1, 3), device=gpu)
+    with pytest.raises(N.OmniCodecError) as err:
+        gemm(x1, p1, out1, k_splits=3, workspace=ws1)
+    assert err.value.status == N.UNSUPPORTED
+    torch.cuda.synchronize()
+    assert bool((out1 == -3.0).all())
+
+
+def test_the_decoder_runs_a_refused_input_conv_split_unsplit(gpu):
+    """The 24 kHz decoder's input conv (512 -> 1536, k = 7, 4 slices) over 64 rows of 5 frames,
+    a shape no split tile holds, through ``from_indices``: every row equals its own decode
+    (1 row, which the split tiles hold) to float32 summation order, so the unsplit fallback
+    ran (bf16 roundings of the two summation orders may differ, inside the decoders' 2e-3
+    bound); a refused split never hands its stale partials to the reduction."""
+    from sglang_omni_amd.models import DacCodecDecoder, make_dac_weights
+    from sglang_omni_amd.models.configs import CODEC_24K
+
+    decoder = DacCodecDecoder(make_dac_weights(CODEC_24K, seed=0), CODEC_24K, device=gpu)
+    assert decoder.in_conv_splits == 4
+    gen = torch.Generator().manual_seed(42)
+    codes = torch.randint(0, CODEC_24K.codebook_size, (64, CODEC_24K.n_codebooks, 5),
+                          generator=gen).to(gpu)
+    batched = decoder.from_indices(codes)
+    assert decoder._workspaces[(64, 5)].in_conv_split is False
+    for r in (0, 17, 63):
+        alone = decoder.from_indices(codes[r:r + 1])
+        assert decoder._workspaces[(1, 5)].in_conv_split is True
+        err = (batched[r] - alone[0]).abs().max().item()
+        assert err <= 2e-3, (r, err)
