@@ -5,8 +5,9 @@ Code2Wav scheduler (sglang_omni/models/qwen3_omni/components/code2wav_scheduler.
 
 * a stream takes a state slot with its first codes and gives it back (zeroed) when it ends or is
   aborted; when no slot is free it decodes each window from its codes with a left context of
-  ``context_frames`` (a whole decode whose leading samples are dropped), and a stream that ends
-  before its first full window decodes without slot state;
+  ``context_frames`` (a whole decode whose leading samples are dropped); a stream that ends
+  before its first full window still holds its slot and decodes its remainder as that slot's
+  first decode;
 * a window is ``window_frames`` new frames, or a finished stream's remainder;
 * a step decodes the windows of one group: first windows go before later ones (they carry their
   requests' time to first audio), then the longest-waiting window; the group is the ready windows
@@ -16,7 +17,10 @@ Code2Wav scheduler (sglang_omni/models/qwen3_omni/components/code2wav_scheduler.
   eagerly), their waveform staged toward the host in the same stream order, so a later replay
   cannot overwrite it first;
 * a failing step fails its participants only: each gets the error, its slot is released, and the
-  other streams continue (the runner disables its graphs itself when a replay raises).
+  other streams continue (the runner disables its graphs itself when a replay raises);
+* a step never waits for the GPU on the host: codes and slot ids go up from pinned memory
+  without blocking, the slot ids are checked distinct on the host, and the waveform leaves
+  through the egress ring (the host waits only for the step ``egress_depth`` steps older).
 """
 
 from __future__ import annotations
@@ -107,7 +111,7 @@ class CodecStepLoop:
             self._release(s.slot)
 
     def _release(self, slot: int) -> None:
-        self.pool.zero_slots(torch.tensor([slot], dtype=torch.long, device=self.pool.device))
+        self.pool.zero_slots(self.pool.stage_index([slot]))
         self.pool.release(slot)
 
     def _window(self, s: _Stream) -> int:
@@ -168,7 +172,7 @@ class CodecStepLoop:
             if group[0].windowed:
                 wave = self._decode_windowed(group, windows)
             else:
-                codes = torch.stack(windows).to(self.decoder.device)
+                codes = self._to_device(torch.stack(windows))
                 index = self.pool.stage_index([s.slot for s in group])
                 first = group[0].emitted == 0
                 if self.runner is not None:
@@ -201,9 +205,20 @@ class CodecStepLoop:
             rows.append(torch.cat([past, w], dim=1))
             keep = torch.cat([s.history, w], dim=1) if s.history is not None else w
             s.history = keep[:, max(0, keep.shape[1] - self.context_frames):]
-        codes = torch.stack(rows).to(self.decoder.device)
+        codes = self._to_device(torch.stack(rows))
         wave = self.decoder.from_indices(codes)
         return wave[..., ctx * self.hop:]
+
+    def _to_device(self, codes: torch.Tensor) -> torch.Tensor:
+        """The step's codes on the decoder's device; host codes go up through pinned memory
+        without blocking the host (the caching host allocator keeps the pinned block until the
+        copy has completed)."""
+        device = self.decoder.device
+        if codes.device == device or device.type != "cuda":
+            return codes.to(device)
+        if codes.device.type == "cpu":
+            codes = codes.pin_memory()
+        return codes.to(device, non_blocking=True)
 
     def _stage(self, ids: list[Hashable], wave: torch.Tensor) -> list[tuple[Hashable, np.ndarray]]:
         if self.egress is None:

@@ -15,7 +15,9 @@ before it. An entry's buffer grows only while the entry holds no transfer.
 
 A transfer that fails part-way leaves its buffer possibly still targeted by a copy that no event
 fences: that buffer is set aside for the life of the egress (never reused, never freed early) and
-every later step is copied synchronously. ``depth = 0`` copies every step synchronously.
+every later step is copied synchronously. Audio of older steps delivered while staging the failed
+step is kept and returned by the next ``poll`` or ``flush``. ``depth = 0`` copies every step
+synchronously.
 """
 
 from __future__ import annotations
@@ -66,6 +68,9 @@ class WaveformEgress:
         self.delivered = 0  # steps delivered so far (they leave in step order)
         self.overlapped = depth > 0  # False once a transfer failed: synchronous from then on
         self.set_aside: list[torch.Tensor] = []  # buffers a failed transfer may still target
+        # audio delivered while staging a step whose transfer then failed: returned first by the
+        # next poll / flush
+        self.carried: list[tuple[Hashable, np.ndarray]] = []
         self.wait_ns = 0  # host time spent waiting for copies
 
     @property
@@ -93,7 +98,7 @@ class WaveformEgress:
         ids = list(request_ids)
         step = self.steps
         if not self.overlapped:
-            delivered = self.flush()  # the steps still in flight leave first
+            delivered = self.flush()  # carried audio and the steps still in flight leave first
             host = packed.cpu()
             self.steps += 1
             self.delivered += 1
@@ -113,11 +118,13 @@ class WaveformEgress:
             entry.event.record(torch.cuda.current_stream(self.device))
         except Exception:
             # no event fences whatever part of the copy was enqueued: keep the buffer alive and
-            # out of the ring, and copy synchronously from now on
+            # out of the ring, and copy synchronously from now on; the older steps' audio
+            # delivered above waits for the next poll / flush
             self.set_aside.append(entry.host)
             entry.host = None
             entry.event = None
             self.overlapped = False
+            self.carried += delivered
             raise
         entry.step, entry.request_ids, entry.width, entry.counts = step, ids, width, counts
         self.steps += 1
@@ -135,7 +142,7 @@ class WaveformEgress:
     def poll(self) -> list[tuple[Hashable, np.ndarray]]:
         """The audio of the pending steps whose copies have completed, oldest first, without
         blocking (delivery stops at the first step still in flight)."""
-        out: list[tuple[Hashable, np.ndarray]] = []
+        out, self.carried = self.carried, []
         while self.in_flight:
             entry = self._entry_of(self.delivered)
             if not entry.event.query():
@@ -145,7 +152,8 @@ class WaveformEgress:
 
     def flush(self) -> list[tuple[Hashable, np.ndarray]]:
         """The audio of every pending step, waiting for their copies."""
-        return self._deliver_through(self.steps - 1) if self.in_flight else []
+        out, self.carried = self.carried, []
+        return out + (self._deliver_through(self.steps - 1) if self.in_flight else [])
 
     def _entry_of(self, step: int) -> _Entry:
         entry = self.ring[step % len(self.ring)]

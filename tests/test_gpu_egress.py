@@ -163,3 +163,23 @@ def test_a_failed_transfer_sets_its_buffer_aside_and_goes_synchronous(gpu, monke
     assert [rid for rid, _ in out] == ["x", "z"]
     assert np.array_equal(out[1][1].view(np.int32), w[2][0, 0].numpy().view(np.int32))
     assert egress.in_flight == 0
+
+
+def test_audio_delivered_before_a_failed_transfer_is_kept(gpu, monkeypatch):
+    """With one ring entry, staging step 1 first delivers step 0; when step 1's transfer then
+    fails (forced on the host: the entry's event refuses to record), step 0's audio is not
+    lost: the next poll returns it."""
+    egress = WaveformEgress(gpu, depth=1)
+    w = [_wave(2, 96, 30 + k) for k in range(2)]
+    assert egress.stage_step(["a0", "b0"], w[0].to(gpu)) == []
+
+    def refuse(stream=None):
+        raise RuntimeError("record refused")
+
+    monkeypatch.setattr(egress.ring[0].event, "record", refuse)
+    with pytest.raises(RuntimeError, match="record refused"):
+        egress.stage_step(["a1", "b1"], w[1].to(gpu))
+    out = egress.poll()
+    assert [rid for rid, _ in out] == ["a0", "b0"]
+    assert np.array_equal(out[1][1].view(np.int32), w[0][1, 0].numpy().view(np.int32))
+    assert egress.poll() == [] and egress.flush() == []
