@@ -188,18 +188,28 @@ def _upsample(x: torch.Tensor, conv: dict[str, Any], stride: int, padding: str) 
                               padding=math.ceil(stride / 2))
 
 
+def residual_trim(x: torch.Tensor, length: int, padding: str = "causal") -> torch.Tensor:
+    """x cut to the ``length`` samples a residual unit's branch returned (modded_dac.py:633-640):
+    with pad = x's length - length > 0, the causal unit keeps x's first ``length`` samples
+    (``x[..., :-pad]``) and the non-causal one drops floor(pad / 2) samples on the left and
+    ceil(pad / 2) on the right (``x[..., pad // 2 : -pad // 2]``); pad <= 0 keeps x."""
+    pad = x.shape[-1] - length
+    if pad <= 0:
+        return x
+    if padding == "causal":
+        return x[..., :x.shape[-1] - pad]
+    return x[..., pad // 2: x.shape[-1] - (pad - pad // 2)]
+
+
 def residual_unit(x: torch.Tensor, unit: dict[str, Any], padding: str = "causal") -> torch.Tensor:
-    """``ResidualUnit.forward``: x + conv1x1(Snake(conv7_d(Snake(x)))). When the convs return
-    fewer samples than x, x is trimmed on the left (causal) or on both sides (modded_dac.py:
-    619-642); both padding modes keep the length here, so nothing is trimmed."""
+    """``ResidualUnit.forward``: x + conv1x1(Snake(conv7_d(Snake(x)))), x cut to the branch's
+    length by ``residual_trim`` when the convs return fewer samples (modded_dac.py:619-642; with
+    the reference's k = 7 convs both padding modes keep the length, so nothing is cut)."""
     y = snake(x, unit["alpha1"])
     y = _conv(y, unit["conv1"], unit["dilation"], padding)
     y = snake(y, unit["alpha2"])
     y = _conv(y, unit["conv2"], 1, padding)
-    trim = x.shape[-1] - y.shape[-1]
-    if trim > 0:
-        x = x[..., trim:] if padding == "causal" else x[..., trim // 2: x.shape[-1] - trim // 2]
-    return x + y
+    return residual_trim(x, y.shape[-1], padding) + y
 
 
 def decoder_block(x: torch.Tensor, block: dict[str, Any], padding: str = "causal") -> torch.Tensor:

@@ -22,10 +22,14 @@ Parity pins (``tests/test_qwen3_code2wav_oracle.py``):
 * ``apply_rope`` against the complex-rotation form of rotary embeddings (pairs (i, i + d/2));
 * ``first_decode_samples`` against the length of the transformers module's output.
 * ``qwen3_tts_decode`` (the Qwen3-TTS tokenizer decoder; its module, ``qwen_tts``, is not
-  installed, so the composition is parity unpinned beyond its pieces): its transformer with
-  identity input / output projections equals ``code2wav_transformer``; ``split_rvq_decode``
-  against a per-frame loop; right-trimmed transposed convs against the reference test's own
-  module form (tests/unit_test/qwen3_tts/test_incremental_codec.py:93-110); T * hop samples.
+  installed): the whole composition, run with the layer kinds of the reference test's pure-torch
+  stand-in decoder injected (``DecoderPieces``), equals that stand-in
+  (tests/unit_test/qwen3_tts/test_incremental_codec.py:68-306, restated in
+  ``tests/test_qwen3_tts_decode_pin.py``) to 1e-12 in float64, and a dropped pre_conv,
+  output_proj or final norm, misordered upsamplers, a missing clamp, rotary or window each fail
+  that pin; its transformer with identity input / output projections equals
+  ``code2wav_transformer``; ``split_rvq_decode`` against a per-frame loop; right-trimmed
+  transposed convs against the reference test's own module form (:93-110); T * hop samples.
 
 The reference's streaming semantics (sglang_omni/models/qwen3_omni/components/
 incremental_codec.py:109-200: a stream decoded in any split of chunks gives the whole decode's
@@ -35,7 +39,8 @@ samples) need no second oracle: the GPU tests check the streamed decode against 
 from __future__ import annotations
 
 import math
-from typing import Any
+from dataclasses import dataclass
+from typing import Any, Callable
 
 import torch
 import torch.nn.functional as F
@@ -43,10 +48,16 @@ import torch.nn.functional as F
 TF_FILE = "TF/models/qwen3_omni_moe/modeling_qwen3_omni_moe.py"
 
 
+def _f(t: torch.Tensor) -> torch.Tensor:
+    """The oracle's working precision: float32, or float64 for float64 inputs and weights (the
+    pins that compare compositions run it in float64)."""
+    return t if t.dtype == torch.float64 else t.float()
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """x / sqrt(mean(x^2) + eps) * weight over the last dimension (TF :3356-3373)."""
-    xf = x.float()
-    return weight.float() * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps))
+    xf = _f(x)
+    return _f(weight) * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps))
 
 
 def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float) -> tuple[torch.Tensor, torch.Tensor]:
@@ -75,25 +86,67 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: 
     qpos = torch.arange(tq)[:, None] + q_offset
     kpos = torch.arange(tk)[None, :]
     allowed = (kpos <= qpos) & (qpos - kpos < window)
-    scores = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) * scale
+    scores = torch.matmul(_f(q), _f(k).transpose(-1, -2).contiguous()) * scale
     scores = scores.masked_fill(~allowed, float("-inf"))
-    return torch.matmul(torch.softmax(scores, dim=-1), v.float())
+    return torch.matmul(torch.softmax(scores, dim=-1), _f(v))
+
+
+def swiglu_mlp(x: torch.Tensor, w: dict[str, torch.Tensor], prefix: str) -> torch.Tensor:
+    """down(silu(gate(x)) * up(x)), no biases (TF :3380-3388)."""
+    gate = F.linear(x, _f(w[f"{prefix}.gate_proj.weight"]))
+    up = F.linear(x, _f(w[f"{prefix}.up_proj.weight"]))
+    return F.linear(F.silu(gate) * up, _f(w[f"{prefix}.down_proj.weight"]))
+
+
+@dataclass(frozen=True)
+class DecoderPieces:
+    """The layer kinds the code2wav / Qwen3-TTS decoder compositions below are built from, each
+    a function of the weights under its module's state name. The defaults are the real decoders'
+    (RMSNorm, SwiGLU, LayerScale, default rotary, SnakeBeta, ConvNeXt LayerNorm eps 1e-6, clamp
+    to [-1, 1]); a test swaps in other kinds (LayerNorm, a GELU MLP, tanh ...) to hold the same
+    composition against another module that composes those kinds the same way.
+
+    * ``norm(h, w, prefix, cfg)``: the norms ``...input_layernorm``, ``...post_attention_
+      layernorm`` and ``pre_transformer.norm``;
+    * ``mlp(h, w, prefix)``: ``...mlp``;
+    * ``layer_scale(a, w, prefix)``: ``...self_attn_layer_scale`` / ``...mlp_layer_scale``;
+    * ``rope(positions, head_dim, cfg)``: the (cos, sin) tables;
+    * ``act(x, w, prefix)``: every activation of the conv stack (``decoder.{i}.block.0``,
+      ``...act1``, ``...act2``, ``decoder.{n+1}``), x [B, C, L];
+    * ``quantize(codes, w, cfg)``: the Qwen3-TTS codes -> latents [B, latent, T];
+    * ``convnext_eps``: the ConvNeXt blocks' LayerNorm epsilon;
+    * ``clamp(x)``: the waveform's final nonlinearity.
+    """
+
+    norm: Callable[..., torch.Tensor] = lambda h, w, prefix, cfg: rms_norm(
+        h, w[f"{prefix}.weight"], cfg.rms_norm_eps)
+    mlp: Callable[..., torch.Tensor] = swiglu_mlp
+    layer_scale: Callable[..., torch.Tensor] = lambda a, w, prefix: _f(w[f"{prefix}.scale"]) * a
+    rope: Callable[..., tuple[torch.Tensor, torch.Tensor]] = lambda positions, hd, cfg: rope_cos_sin(
+        positions, hd, cfg.rope_theta)
+    act: Callable[..., torch.Tensor] = lambda x, w, prefix: snake_beta(
+        x, w[f"{prefix}.alpha"], w[f"{prefix}.beta"])
+    quantize: Callable[..., torch.Tensor] = lambda codes, w, cfg: split_rvq_decode(
+        codes, w, cfg).transpose(1, 2)
+    convnext_eps: float = 1e-6
+    clamp: Callable[[torch.Tensor], torch.Tensor] = lambda x: x.clamp(-1.0, 1.0)
 
 
 def transformer_layer(h: torch.Tensor, w: dict[str, torch.Tensor], prefix: str, cfg: Any,
-                      cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+                      cos: torch.Tensor, sin: torch.Tensor,
+                      pieces: "DecoderPieces | None" = None) -> torch.Tensor:
     """One pre-transformer layer on h [B, T, C] (TF :3391-3451): RMSNorm -> q/k/v -> rotary ->
     window attention -> o -> layer scale + residual; RMSNorm -> SwiGLU MLP -> layer scale +
     residual."""
+    pieces = pieces or DecoderPieces()
     b, t, c = h.shape
     heads = cfg.num_attention_heads
     kv_heads = cfg.num_key_value_heads
     hd = getattr(cfg, "head_dim", c // heads)
-    eps = cfg.rms_norm_eps
-    x = rms_norm(h, w[f"{prefix}.input_layernorm.weight"], eps)
-    q = F.linear(x, w[f"{prefix}.self_attn.q_proj.weight"].float()).view(b, t, heads, hd)
-    k = F.linear(x, w[f"{prefix}.self_attn.k_proj.weight"].float()).view(b, t, kv_heads, hd)
-    v = F.linear(x, w[f"{prefix}.self_attn.v_proj.weight"].float()).view(b, t, kv_heads, hd)
+    x = pieces.norm(h, w, f"{prefix}.input_layernorm", cfg)
+    q = F.linear(x, _f(w[f"{prefix}.self_attn.q_proj.weight"])).view(b, t, heads, hd)
+    k = F.linear(x, _f(w[f"{prefix}.self_attn.k_proj.weight"])).view(b, t, kv_heads, hd)
+    v = F.linear(x, _f(w[f"{prefix}.self_attn.v_proj.weight"])).view(b, t, kv_heads, hd)
     q = apply_rope(q.transpose(1, 2), cos, sin)
     k = apply_rope(k.transpose(1, 2), cos, sin)
     v = v.transpose(1, 2)
@@ -102,22 +155,23 @@ def transformer_layer(h: torch.Tensor, w: dict[str, torch.Tensor], prefix: str, 
         v = v.repeat_interleave(heads // kv_heads, dim=1)
     a = window_attention(q, k, v, cfg.sliding_window, hd ** -0.5)
     a = F.linear(a.transpose(1, 2).reshape(b, t, heads * hd),
-                 w[f"{prefix}.self_attn.o_proj.weight"].float())
-    h = h + w[f"{prefix}.self_attn_layer_scale.scale"].float() * a
-    x = rms_norm(h, w[f"{prefix}.post_attention_layernorm.weight"], eps)
-    gate = F.linear(x, w[f"{prefix}.mlp.gate_proj.weight"].float())
-    up = F.linear(x, w[f"{prefix}.mlp.up_proj.weight"].float())
-    m = F.linear(F.silu(gate) * up, w[f"{prefix}.mlp.down_proj.weight"].float())
-    return h + w[f"{prefix}.mlp_layer_scale.scale"].float() * m
+                 _f(w[f"{prefix}.self_attn.o_proj.weight"]))
+    h = h + pieces.layer_scale(a, w, f"{prefix}.self_attn_layer_scale")
+    x = pieces.norm(h, w, f"{prefix}.post_attention_layernorm", cfg)
+    m = pieces.mlp(x, w, f"{prefix}.mlp")
+    return h + pieces.layer_scale(m, w, f"{prefix}.mlp_layer_scale")
 
 
-def code2wav_transformer(h: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
-    """The pre-transformer on inputs_embeds [B, T, C] at positions 0..T-1 (TF :3484-3539)."""
+def code2wav_transformer(h: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any,
+                         pieces: "DecoderPieces | None" = None) -> torch.Tensor:
+    """The pre-transformer on inputs_embeds [B, T, C] at positions 0..T-1 (TF :3484-3539):
+    its layers, then the final norm."""
+    pieces = pieces or DecoderPieces()
     hd = getattr(cfg, "head_dim", cfg.hidden_size // cfg.num_attention_heads)
-    cos, sin = rope_cos_sin(torch.arange(h.shape[1]), hd, cfg.rope_theta)
+    cos, sin = pieces.rope(torch.arange(h.shape[1]), hd, cfg)
     for i in range(cfg.num_hidden_layers):
-        h = transformer_layer(h, w, f"pre_transformer.layers.{i}", cfg, cos, sin)
-    return rms_norm(h, w["pre_transformer.norm.weight"], cfg.rms_norm_eps)
+        h = transformer_layer(h, w, f"pre_transformer.layers.{i}", cfg, cos, sin, pieces)
+    return pieces.norm(h, w, "pre_transformer.norm", cfg)
 
 
 def causal_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, *,
@@ -125,8 +179,8 @@ def causal_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None
     """Qwen3OmniMoeCausalConvNet at stride 1 (TF :3180-3213): (k-1)*d zeros on the left, none
     on the right (the extra padding is 0 at stride 1)."""
     k = weight.shape[-1]
-    xp = F.pad(x.float(), ((k - 1) * dilation, 0))
-    return F.conv1d(xp, weight.float(), None if bias is None else bias.float(),
+    xp = F.pad(_f(x), ((k - 1) * dilation, 0))
+    return F.conv1d(xp, _f(weight), None if bias is None else _f(bias),
                     dilation=dilation, groups=groups)
 
 
@@ -135,68 +189,89 @@ def causal_trans_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
     """Qwen3OmniMoeCausalTransConvNet (TF :3216-3228): ConvTranspose1d, then k - s samples
     trimmed on both sides; with trim "right" the Qwen3-TTS tokenizer's form, k - s trimmed on the
     right only (right_pad, qwen3_tts/incremental_codec.py:191-237 emits T * s samples)."""
-    y = F.conv_transpose1d(x.float(), weight.float(), bias.float(), stride=stride)
+    y = F.conv_transpose1d(_f(x), _f(weight), _f(bias), stride=stride)
     pad = weight.shape[-1] - stride
     if trim == "right":
         return y[..., :y.shape[-1] - pad]
     return y[..., pad:y.shape[-1] - pad]
 
 
-def convnext_block(x: torch.Tensor, w: dict[str, torch.Tensor], prefix: str) -> torch.Tensor:
+def convnext_block(x: torch.Tensor, w: dict[str, torch.Tensor], prefix: str,
+                   eps: float = 1e-6) -> torch.Tensor:
     """Qwen3OmniMoeConvNeXtBlock (TF :3231-3264) on [B, C, L]: depthwise causal conv k7 ->
-    LayerNorm(eps 1e-6) -> Linear 4C -> GELU (erf) -> Linear C -> gamma -> + input."""
+    LayerNorm(eps, 1e-6 in the real decoders) -> Linear 4C -> GELU (erf) -> Linear C -> gamma
+    -> + input."""
     c = x.shape[1]
     y = causal_conv(x, w[f"{prefix}.dwconv.conv.weight"], w[f"{prefix}.dwconv.conv.bias"],
                     groups=c)
-    y = F.layer_norm(y.transpose(1, 2), (c,), w[f"{prefix}.norm.weight"].float(),
-                     w[f"{prefix}.norm.bias"].float(), eps=1e-6)
-    y = F.linear(y, w[f"{prefix}.pwconv1.weight"].float(), w[f"{prefix}.pwconv1.bias"].float())
+    y = F.layer_norm(y.transpose(1, 2), (c,), _f(w[f"{prefix}.norm.weight"]),
+                     _f(w[f"{prefix}.norm.bias"]), eps=eps)
+    y = F.linear(y, _f(w[f"{prefix}.pwconv1.weight"]), _f(w[f"{prefix}.pwconv1.bias"]))
     y = F.gelu(y)
-    y = F.linear(y, w[f"{prefix}.pwconv2.weight"].float(), w[f"{prefix}.pwconv2.bias"].float())
-    y = w[f"{prefix}.gamma"].float() * y
-    return x.float() + y.transpose(1, 2)
+    y = F.linear(y, _f(w[f"{prefix}.pwconv2.weight"]), _f(w[f"{prefix}.pwconv2.bias"]))
+    y = _f(w[f"{prefix}.gamma"]) * y
+    return _f(x) + y.transpose(1, 2)
 
 
 def snake_beta(x: torch.Tensor, alpha: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:
     """x + (exp(beta) + 1e-9)^-1 * sin(exp(alpha) * x)^2 per channel (TF :3566-3581)."""
-    a = torch.exp(alpha.float()).view(1, -1, 1)
-    inv_b = 1.0 / (torch.exp(beta.float()).view(1, -1, 1) + 1e-9)
+    a = torch.exp(_f(alpha)).view(1, -1, 1)
+    inv_b = 1.0 / (torch.exp(_f(beta)).view(1, -1, 1) + 1e-9)
     return x + inv_b * torch.sin(x * a).pow(2)
 
 
-def code2wav_conv_stack(h: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
+def code2wav_upsample(x: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any,
+                      pieces: "DecoderPieces | None" = None) -> torch.Tensor:
+    """The upsamplers on x [B, C, T] (TF :3677-3679): per ratio, a causal transposed conv
+    (stride = kernel = ratio), then a ConvNeXt block."""
+    pieces = pieces or DecoderPieces()
+    trim = getattr(cfg, "transconv_trim", "both")
+    for i, factor in enumerate(cfg.upsampling_ratios):
+        x = causal_trans_conv(x, w[f"upsample.{i}.0.conv.weight"], w[f"upsample.{i}.0.conv.bias"],
+                              factor, trim)
+        x = convnext_block(x, w, f"upsample.{i}.1", pieces.convnext_eps)
+    return x
+
+
+def code2wav_decoder(x: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any,
+                     pieces: "DecoderPieces | None" = None) -> torch.Tensor:
+    """The decoder (TF :3680-3684) on x [B, C, L], before the clamp: conv k7, then per block an
+    activation -> causal transposed conv -> residual units (act -> conv k7 dilation 1/3/9 ->
+    act -> conv k1, + input), then an activation -> conv to one channel."""
+    pieces = pieces or DecoderPieces()
+    trim = getattr(cfg, "transconv_trim", "both")
+    x = causal_conv(x, w["decoder.0.conv.weight"], w["decoder.0.conv.bias"])
+    for bi, rate in enumerate(cfg.upsample_rates, start=1):
+        p = f"decoder.{bi}.block"
+        x = pieces.act(x, w, f"{p}.0")
+        x = causal_trans_conv(x, w[f"{p}.1.conv.weight"], w[f"{p}.1.conv.bias"], rate, trim)
+        for u, d in enumerate((1, 3, 9)):
+            q = f"{p}.{u + 2}"
+            y = pieces.act(x, w, f"{q}.act1")
+            y = causal_conv(y, w[f"{q}.conv1.conv.weight"], w[f"{q}.conv1.conv.bias"], dilation=d)
+            y = pieces.act(y, w, f"{q}.act2")
+            y = causal_conv(y, w[f"{q}.conv2.conv.weight"], w[f"{q}.conv2.conv.bias"])
+            x = x + y
+    n = len(cfg.upsample_rates)
+    x = pieces.act(x, w, f"decoder.{n + 1}")
+    return causal_conv(x, w[f"decoder.{n + 2}.conv.weight"], w[f"decoder.{n + 2}.conv.bias"])
+
+
+def code2wav_conv_stack(h: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any,
+                        pieces: "DecoderPieces | None" = None) -> torch.Tensor:
     """Everything after the pre-transformer (TF :3677-3684) on h [B, T, C]: the ConvNeXt
     upsamplers, the decoder blocks (SnakeBeta -> causal transposed conv -> residual units of
     SnakeBeta -> conv k7 dilation 1/3/9 -> SnakeBeta -> conv k1, + input), the final SnakeBeta
     -> conv to one channel, clamp to [-1, 1]. Returns [B, 1, samples]."""
-    trim = getattr(cfg, "transconv_trim", "both")
-    x = h.float().transpose(1, 2)
-    for i, factor in enumerate(cfg.upsampling_ratios):
-        x = causal_trans_conv(x, w[f"upsample.{i}.0.conv.weight"], w[f"upsample.{i}.0.conv.bias"],
-                              factor, trim)
-        x = convnext_block(x, w, f"upsample.{i}.1")
-    x = causal_conv(x, w["decoder.0.conv.weight"], w["decoder.0.conv.bias"])
-    for bi, rate in enumerate(cfg.upsample_rates, start=1):
-        p = f"decoder.{bi}.block"
-        x = snake_beta(x, w[f"{p}.0.alpha"], w[f"{p}.0.beta"])
-        x = causal_trans_conv(x, w[f"{p}.1.conv.weight"], w[f"{p}.1.conv.bias"], rate, trim)
-        for u, d in enumerate((1, 3, 9)):
-            q = f"{p}.{u + 2}"
-            y = snake_beta(x, w[f"{q}.act1.alpha"], w[f"{q}.act1.beta"])
-            y = causal_conv(y, w[f"{q}.conv1.conv.weight"], w[f"{q}.conv1.conv.bias"], dilation=d)
-            y = snake_beta(y, w[f"{q}.act2.alpha"], w[f"{q}.act2.beta"])
-            y = causal_conv(y, w[f"{q}.conv2.conv.weight"], w[f"{q}.conv2.conv.bias"])
-            x = x + y
-    n = len(cfg.upsample_rates)
-    x = snake_beta(x, w[f"decoder.{n + 1}.alpha"], w[f"decoder.{n + 1}.beta"])
-    x = causal_conv(x, w[f"decoder.{n + 2}.conv.weight"], w[f"decoder.{n + 2}.conv.bias"])
-    return x.clamp(-1.0, 1.0)
+    pieces = pieces or DecoderPieces()
+    x = code2wav_upsample(_f(h).transpose(1, 2), w, cfg, pieces)
+    return pieces.clamp(code2wav_decoder(x, w, cfg, pieces))
 
 
 def code_embedding_mean(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
     """code_embedding(codes + q * codebook_size).mean(1) (TF :3675): [B, Q, T] -> [B, T, C]."""
     offset = torch.arange(cfg.num_quantizers).view(1, -1, 1) * cfg.codebook_size
-    return F.embedding(codes + offset, w["code_embedding.weight"].float()).mean(1)
+    return F.embedding(codes + offset, _f(w["code_embedding.weight"])).mean(1)
 
 
 def qwen3_code2wav(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
@@ -222,23 +297,37 @@ def split_rvq_decode(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) 
     return out
 
 
-def qwen3_tts_decode(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any) -> torch.Tensor:
+def tts_pre_conv(z: torch.Tensor, w: dict[str, torch.Tensor]) -> torch.Tensor:
+    """The tokenizer decoder's causal ``pre_conv`` on the latents [B, latent, T]."""
+    return causal_conv(z, w["pre_conv.conv.weight"], w["pre_conv.conv.bias"])
+
+
+def tts_transformer(z: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any,
+                    pieces: "DecoderPieces | None" = None) -> torch.Tensor:
+    """The tokenizer decoder's pre-transformer on z [B, T, latent] (the reference's
+    ``incremental_transformer``, qwen3_tts/incremental_codec.py:533-576, over a whole stream):
+    input_proj -> layers -> norm -> output_proj. Returns [B, T, latent]."""
+    h = F.linear(z, _f(w["pre_transformer.input_proj.weight"]),
+                 _f(w["pre_transformer.input_proj.bias"]))
+    h = code2wav_transformer(h, w, cfg, pieces)
+    return F.linear(h, _f(w["pre_transformer.output_proj.weight"]),
+                    _f(w["pre_transformer.output_proj.bias"]))
+
+
+def qwen3_tts_decode(codes: torch.Tensor, w: dict[str, torch.Tensor], cfg: Any,
+                     pieces: "DecoderPieces | None" = None) -> torch.Tensor:
     """The Qwen3-TTS tokenizer decoder's whole-stream decode as the reference's incremental
-    decoder composes it (qwen3_tts/incremental_codec.py:1136-1276): split RVQ -> causal pre_conv
-    -> input_proj -> pre-transformer layers -> RMSNorm -> output_proj -> the conv stack with
-    right-trimmed transposed convs -> clamp. [B, Q, T] -> [B, 1, T * hop]."""
-    z = split_rvq_decode(codes, w, cfg).float().transpose(1, 2)
-    z = causal_conv(z, w["pre_conv.conv.weight"], w["pre_conv.conv.bias"]).transpose(1, 2)
-    h = F.linear(z, w["pre_transformer.input_proj.weight"].float(),
-                 w["pre_transformer.input_proj.bias"].float())
-    hd = cfg.head_dim
-    cos, sin = rope_cos_sin(torch.arange(h.shape[1]), hd, cfg.rope_theta)
-    for i in range(cfg.num_hidden_layers):
-        h = transformer_layer(h, w, f"pre_transformer.layers.{i}", cfg, cos, sin)
-    h = rms_norm(h, w["pre_transformer.norm.weight"], cfg.rms_norm_eps)
-    h = F.linear(h, w["pre_transformer.output_proj.weight"].float(),
-                 w["pre_transformer.output_proj.bias"].float())
-    return code2wav_conv_stack(h, w, cfg)
+    decoder composes it (``frame_tensors`` then ``conv_stack_tensors``, qwen3_tts/
+    incremental_codec.py:1151-1276): quantizer decode -> causal pre_conv -> pre-transformer
+    (input_proj -> layers -> norm -> output_proj) -> the upsamplers (right-trimmed transposed
+    conv -> ConvNeXt) -> the decoder (conv, blocks, activation, conv to one channel) -> clamp.
+    [B, Q, T] -> [B, 1, T * hop], in float64 when the weights are float64."""
+    pieces = pieces or DecoderPieces()
+    dt = torch.float64 if w["pre_conv.conv.weight"].dtype == torch.float64 else torch.float32
+    z = tts_pre_conv(pieces.quantize(codes, w, cfg).to(dt), w)
+    h = tts_transformer(z.transpose(1, 2), w, cfg, pieces)
+    x = code2wav_upsample(h.transpose(1, 2), w, cfg, pieces)
+    return pieces.clamp(code2wav_decoder(x, w, cfg, pieces))
 
 
 def total_upsample(cfg: Any) -> int:

@@ -300,6 +300,33 @@ def test_the_residual_unit_pin_rejects_the_conv_before_snake_order():
     assert not torch.allclose(swapped, expected, atol=1e-3)
 
 
+@pytest.mark.parametrize("pad", [1, 2, 3, 4, 5])
+def test_residual_trim_known_answers(pad):
+    """modded_dac.py:633-640: a causal unit keeps x's first L - pad samples (``x[..., :-pad]``);
+    a non-causal one centres them, floor(pad / 2) dropped on the left and ceil(pad / 2) on the
+    right (``x[..., pad // 2 : -pad // 2]``)."""
+    x = torch.arange(20.0).view(1, 1, 20)
+    assert O.residual_trim(x, 20 - pad, "causal").flatten().tolist() == list(range(20 - pad))
+    assert O.residual_trim(x, 20 - pad, "same").flatten().tolist() == \
+        list(range(pad // 2, 20 - (pad + 1) // 2))
+    assert O.residual_trim(x, 20, "causal") is x and O.residual_trim(x, 20, "same") is x
+
+
+def test_residual_unit_cuts_x_to_a_shorter_branch():
+    """A non-causal unit whose k = 6 conv returns one sample fewer than x adds the branch to
+    x[..., :-1] (pad 1: x[..., 0 : -1]), the branch evaluated here with plain conv1d."""
+    gen = torch.Generator().manual_seed(61)
+    unit = _unit(gen, 4, 1)
+    unit["conv1"]["weight"] = torch.randn(4, 4, 6, generator=gen) * 0.2
+    x = torch.randn(1, 4, 21, generator=gen)
+    y = O.snake(x, unit["alpha1"])
+    y = F.conv1d(y, unit["conv1"]["weight"], unit["conv1"]["bias"], padding=2)
+    y = O.snake(y, unit["alpha2"])
+    y = F.conv1d(y, unit["conv2"]["weight"], unit["conv2"]["bias"])
+    assert y.shape[-1] == 20
+    torch.testing.assert_close(O.residual_unit(x, unit, "same"), x[..., :20] + y)
+
+
 def test_decoder_block_matches_the_qwen3_block_up_to_the_trim():
     from transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe import (
         Qwen3OmniMoeCode2WavConfig,
