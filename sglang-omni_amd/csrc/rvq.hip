@@ -2,11 +2,16 @@
 //
 // Bandwidth-bound: every frame reads K table rows of D elements, its K codes and writes one
 // D-element row. One wave per frame covers D in 16-byte pieces (8 bf16 or 4 fp32 per lane per
-// piece). The codes of a frame are loaded once, one per lane, and broadcast across the wave with
-// a cross-lane read, so each table row is a fully coalesced 16-byte-per-lane load. All K row loads
-// of a frame are issued before the first add (K <= 64 is unrolled in groups of 8), keeping enough
-// bytes in flight per CU to cover HBM latency; the adds then run strictly in k order, so float32
-// results are bit-identical to the sequential sum the reference computes.
+// piece), so each table row is a fully coalesced 16-byte-per-lane load; the adds run strictly in
+// k order, so float32 results are bit-identical to the sequential sum the reference computes.
+//
+// K <= 32 and at most 8192 frames (every codec's decode step here): rvq_gather_frame_kernel, one
+// 64-thread workgroup per frame, so a decode step's few hundred frames spread over every CU. Lane k
+// loads codebook k's code (one round trip for all K), the row indices are broadcast by cross-lane
+// reads, and every one of the K row loads is in flight (raw 16-byte pieces held in registers)
+// before the first add: a frame costs two dependent memory round trips (codes, rows) and the
+// store. Larger K or batches: rvq_gather_sum_kernel, four frames per workgroup, the rows loaded
+// eight at a time (many waves cover the latency there).
 #include "common.h"
 
 namespace {
@@ -21,6 +26,45 @@ __device__ __forceinline__ int64_t load_code(const CodeT* codes, int64_t idx) {
 
 __device__ __forceinline__ float4 load_row4_f32(const float* p) {
   return *reinterpret_cast<const float4*>(p);
+}
+
+// Store one lane's VEC sums at element d0 of the output row starting at element row_off: bf16
+// (rounded to nearest even) or float32, 16 / 8-byte stores when the row is contiguous.
+template <int VEC, bool OUT_BF16>
+__device__ __forceinline__ void store_piece(const float* acc, void* __restrict__ out,
+                                            int64_t row_off, int64_t d0, int64_t os_d) {
+  if (OUT_BF16) {
+    u16* o = reinterpret_cast<u16*>(out) + row_off;
+    if (os_d == 1) {
+      u16 h[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) h[e] = float_to_bits_bf16(acc[e]);
+      if constexpr (VEC == 8) {
+        uint4 v;
+        v.x = h[0] | ((uint32_t)h[1] << 16);
+        v.y = h[2] | ((uint32_t)h[3] << 16);
+        v.z = h[4] | ((uint32_t)h[5] << 16);
+        v.w = h[6] | ((uint32_t)h[7] << 16);
+        *reinterpret_cast<uint4*>(o + d0) = v;
+      } else {
+        uint2 v;
+        v.x = h[0] | ((uint32_t)h[1] << 16);
+        v.y = h[2] | ((uint32_t)h[3] << 16);
+        *reinterpret_cast<uint2*>(o + d0) = v;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[(d0 + e) * os_d] = float_to_bits_bf16(acc[e]);
+    }
+  } else {
+    float* o = reinterpret_cast<float*>(out) + row_off;
+    if (os_d == 1 && VEC == 4) {
+      *reinterpret_cast<float4*>(o + d0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[(d0 + e) * os_d] = acc[e];
+    }
+  }
 }
 
 // TableT = float (4 elements / 16 B) or u16 bf16 bits (8 elements / 16 B).
@@ -97,41 +141,96 @@ __global__ void __launch_bounds__(256) rvq_gather_sum_kernel(
       for (int e = 0; e < VEC; ++e) acc[e] = acc[e] / kf;
     }
     if (!in_row) continue;
-    const int64_t d0 = piece * VEC;
-    if (OUT_BF16) {
-      u16* o = reinterpret_cast<u16*>(out) + b * os_b + t * os_t;
-      if (os_d == 1) {
-        u16 h[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) h[e] = float_to_bits_bf16(acc[e]);
-        if constexpr (VEC == 8) {
-          uint4 v;
-          v.x = h[0] | ((uint32_t)h[1] << 16);
-          v.y = h[2] | ((uint32_t)h[3] << 16);
-          v.z = h[4] | ((uint32_t)h[5] << 16);
-          v.w = h[6] | ((uint32_t)h[7] << 16);
-          *reinterpret_cast<uint4*>(o + d0) = v;
-        } else {
-          uint2 v;
-          v.x = h[0] | ((uint32_t)h[1] << 16);
-          v.y = h[2] | ((uint32_t)h[3] << 16);
-          *reinterpret_cast<uint2*>(o + d0) = v;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[(d0 + e) * os_d] = float_to_bits_bf16(acc[e]);
-      }
-    } else {
-      float* o = reinterpret_cast<float*>(out) + b * os_b + t * os_t;
-      if (os_d == 1 && VEC == 4) {
-        *reinterpret_cast<float4*>(o + d0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[(d0 + e) * os_d] = acc[e];
-      }
-    }
+    store_piece<VEC, OUT_BF16>(acc, out, b * os_b + t * os_t, piece * VEC, os_d);
   }
 }
+
+// K <= KMAX codebooks, one 64-thread workgroup per frame (fewer than 2^31 frames, each with
+// fewer than 2^31 elements of codes: 32-bit index arithmetic): lane k loads codebook k's code
+// (one round trip for all of them), the row indices are broadcast by cross-lane reads into
+// scalar registers, and the K row pieces are loaded as raw 16-byte values, all in flight before
+// the first add, then widened and added in k order.
+template <typename CodeT, typename TableT, int VEC, bool OUT_BF16, int KMAX>
+__global__ void __launch_bounds__(64) rvq_gather_frame_kernel(
+    const CodeT* __restrict__ codes, int num_codebooks, int frames, int64_t cs_b, int64_t cs_k,
+    int64_t cs_t, const TableT* __restrict__ table, int codebook_size, int dim,
+    void* __restrict__ out, int64_t os_b, int64_t os_t, int64_t os_d, int flags) {
+  const int lane = threadIdx.x;
+  const int frame = blockIdx.x;
+  const int b = frame / frames;
+  const int t = frame - b * frames;
+  const bool clamp = (flags & OMNI_RVQ_CLAMP) != 0;
+  // Row index of the lane's codebook's code into the flattened [K * V] table (-1: the code adds
+  // nothing); K * V < 2^31 is checked on the host.
+  int my_row = -1;
+  if (lane < num_codebooks) {
+    int64_t c = (int64_t)codes[b * cs_b + (int64_t)lane * cs_k + t * cs_t];
+    if (c >= codebook_size && clamp) c = codebook_size - 1;
+    my_row = (c >= 0 && c < codebook_size) ? lane * codebook_size + (int)c : -1;
+  }
+  int rows[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) rows[k] = __builtin_amdgcn_readlane(my_row, k);
+  const int pieces = dim / VEC;  // dim % VEC == 0 is checked on the host
+  for (int piece = lane; piece < pieces; piece += kWave) {
+    uint4 raw[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      raw[k] = uint4{0u, 0u, 0u, 0u};
+      if (rows[k] >= 0)
+        raw[k] = *reinterpret_cast<const uint4*>(table + (int64_t)rows[k] * dim + piece * VEC);
+    }
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (rows[k] < 0) continue;
+      const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+      if constexpr (VEC == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + __uint_as_float(w[e]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = acc[2 * q] + __uint_as_float(w[q] << 16);
+          acc[2 * q + 1] = acc[2 * q + 1] + __uint_as_float(w[q] & 0xffff0000u);
+        }
+      }
+    }
+    if (flags & OMNI_RVQ_MEAN) {
+      const float kf = (float)num_codebooks;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = acc[e] / kf;
+    }
+    store_piece<VEC, OUT_BF16>(acc, out, b * os_b + t * os_t, (int64_t)piece * VEC, os_d);
+  }
+}
+
+template <typename CodeT, typename TableT, int VEC, bool OUT_BF16>
+void launch_frames(const CodeT* c, int64_t batch, int k, int64_t frames, int64_t cs_b,
+                   int64_t cs_k, int64_t cs_t, const TableT* t, int64_t v, int64_t dim, void* out,
+                   int64_t os_b, int64_t os_t, int64_t os_d, int flags, hipStream_t stream) {
+  const dim3 grid((unsigned)(batch * frames)), block(64);
+  const int fr = (int)frames, vi = (int)v, di = (int)dim;
+  if (k <= 8)
+    hipLaunchKernelGGL((rvq_gather_frame_kernel<CodeT, TableT, VEC, OUT_BF16, 8>), grid, block, 0,
+                       stream, c, k, fr, cs_b, cs_k, cs_t, t, vi, di, out, os_b, os_t, os_d, flags);
+  else if (k <= 16)
+    hipLaunchKernelGGL((rvq_gather_frame_kernel<CodeT, TableT, VEC, OUT_BF16, 16>), grid, block,
+                       0, stream, c, k, fr, cs_b, cs_k, cs_t, t, vi, di, out, os_b, os_t, os_d,
+                       flags);
+  else
+    hipLaunchKernelGGL((rvq_gather_frame_kernel<CodeT, TableT, VEC, OUT_BF16, 32>), grid, block,
+                       0, stream, c, k, fr, cs_b, cs_k, cs_t, t, vi, di, out, os_b, os_t, os_d,
+                       flags);
+}
+
+// The frame kernel takes decode-step sizes (latency-bound: a few thousand frames or fewer);
+// large batches keep the four-frame workgroups, whose many waves already cover the latency
+// (12 000 frames of 32 codebooks: 51.5 against 53.8 us).
+constexpr int kFrameKernelMaxK = 32;
+constexpr int64_t kFrameKernelMaxFrames = 8192;
 
 template <typename CodeT>
 int launch_rvq(const void* codes, int64_t batch, int64_t k, int64_t frames, int64_t cs_b,
@@ -143,6 +242,27 @@ int launch_rvq(const void* codes, int64_t batch, int64_t k, int64_t frames, int6
   const dim3 block(256);
   const CodeT* c = reinterpret_cast<const CodeT*>(codes);
   const bool out_bf16 = out_dtype == OMNI_DTYPE_BF16;
+  if (k <= kFrameKernelMaxK && total <= kFrameKernelMaxFrames && dim <= 0x7fffffff) {
+    if (table_dtype == OMNI_DTYPE_F32) {
+      const float* t = reinterpret_cast<const float*>(table);
+      if (out_bf16)
+        launch_frames<CodeT, float, 4, true>(c, batch, (int)k, frames, cs_b, cs_k, cs_t, t, v,
+                                             dim, out, os_b, os_t, os_d, flags, stream);
+      else
+        launch_frames<CodeT, float, 4, false>(c, batch, (int)k, frames, cs_b, cs_k, cs_t, t, v,
+                                              dim, out, os_b, os_t, os_d, flags, stream);
+    } else {
+      const u16* t = reinterpret_cast<const u16*>(table);
+      if (out_bf16)
+        launch_frames<CodeT, u16, 8, true>(c, batch, (int)k, frames, cs_b, cs_k, cs_t, t, v, dim,
+                                           out, os_b, os_t, os_d, flags, stream);
+      else
+        launch_frames<CodeT, u16, 8, false>(c, batch, (int)k, frames, cs_b, cs_k, cs_t, t, v,
+                                            dim, out, os_b, os_t, os_d, flags, stream);
+    }
+    OMNI_LAUNCH_CHECK();
+    return OMNI_OK;
+  }
   if (table_dtype == OMNI_DTYPE_F32) {
     const float* t = reinterpret_cast<const float*>(table);
     if (out_bf16)

@@ -34,6 +34,8 @@ pytestmark = pytest.mark.gpu
         (3, 32, 1024, 512, 37, torch.int64),
         (2, 1, 64, 24, 5, torch.int32),
         (2, 9, 33, 520, 3, torch.int64),         # K not a multiple of 8, D past one wave
+        (1, 40, 64, 128, 9, torch.int32),        # K > 32: the four-frame kernel
+        (3, 4, 256, 64, 2900, torch.int64),      # > 8192 frames: the four-frame kernel
     ],
 )
 def test_rvq_gather_sum_is_bit_exact_in_fp32(gpu, batch, k, v, d, t, code_dtype):
