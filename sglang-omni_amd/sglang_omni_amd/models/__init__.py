@@ -14,6 +14,7 @@ from .configs import (
     make_hifigan_weights,
     make_qwen3_code2wav_weights,
 )
+from .codec_state_arena import Qwen3TTSCodecStateArena
 from .dac_codec import CodecStatePool, DacCodecDecoder
 from .dac_weights import dac_weight_tree
 from .graph_runner import CodecGraphRunner, GraphKey
@@ -44,6 +45,7 @@ __all__ = [
     "Qwen3TTSCodecConfig",
     "Qwen3TTSCodecDecoder",
     "Qwen3TTSCodecState",
+    "Qwen3TTSCodecStateArena",
     "make_dac_weights",
     "make_hifigan_weights",
     "dac_weight_tree",

@@ -88,6 +88,7 @@ class _Block:
     c_out: int
     stack: list[ResidualUnitWeights] | None = None  # the units as one residual-stack launch
     stack_coef: torch.Tensor | None = None  # their coefficient rows (computed once)
+    up_kernel: int = 0  # the transposed conv's kernel size
 
 
 # channel counts the fused residual-unit kernel handles (one column tile holds every channel)
@@ -272,7 +273,8 @@ class DacCodecDecoder:
                 units.append(_Unit(c1, c2, a2, b2, an, bn,
                                    c1.conv.c_out in (FUSED_UNIT_CHANNELS if fp8
                                                      else FUSED_UNIT_CHANNELS_BF16)))
-            blk = _Block(up, units, br["stride"], up.conv.c_out)
+            blk = _Block(up, units, br["stride"], up.conv.c_out,
+                         up_kernel=int(br["up"]["weight"].shape[-1]))
             if (residual_stacks and blk.c_out in STACK_CHANNELS
                     and len(units) <= N.MAX_RESIDUAL_UNITS
                     and all(u.conv1.conv.taps == 7 and u.conv1.conv.dilation <= 10 for u in units)):
@@ -353,7 +355,7 @@ class DacCodecDecoder:
         return flat[: batch * length * channels].view(batch, length, channels)
 
     def _decode(self, codes: torch.Tensor, state: dict | None, *,
-                latents: bool = False) -> torch.Tensor:
+                latents: bool = False, window: int | None = None) -> torch.Tensor:
         if codes.dim() != 3:
             raise ValueError(f"codes must be [B, Q, T], got {tuple(codes.shape)}")
         batch, _, frames = codes.shape
@@ -381,6 +383,11 @@ class DacCodecDecoder:
             z, length = codes.transpose(1, 2).to(torch.bfloat16).contiguous(), frames
         else:
             z, length = self._front(codes, ws, state)
+        if window is not None and window * self.front_upsample < length:
+            # the conv stack over the last ``window`` frames only (a tail decode): their samples
+            # and the state the stack leaves do not depend on what precedes the window
+            keep = window * self.front_upsample
+            z, length = z[:, length - keep:].contiguous(), keep
         # the whole decode and a stream's first decode drop each transposed conv's first s
         # samples when the decoder trims both sides
         trim = self.trim_first and (state is None or state["cold"])

@@ -444,21 +444,40 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
 
 
 class Qwen3TTSCodecState:
-    """One cohort of streams' decoder state for ``Qwen3TTSCodecDecoder.decode``: a slot pool with
-    one slot per row (conv histories, transposed-conv contexts, K / V rings, frame positions)
-    and the frames the rows have decoded (``frame_position``), as the reference's
-    ``Qwen3TTSIncrementalCodecState`` (qwen3_tts/incremental_codec.py:74-133) carries them."""
+    """One cohort of streams' decoder state for ``Qwen3TTSCodecDecoder.decode``, as the
+    reference's ``Qwen3TTSIncrementalCodecState`` (qwen3_tts/incremental_codec.py:74-133)
+    carries it: rows bound to slots of a slot pool (conv histories, transposed-conv contexts,
+    K / V rings, the slots' frame positions).
 
-    def __init__(self, pool: Code2WavStatePool, batch_size: int, device: torch.device):
+    * ``init_state``: a private pool with one slot per row; every row starts together and
+      ``frame_position`` counts the frames they have decoded (the first decode is cold).
+    * ``Qwen3TTSCodecStateArena.gather``: rows bound to arena slots in place (no copy); each
+      slot carries its own absolute position (``frame_positions``, settable), and a fresh slot
+      is zeroed, so cold and warm rows decode together.
+    """
+
+    def __init__(self, pool: Code2WavStatePool, batch_size: int, device: torch.device, *,
+                 slot_index: torch.Tensor | None = None, per_row_positions: bool = False):
         self.pool = pool
         self.batch_size = batch_size
-        self.slot_index = torch.arange(batch_size, dtype=torch.int64, device=device)
+        self.slot_index = (torch.arange(batch_size, dtype=torch.int64, device=device)
+                           if slot_index is None else slot_index)
         self.frame_position = 0
+        self.per_row_positions = per_row_positions
+        self.slots: list[int] | None = None  # the host slot ids of an arena cohort
 
     @property
     def frame_positions(self) -> torch.Tensor:
         """The rows' absolute frame positions (on the device)."""
         return self.pool.frame_positions[self.slot_index]
+
+    @frame_positions.setter
+    def frame_positions(self, positions) -> None:
+        values = torch.as_tensor(positions, dtype=torch.int64)
+        if values.shape != (self.batch_size,):
+            raise ValueError(f"{self.batch_size} rows, {tuple(values.shape)} positions")
+        self.pool.frame_positions.index_copy_(0, self.slot_index,
+                                              values.to(self.pool.frame_positions.device))
 
     def advance(self, fresh_frames: int) -> None:
         self.frame_position += fresh_frames
@@ -508,12 +527,75 @@ class Qwen3TTSCodecDecoder(Qwen3Code2WavDecoder):
         if int(codes.shape[0]) != state.batch_size:
             raise ValueError(f"the state holds {state.batch_size} rows, the codes {codes.shape[0]}")
         with torch.no_grad():
-            waveform = self._decode(codes, {"pool": state.pool, "slot_index": state.slot_index,
-                                            "cold": state.frame_position == 0})
+            waveform = self._decode(codes, self._step_state(state))
         if int(waveform.shape[-1]) != fresh_frames * self.total_upsample:
             raise RuntimeError("Qwen3-TTS incremental codec decoder returned the wrong sample count")
         state.advance(fresh_frames)
         return waveform
+
+    @staticmethod
+    def _step_state(state: Qwen3TTSCodecState) -> dict:
+        # arena rows decode warm: a fresh slot is zeroed (histories, contexts, K / V, position
+        # 0), which is what a cold decode reads, and the attention keys start at position 0
+        cold = not state.per_row_positions and state.frame_position == 0
+        return {"pool": state.pool, "slot_index": state.slot_index, "cold": cold}
+
+    def tail_frames(self, emit_frames: int) -> int:
+        """The code frames the last ``emit_frames`` frames' samples and the conv stack's state
+        depend on (``tail_frames``, qwen3_tts/incremental_codec.py:1085-1110), walked back from
+        the waveform: a causal conv adds its context, a transposed conv of kernel k and stride s
+        maps n samples to (n + k - 1) // s inputs."""
+        samples = int(emit_frames) * self.total_upsample + (self.final_taps - 1)
+        for blk in reversed(self.blocks):
+            for unit in reversed(blk.units):
+                samples += unit.conv1.conv.left_pad  # the k = 1 conv adds none
+            samples = (samples + blk.up_kernel - 1) // blk.stride
+        samples += self.in_conv.conv.left_pad
+        for up in reversed(self.upsamplers):
+            samples += up["dw_weight"].shape[0] - 1  # the ConvNeXt depthwise conv
+            samples = (samples + up["factor"] - 1) // up["factor"]  # kernel = stride
+        return samples
+
+    def decode_tail(self, codes: torch.Tensor, valid_frames, state: Qwen3TTSCodecState,
+                    emit_frames: int) -> torch.Tensor:
+        """Row i's first ``valid_frames[i]`` frames of ``codes`` decoded after its state, the
+        conv stack run over the last ``tail_frames(emit_frames)`` of them only; returns the
+        samples of the last ``emit_frames`` frames of each row, (B, 1, emit_frames * hop), and
+        advances each row by its valid frames (``decode_tail``, qwen3_tts/incremental_codec.py:
+        1112-1134). Needs arena rows (per-row positions) and tail_frames <= valid_frames[i] <=
+        T. Rows of one width decode together (their transformer, pre_conv and ConvNeXt state
+        end at their own last frame)."""
+        if not state.per_row_positions:
+            raise ValueError("Qwen3-TTS tail decoding needs per-row frame positions")
+        if codes.ndim != 3 or int(codes.shape[0]) != state.batch_size:
+            raise ValueError(f"codes must be [{state.batch_size}, Q, T], got {tuple(codes.shape)}")
+        widths = [int(w) for w in torch.as_tensor(valid_frames).reshape(-1).tolist()]
+        if len(widths) != state.batch_size:
+            raise ValueError(f"{len(widths)} valid frame counts for {state.batch_size} rows")
+        tail = self.tail_frames(emit_frames)
+        if emit_frames < 1 or any(w < tail or w > codes.shape[-1] for w in widths):
+            raise ValueError(f"every row needs between tail_frames ({tail}) and {codes.shape[-1]} "
+                             f"valid frames, and emit_frames >= 1; got {widths}")
+        samples = int(emit_frames) * self.total_upsample
+        out = torch.empty(state.batch_size, 1, samples, dtype=torch.float32, device=self.device)
+        with torch.no_grad():
+            for w in sorted(set(widths)):
+                rows = [i for i, v in enumerate(widths) if v == w]
+                if len(rows) == state.batch_size:
+                    sub_codes, sub_index = codes[..., :w], state.slot_index
+                else:
+                    pick = torch.tensor(rows, dtype=torch.int64).to(self.device)
+                    sub_codes = codes.index_select(0, pick)[..., :w]
+                    sub_index = state.slot_index.index_select(0, pick)
+                step = {"pool": state.pool, "slot_index": sub_index, "cold": False}
+                wave = self._decode(sub_codes.contiguous(), step, window=tail)
+                if len(rows) == state.batch_size:
+                    out.copy_(wave[..., -samples:])
+                else:
+                    out.index_copy_(0, pick, wave[..., -samples:].contiguous())
+        return out
+
+
 
     def precompile(self, codes: torch.Tensor, state: Qwen3TTSCodecState) -> None:
         """Admit (B, T) for ``decode(..., compiled=True)``: the HIP path needs no tracing, so this
