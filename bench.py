@@ -269,7 +269,8 @@ def run_only(args, device) -> None:
         if blk.stack is None or blk.c_out != 96:
             raise SystemExit("the decoder's last block runs no 96-channel residual stack")
         gen = torch.Generator().manual_seed(0)
-        x = (torch.randn(STREAMS, 23040, 96, generator=gen) * 0.3).to(device)
+        x = (torch.randn(STREAMS, 23040, 96, generator=gen) * 0.3).to(device,
+                                                                    decoder.residual_dtype)
         wave = torch.empty(STREAMS, 1, 23040, dtype=torch.float32, device=device)
         final = FinalConv(decoder.final_weight, decoder.final_bias, N.ACT_TANH, wave)
         last = blk.units[-1]

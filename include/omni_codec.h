@@ -100,7 +100,8 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 8: omni_conv1d_splitk takes k = 7, history and activations */
+int omni_codec_abi_version(void); /* 9: float16 residual streams (omni_conv_args.residual_dtype,
+                                      omni_residual_stack_args.x_dtype) */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -134,11 +135,13 @@ int omni_rvq_gather_sum(const void* codes, int codes_dtype, int64_t batch, int64
  *     v = (sum_{n'} W2[n, n'] * h[b, i, n']) * weight2_scale[n] (fp8 only) + bias2[n]
  *   v = v (+ residual[b, i, n])
  *   v = ((mix_a[b, i, n] + mix_b[b, i, n]) + v) * mix_scale      (optional, mix_a != NULL)
- *   sum_out[b, i, n] = v            (float32, optional)
+ *   sum_out[b, i, n] = v            (optional; float32, or float16 rounded to nearest even)
  *   out[b, i, n] = act(v)           (bf16 or float32; optional when sum_out is given)
  *
  * for i < length and n < n_cols. x holds x_length positions per row (x_length = 0 means length);
- * the residual, mix and sum_out tensors share the residual strides; sum_out may alias residual
+ * the residual, mix and sum_out tensors share the residual strides; residual and sum_out are
+ * float32, or float16 with residual_dtype = OMNI_DTYPE_F16 (a residual stream kept in half
+ * precision between launches, added in float32; then no mix); sum_out may alias residual
  * (each element is read before it is written by the same thread) but no output may alias x. A
  * causal Conv1d is taps = k, left_pad = (k-1)*d; a ConvTranspose1d of stride s is its polyphase
  * form (n = phase * c_out + co, so out viewed as [B, length * s, c_out] is the transposed conv's
@@ -185,12 +188,12 @@ typedef struct omni_conv_args {
                                zeros and writes no history */
   int64_t hist_slot_stride; /* elements between consecutive slots (= 2 * left_pad * c_in) */
   int history_cold;
-  const float* residual;
+  const void* residual; /* float32, or float16 (residual_dtype) */
   int64_t residual_stride_b, residual_stride_t;
   const float* mix_a;
   const float* mix_b;
   float mix_scale;
-  float* sum_out;
+  void* sum_out; /* float32, or float16 (residual_dtype) */
   void* out;
   int out_dtype;
   int64_t out_stride_b, out_stride_t;
@@ -198,6 +201,8 @@ typedef struct omni_conv_args {
   const float* act_a;
   const float* act_b;
   float act_slope;
+  /* ABI version 9: OMNI_DTYPE_F32 (0) or OMNI_DTYPE_F16, the dtype of residual and sum_out */
+  int residual_dtype;
 } omni_conv_args;
 
 int omni_conv1d_fused(const omni_conv_args* args, omni_stream_t stream);
@@ -278,7 +283,8 @@ int omni_conv1d_plan(const omni_conv_args* args, int kernel, int config, int* ke
 
 /*
  * The residual units of a DAC decoder block in one launch (Snake -> conv k = 7, dilation d ->
- * Snake -> conv k = 1 -> + x, for each unit in turn), the residual stream kept in float32:
+ * Snake -> conv k = 1 -> + x, for each unit in turn), the residual stream kept in float32 (x read
+ * as float32 or float16, x_out written as either, x_dtype):
  *
  *   x_0 = x
  *   for each unit k:
@@ -287,11 +293,12 @@ int omni_conv1d_plan(const omni_conv_args* args, int kernel, int config, int* ke
  *     h   = Snake(mid_act_a, mid_act_b)(v) rounded to bf16
  *     x_{k+1} = (sum_n' W2_k[n, n'] * h[n']) * w2_scale + bias2 + x_k
  *   out   = Snake(out_act_a, out_act_b)(x_last) rounded to bf16   (the next layer's operand)
- *   x_out = x_last                                                   (float32, optional)
+ *   x_out = x_last                                        (optional; float32 or float16)
  *   final_out = the decoder's final conv of out (optional, below)
  *
- * with the arithmetic of one omni_conv1d_fused residual-unit call per unit, so the results are
- * the same bits. Weights use omni_conv1d_fused's packing ([C/32][C][7][32] and [C/32][C][32],
+ * with the arithmetic of one omni_conv1d_fused residual-unit call per unit, so with a float32
+ * residual stream the results are the same bits (with a float16 one the calls round x between
+ * units, which the stack does not). Weights use omni_conv1d_fused's packing ([C/32][C][7][32] and [C/32][C][32],
  * bf16, or fp8-e4m3 with per-column scales). Each unit's dilated conv keeps its own streaming
  * history (unit.hist_pool, bf16 [slots][2][6 * d_k][C], the omni_conv1d_fused contract with
  * the shared slot_index / slot_parity / history_cold). channels = 96; x, out and x_out are
@@ -321,7 +328,7 @@ typedef struct omni_residual_unit {
 #define OMNI_MAX_RESIDUAL_UNITS 4
 
 typedef struct omni_residual_stack_args {
-  const float* x;
+  const void* x; /* float32, or float16 (x_dtype) */
   int64_t x_stride_b, x_stride_t;
   int64_t batch, length, channels;
   int weight_dtype;
@@ -335,7 +342,7 @@ typedef struct omni_residual_stack_args {
   const float* out_act_b;
   void* out; /* bf16 */
   int64_t out_stride_b, out_stride_t;
-  float* x_out; /* optional */
+  void* x_out; /* optional; float32, or float16 (x_dtype) */
   int64_t x_out_stride_b, x_out_stride_t;
   /* Optional (final_weight != NULL): the decoder's conv to one channel fused behind the stack,
    * over u = Snake(out_act)(x_last) rounded to bf16:
@@ -359,6 +366,9 @@ typedef struct omni_residual_stack_args {
      workgroup, precomputed by omni_residual_stack_coefficients for these units (16-byte
      aligned), or NULL */
   const float* coef_table;
+  /* ABI version 9: OMNI_DTYPE_F32 (0) or OMNI_DTYPE_F16, the dtype of x and x_out (the stack
+     keeps x in float32 between its units and rounds x_out once) */
+  int x_dtype;
 } omni_residual_stack_args;
 
 /* Fills table[(num_units * 8 + 2) * channels] (float32, device, 16-byte aligned) with the

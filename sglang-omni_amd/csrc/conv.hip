@@ -110,12 +110,19 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
   if (!aligned16(a->weight)) return OMNI_ERR_INVALID_ARG;
   if (a->x_length < 0) return OMNI_ERR_INVALID_ARG;
   const bool has_r = a->residual || a->sum_out || a->mix_a;
+  if (a->residual_dtype != OMNI_DTYPE_F32 && a->residual_dtype != OMNI_DTYPE_F16)
+    return OMNI_ERR_INVALID_ARG;
+  const bool r_f16 = a->residual_dtype == OMNI_DTYPE_F16;
   if (has_r && (a->residual_stride_t % 4 || a->residual_stride_b % 4 ||
                 a->residual_stride_t < a->n_cols))
     return OMNI_ERR_INVALID_ARG;
-  if ((a->residual && !aligned16(a->residual)) || (a->sum_out && !aligned16(a->sum_out)))
+  // 16-byte float32 / 8-byte float16 accesses of 4 elements
+  auto r_aligned = [&](const void* ptr) {
+    return (reinterpret_cast<uintptr_t>(ptr) & (r_f16 ? 7 : 15)) == 0;
+  };
+  if ((a->residual && !r_aligned(a->residual)) || (a->sum_out && !r_aligned(a->sum_out)))
     return OMNI_ERR_INVALID_ARG;
-  if (a->mix_a && (!a->mix_b || !aligned16(a->mix_a) || !aligned16(a->mix_b)))
+  if (a->mix_a && (r_f16 || !a->mix_b || !aligned16(a->mix_a) || !aligned16(a->mix_b)))
     return OMNI_ERR_INVALID_ARG;
   if (a->out && a->out_stride_t < a->n_cols) return OMNI_ERR_INVALID_ARG;
   if (a->out) {
@@ -143,7 +150,7 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
   const int64_t hist_bytes = a->hist_pool ? a->hist_num_slots * a->hist_slot_stride * 2 : 0;
   const int64_t r_bytes =
       has_r ? ((a->batch - 1) * a->residual_stride_b + (a->length - 1) * a->residual_stride_t +
-               a->n_cols) * 4 : 0;
+               a->n_cols) * (r_f16 ? 2 : 4) : 0;
   const int64_t o_bytes =
       a->out ? ((a->batch - 1) * a->out_stride_b + (a->length - 1) * a->out_stride_t + a->n_cols) *
                    (a->out_dtype == OMNI_DTYPE_F32 ? 4 : 2) : 0;
@@ -203,6 +210,7 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
   p.mix_b = a->mix_b;
   p.mix_scale = a->mix_scale;
   p.sum_out = a->sum_out;
+  p.r_f16 = r_f16 ? 1 : 0;
   p.out = a->out;
   p.out_bf16 = a->out_dtype == OMNI_DTYPE_BF16;
   p.o_sb = a->out_stride_b;

@@ -216,6 +216,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
     q.out = nullptr;
     q.act = OMNI_ACT_NONE;
     q.sum_out = p.partial + (int64_t)split * M * n_cols;
+    q.r_f16 = 0;
     q.r_st = n_cols;
     q.r_sb = (int64_t)L * n_cols;
     q.r_bytes = (uint32_t)((int64_t)M * n_cols * 4);

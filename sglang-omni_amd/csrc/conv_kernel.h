@@ -22,8 +22,9 @@
 // first GEMM's last chunk), and only its result leaves the workgroup.
 //
 // The epilogue works on the MFMA accumulator layout (lane = position, 4 consecutive channels per
-// lane) and fuses the per-column weight scale (fp8), bias, the float32 residual add, the float32
-// residual-stream store and the activation (Snake / LeakyReLU / tanh / clamp) into the stores.
+// lane) and fuses the per-column weight scale (fp8), bias, the residual add (in float32, the
+// stream read as float32 or float16), the residual-stream store (float32, or float16 rounded to
+// nearest even) and the activation (Snake / LeakyReLU / tanh / clamp) into the stores.
 //
 // Streaming: positions left of 0 come from the slot's history copy (slot_parity & 1); the
 // workgroups of column tile 0 write the last left_pad activated input samples into the other
@@ -64,12 +65,13 @@ struct ConvParams {
   int64_t hist_slots;
   int64_t hist_slot_stride;
   int hist_cold;
-  const float* residual;
+  const void* residual;  // float32, or float16 when r_f16
   int64_t r_sb, r_st;  // shared by residual, mix_a, mix_b and sum_out
   const float* mix_a;
   const float* mix_b;
   float mix_scale;
-  float* sum_out;
+  void* sum_out;  // float32, or float16 when r_f16
+  int r_f16;      // residual and sum_out are float16 (a half-precision residual stream; no mix)
   void* out;
   int out_bf16;
   int64_t o_sb, o_st;
@@ -180,6 +182,38 @@ __device__ __forceinline__ void stage_coefficients(const ConvParams& p, float* c
   }
 }
 
+// Four consecutive elements of a residual stream at byte offset off (kOutOfRange reads zeros),
+// as loaded: float32 (one 16-byte load), or float16 (one 8-byte load, in the first two words).
+// The raw bits are widened only where they are used (widen_residual4), so a prefetch's wait stays
+// at its use.
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 load_residual4_raw(__amdgpu_buffer_rsrc_t rsrc, uint32_t off,
+                                                    int f16) {
+  if (f16) {
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, 0);
+    return u32x4{w.x, w.y, 0u, 0u};
+  }
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+}
+// The four float32 values of a raw residual load (float16 widened exactly).
+__device__ __forceinline__ f32x4 widen_residual4(u32x4 raw, int f16) {
+  if (f16) return __builtin_convertvector(__builtin_bit_cast(f16x4, u32x2{raw.x, raw.y}), f32x4);
+  return __builtin_bit_cast(f32x4, raw);
+}
+__device__ __forceinline__ f32x4 load_residual4(__amdgpu_buffer_rsrc_t rsrc, uint32_t off,
+                                                int f16) {
+  return widen_residual4(load_residual4_raw(rsrc, off, f16), f16);
+}
+// ... and the store: float32, or float16 rounded to nearest even (kOutOfRange drops it).
+__device__ __forceinline__ void store_residual4(f32x4 v, __amdgpu_buffer_rsrc_t rsrc, uint32_t off,
+                                                int f16) {
+  if (f16)
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, __builtin_convertvector(v, f16x4)),
+                                          rsrc, off, 0, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsrc, off, 0, 0);
+}
+
 // The epilogue shared by the conv kernels, from the accumulators of a BCO x BP tile (column
 // tile n0, positions [m0, m_end)) to HBM, in two steps per pass over half the position waves:
 // (1) in the accumulator layout (lane = position, 4 consecutive columns per lane) each wave adds
@@ -217,6 +251,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
   // fit 32 bits (the byte extents are below 2 GiB).
   const bool packed = p.r_sb == (int64_t)L * p.r_st && p.o_sb == (int64_t)L * p.o_st;
   const uint32_t r_st = (uint32_t)p.r_st, o_st = (uint32_t)p.o_st;
+  const uint32_t rsize = p.r_f16 ? 2u : 4u;  // bytes per residual-stream element
   const bool live = walker && n_q < n_cols;
   // element offsets of flat position m in the residual-shaped tensors and in out
   auto offsets = [&](int m, uint32_t& re, uint32_t& oe) __attribute__((always_inline)) {
@@ -246,7 +281,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
       uint32_t re, oe;
       offsets(mp + r, re, oe);
       const bool ok = live && r0 + u * RSTEP < prow;
-      roff[u] = ok ? re * 4 : kOutOfRange;
+      roff[u] = ok ? re * rsize : kOutOfRange;
       ooff[u] = ok ? oe : kOutOfRange;
       v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
     }
@@ -254,11 +289,10 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
       if (!have_res) {
         const auto rr = buffer_rsrc(p.residual, p.r_bytes);
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
-          res[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, roff[u], 0, 0));
+        for (int u = 0; u < NU; ++u) res[u] = load_residual4_raw(rr, roff[u], p.r_f16);
       }
 #pragma unroll
-      for (int u = 0; u < NU; ++u) v[u] += res[u];
+      for (int u = 0; u < NU; ++u) v[u] += widen_residual4(res[u], p.r_f16);
     }
     if (p.mix_a) {
       const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
@@ -273,8 +307,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
     if (p.sum_out) {
       const auto rs = buffer_rsrc(p.sum_out, p.r_bytes);
 #pragma unroll
-      for (int u = 0; u < NU; ++u)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rs, roff[u], 0, 0);
+      for (int u = 0; u < NU; ++u) store_residual4(v[u], rs, roff[u], p.r_f16);
     }
     if (p.out != nullptr) {
       const int act = p.act;
@@ -310,7 +343,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
   constexpr int NPASS = (WAVES_P + EPI_WAVES - 1) / EPI_WAVES;
   constexpr int UR = (Tile::EPI_ROWS + RSTEP - 1) / RSTEP;  // rows per walker and pass
   constexpr bool PREFETCH = UR <= 10 && NT <= 512;
-  f32x4 pre[PREFETCH ? UR : 1];
+  u32x4 pre[PREFETCH ? UR : 1];  // raw residual loads (load_residual4_raw)
   auto prefetch = [&](int pass) __attribute__((always_inline)) {
     if constexpr (PREFETCH) {
       if (p.residual) {
@@ -322,8 +355,8 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
           const int r = r_first + u * RSTEP;
           uint32_t re, oe;
           offsets(mp + min(r, prow - 1), re, oe);
-          const uint32_t off = live && r < prow ? re * 4 : kOutOfRange;
-          pre[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0));
+          const uint32_t off = live && r < prow ? re * rsize : kOutOfRange;
+          pre[u] = load_residual4_raw(rr, off, p.r_f16);
         }
       }
     }
@@ -355,7 +388,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
     } else {
       constexpr int U = 4;  // rows in flight per thread
       for (int r0 = r_first; r0 < prow; r0 += U * RSTEP) {
-        f32x4 res[U];
+        u32x4 res[U];
         finish(std::integral_constant<int, U>{}, mp, prow, r0, false, res);
       }
     }

@@ -11,7 +11,8 @@
 //     reaches before the segment's first staged row gives a value no later unit's valid row
 //     reads (row q of a segment is exact for unit k once q >= halo_1 + ... + halo_k).
 //   * x: float32 in the MFMA accumulator layout (lane = row, 4 consecutive channels per lane),
-//     loaded once from HBM, updated in place by each unit's k = 1 conv.
+//     loaded once from HBM (float32, or a float16 residual stream widened exactly), updated in
+//     place by each unit's k = 1 conv.
 //   * the operand u_k = Snake(x_k) and the h tile between the two convs: bf16 in one LDS tile
 //     [C/32][guard + rows][32] (64-byte rows, the 16-byte slots rotated by (row / 4) % 4 so the
 //     accumulator-layout writes and the operand reads both spread over all banks); guard rows
@@ -67,7 +68,8 @@ struct StackUnit {
 };
 
 struct StackParams {
-  const float* x;
+  const void* x;  // float32, or float16 when x_f16 (x_out likewise)
+  int x_f16;
   int x_sb, x_st;
   int batch, length;
   int nunits;
@@ -80,7 +82,7 @@ struct StackParams {
   const float* out_b;
   u16* out;
   int o_sb, o_st;
-  float* x_out;
+  void* x_out;
   int xo_sb, xo_st;
   uint32_t x_bytes, o_bytes, xo_bytes;
   // the decoder's final conv to one channel (fin_w != NULL): [fin_taps][C] float32 weights
@@ -207,6 +209,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   const int lrow = lane & 15;
   const int lk = (lane >> 4) * 8;
   const int wco0 = wave_co * TCO * 16;
+  const uint32_t xsize = p.x_f16 ? 2u : 4u;  // bytes per element of x and x_out
 
   // The workgroup's positions: nseg row segments of len positions from position i0 of rows b0..
   // (one tile), or in the sweep the positions [i0, seg_end) of row b0, tile after tile.
@@ -406,8 +409,10 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         const int pos = pos_of(t, ln & 15);
         const bool ok = pos >= 0 && pos < L;
         const uint32_t off =
-            ok ? (uint32_t)((b0 + seg_of(t, ln & 15)) * p.x_sb + pos * p.x_st + n) * 4 : kOutOfRange;
-        xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            ok ? (uint32_t)((b0 + seg_of(t, ln & 15)) * p.x_sb + pos * p.x_st + n) * xsize
+               : kOutOfRange;
+        // raw bits (widened at unit 0's operand, where the load is first waited for)
+        xv[c][t] = __builtin_bit_cast(f32x4, omni_conv::load_residual4_raw(xr, off, p.x_f16));
       }
     }
   }
@@ -448,7 +453,8 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     const f32x4 b = *reinterpret_cast<const f32x4*>(in0 + C + n);
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
-      const f32x4 v = xv[c][t];
+      const f32x4 v = omni_conv::widen_residual4(__builtin_bit_cast(u32x4, xv[c][t]), p.x_f16);
+      xv[c][t] = v;
       put(c, t, snake_rev(v[0], a[0], b[0]), snake_rev(v[1], a[1], b[1]),
           snake_rev(v[2], a[2], b[2]), snake_rev(v[3], a[3], b[3]));
     }
@@ -698,8 +704,10 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
           const int r = wave_p * TP * 16 + t * 16 + (ln & 15);
           const int pos = ni0 + r;
           const bool ok = r < nrows && pos < L;
-          const uint32_t off = ok ? (uint32_t)(b0 * p.x_sb + pos * p.x_st + n) * 4 : kOutOfRange;
-          xv[c][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+          const uint32_t off = ok ? (uint32_t)(b0 * p.x_sb + pos * p.x_st + n) * xsize : kOutOfRange;
+          // the raw bits (a float16 stream in the first two words), widened where the next tile
+          // first reads them, so this load's wait stays there
+          xv[c][t] = __builtin_bit_cast(f32x4, omni_conv::load_residual4_raw(xr, off, p.x_f16));
         }
       }
       x_ready = true;
@@ -835,9 +843,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         const int q = row_of(t, lr) - seg_of(t, lr) * span;
         const bool ok = row_of(t, lr) < rows && q >= H;
         const uint32_t off =
-            ok ? (uint32_t)((b0 + seg_of(t, lr)) * p.xo_sb + pos_of(t, lr) * p.xo_st + n) * 4
+            ok ? (uint32_t)((b0 + seg_of(t, lr)) * p.xo_sb + pos_of(t, lr) * p.xo_st + n) * xsize
                : kOutOfRange;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xv[c][t]), xo, off, 0, 0);
+        omni_conv::store_residual4(xv[c][t], xo, off, p.x_f16);
       }
     }
   }

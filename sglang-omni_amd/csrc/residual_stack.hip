@@ -78,8 +78,14 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   const bool fp8 = a->weight_dtype == OMNI_DTYPE_FP8_E4M3;
   const int64_t C = a->channels;
   if (C != 96) return C > 0 && C % 32 == 0 ? OMNI_ERR_UNSUPPORTED : OMNI_ERR_INVALID_ARG;
-  // 16-byte accesses of x, out and x_out rows
-  if (!aligned16(a->x) || a->x_stride_t < C || a->x_stride_t % 4 || a->x_stride_b % 4)
+  if (a->x_dtype != OMNI_DTYPE_F32 && a->x_dtype != OMNI_DTYPE_F16) return OMNI_ERR_INVALID_ARG;
+  const bool x_f16 = a->x_dtype == OMNI_DTYPE_F16;
+  const int64_t x_elem = x_f16 ? 2 : 4;
+  // 16-byte accesses of out rows; 16-byte (float32) or 8-byte (float16) accesses of x and x_out
+  auto x_aligned = [&](const void* ptr) {
+    return (reinterpret_cast<uintptr_t>(ptr) & (x_f16 ? 7 : 15)) == 0;
+  };
+  if (!x_aligned(a->x) || a->x_stride_t < C || a->x_stride_t % 4 || a->x_stride_b % 4)
     return OMNI_ERR_INVALID_ARG;
   if (a->out &&
       (!aligned16(a->out) || a->out_stride_t < C || a->out_stride_t % 8 || a->out_stride_b % 8))
@@ -97,7 +103,7 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
       return OMNI_ERR_INVALID_ARG;
   }
   if (a->coef_table && !aligned16(a->coef_table)) return OMNI_ERR_INVALID_ARG;
-  if (a->x_out && (!aligned16(a->x_out) || a->x_out_stride_t < C || a->x_out_stride_t % 4 ||
+  if (a->x_out && (!x_aligned(a->x_out) || a->x_out_stride_t < C || a->x_out_stride_t % 4 ||
                    a->x_out_stride_b % 4))
     return OMNI_ERR_INVALID_ARG;
   bool any_hist = false;
@@ -131,7 +137,7 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   // byte extents (buffer offsets are 32-bit)
   const int64_t B = a->batch, L = a->length;
   const int64_t limit = 0x7fffffffLL;
-  const int64_t x_bytes = ((B - 1) * a->x_stride_b + (L - 1) * a->x_stride_t + C) * 4;
+  const int64_t x_bytes = ((B - 1) * a->x_stride_b + (L - 1) * a->x_stride_t + C) * x_elem;
   const int64_t o_bytes =
       a->out ? ((B - 1) * a->out_stride_b + (L - 1) * a->out_stride_t + C) * 2 : 0;
   const int64_t fh_bytes =
@@ -139,11 +145,12 @@ extern "C" int omni_residual_stack(const omni_residual_stack_args* a, omni_strea
   if (fin && ((B - 1) * a->final_out_stride_b + L > limit || fh_bytes > limit))
     return OMNI_ERR_UNSUPPORTED;
   const int64_t xo_bytes =
-      a->x_out ? ((B - 1) * a->x_out_stride_b + (L - 1) * a->x_out_stride_t + C) * 4 : 0;
+      a->x_out ? ((B - 1) * a->x_out_stride_b + (L - 1) * a->x_out_stride_t + C) * x_elem : 0;
   if (x_bytes > limit || o_bytes > limit || xo_bytes > limit) return OMNI_ERR_UNSUPPORTED;
 
   StackParams p{};
   p.x = a->x;
+  p.x_f16 = x_f16 ? 1 : 0;
   p.x_sb = (int)a->x_stride_b;
   p.x_st = (int)a->x_stride_t;
   p.batch = (int)B;

@@ -41,7 +41,7 @@ class OmniCodecError(RuntimeError):
 
 INVALID_ARG = 1
 UNSUPPORTED = 2
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # kernel families of omni_conv1d_fused (omni_conv1d_plan / omni_conv1d_fused_with)
 CONV_KERNEL_AUTO, CONV_KERNEL_DMA, CONV_KERNEL_STAGED, CONV_KERNEL_STAGED11, CONV_KERNEL_FUSED_UNIT = range(5)
@@ -102,6 +102,7 @@ class ConvArgs(ctypes.Structure):
         ("act_a", ctypes.c_void_p),
         ("act_b", ctypes.c_void_p),
         ("act_slope", ctypes.c_float),
+        ("residual_dtype", ctypes.c_int),
     ]
 
 
@@ -162,6 +163,7 @@ class ResidualStackArgs(ctypes.Structure):
         ("final_out", ctypes.c_void_p),
         ("final_out_stride_b", ctypes.c_int64),
         ("coef_table", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int),
     ]
 
 

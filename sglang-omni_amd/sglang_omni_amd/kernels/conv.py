@@ -225,12 +225,18 @@ def _conv_args(
         if t.data_ptr() == x.data_ptr():
             raise ValueError("an output may not alias x")
     aux = [t for t in (residual, sum_out) if t is not None]
+    # the residual stream: float32, or float16 (a half-precision stream, added in float32)
+    r_dtype = aux[0].dtype if aux else torch.float32
+    if r_dtype not in (torch.float32, torch.float16):
+        raise ValueError("residual / sum_out must be float32 or float16")
     if mix is not None:
         N.require_device(mix[0], mix[1])
+        if r_dtype != torch.float32:
+            raise ValueError("a mix takes a float32 residual stream")
         aux += [mix[0], mix[1]]
     for t in aux:
-        if t.dtype != torch.float32 or t.stride() != aux[0].stride():
-            raise ValueError("residual / sum_out / mix must be float32 with one shared stride")
+        if t.dtype != r_dtype or t.stride() != aux[0].stride():
+            raise ValueError("residual / sum_out / mix must share one dtype and one stride")
         if (t.device != dev or t.dim() != 3 or t.shape[0] != batch or t.shape[1] < length
                 or t.shape[2] != n_cols):
             raise ValueError(f"residual / sum_out / mix must be [B, {length}, {n_cols}] on {dev}")
@@ -289,6 +295,7 @@ def _conv_args(
         args.mix_b = mix[1].data_ptr()
         args.mix_scale = float(mix[2])
     args.sum_out = N.ptr(sum_out)
+    args.residual_dtype = N.omni_dtype(r_dtype)
     if out is not None:
         args.out = out.data_ptr()
         args.out_dtype = N.omni_dtype(out.dtype)
@@ -350,8 +357,9 @@ def fused_conv(x: torch.Tensor, conv: PackedConv, out: torch.Tensor | None, *,
     x [B, >=x_length, C_in] bf16 or float32 (rows may sit in longer buffers; channel stride 1),
     activated per input channel by ``in_activation`` while it is staged; ``second`` is a k = 1
     conv (C_out -> C_out) fused behind this one with ``mid_activation`` between them;
-    out [B, length, n_cols] bf16 or float32; residual / sum_out / mix tensors float32 with out's
-    logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16 with int64
+    out [B, length, n_cols] bf16 or float32; residual / sum_out (float32, or float16: a
+    half-precision residual stream, added in float32 and rounded once when stored) / mix
+    (float32 streams only) tensors with out's logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16 with int64
     slot_index [B] and slot_parity [slots]. ``kernel`` / ``config`` name a kernel family and the
     1-based entry of its tile list (``omni_conv1d_fused_with``) instead of the size-based choice.
     """
@@ -484,8 +492,9 @@ def residual_stack(
     final: FinalConv | None = None,
     coef_table: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Launch ``omni_residual_stack``: every unit in turn over x [B, L, C] float32, then
-    out = Snake(out_a, out_b)(x_last) as bf16 [B, L, C] (and x_last into x_out, float32).
+    """Launch ``omni_residual_stack``: every unit in turn over x [B, L, C] (float32, or a
+    float16 residual stream, kept in float32 between the units), then out = Snake(out_a,
+    out_b)(x_last) as bf16 [B, L, C] (and x_last into x_out, in x's dtype).
     histories[k] is unit k's conv1 history pool [slots, 2, 6 * dilation, C] bf16 (streaming).
     With ``final`` the decoder's conv to one channel runs over out inside the same launch and
     writes final.out [B, 1, L] float32 (out may then be None: the operand stays on chip); returns
@@ -494,16 +503,16 @@ def residual_stack(
     dev = x.device
     if not 1 <= len(units) <= N.MAX_RESIDUAL_UNITS:
         raise ValueError(f"1..{N.MAX_RESIDUAL_UNITS} residual units per launch")
-    if x.dtype != torch.float32 or x.dim() != 3 or x.stride(2) != 1:
-        raise ValueError("x must be float32 [B, L, C] with channel stride 1")
+    if x.dtype not in (torch.float32, torch.float16) or x.dim() != 3 or x.stride(2) != 1:
+        raise ValueError("x must be float32 or float16 [B, L, C] with channel stride 1")
     batch, length, channels = x.shape
     if out is None and final is None:
         raise ValueError("the stack needs an output: out, or a final conv")
-    for t, dt in ((out, torch.bfloat16), (x_out, torch.float32)):
+    for t, dt in ((out, torch.bfloat16), (x_out, x.dtype)):
         if t is None:
             continue
         if t.dtype != dt or t.dim() != 3 or tuple(t.shape) != (batch, length, channels) or t.stride(2) != 1:
-            raise ValueError("out / x_out must be [B, L, C] (bf16 / float32) with channel stride 1")
+            raise ValueError("out / x_out must be [B, L, C] (bf16 / x's dtype) with channel stride 1")
         if t.data_ptr() == x.data_ptr():
             raise ValueError("an output may not alias x")
     for t in (out, x_out):
@@ -540,6 +549,7 @@ def residual_stack(
     wdtype = units[0].conv1.weight.dtype
     args = N.ResidualStackArgs()
     args.x = x.data_ptr()
+    args.x_dtype = N.omni_dtype(x.dtype)
     args.x_stride_b, args.x_stride_t = x.stride(0), x.stride(1)
     args.batch, args.length, args.channels = batch, length, channels
     args.weight_dtype = N.omni_dtype(wdtype)

@@ -10,18 +10,19 @@ slot_index, first_decode=...)``) with a ``CodecStatePool``-shaped state pool
 The decoder follows ``Decoder`` / ``DecoderBlock`` / ``ResidualUnit`` / ``CausalConvNet`` /
 ``CausalTransConvNet`` of sglang_omni/models/fishaudio_s2_pro/fish_speech/models/dac/
 modded_dac.py:541-835 fed by the RVQ gather-sum (rvq.py:374-388). Every op runs in a HIP kernel,
-on channels-last activations. The residual stream x stays float32 in HBM; every producer also
+on channels-last activations. The residual stream x stays in HBM between launches as float16
+(``residual_dtype``; float32 on request), every residual add in float32; every producer also
 writes the next conv's operand u = Snake(x) as bf16 in its epilogue, so each conv reads a ready
 bf16 operand:
 
     rvq_gather_sum                       codes -> z (bf16)
     conv k7 (512 -> C0)                  z -> u = Snake(block 0)(x) (bf16)
     per block:
-      polyphase ConvTranspose (k = 2s)   u -> x (float32), u = Snake(unit 0 act1)(x)
+      polyphase ConvTranspose (k = 2s)   u -> x, u = Snake(unit 0 act1)(x)
       per residual unit (d = 1, 3, 9):
         96 channels (192 with fp8 weights): one launch
                                          conv k7 dilation d; bias + Snake(act2) -> bf16 tile in
-                                         LDS; conv k1; bias + x -> x (float32, in place),
+                                         LDS; conv k1; bias + x -> x (in place),
                                          u' = Snake(next)(x) (bf16)
         otherwise:         two launches  conv k7; bias + Snake(act2) -> h (bf16)
                                          conv k1 of h; bias + x -> x (in place), u' = Snake(next)(x)
@@ -192,13 +193,14 @@ class CodecStatePool:
 @dataclass
 class _Workspace:
     z: torch.Tensor | None
-    x: torch.Tensor  # the float32 residual stream (updated in place by each residual unit)
+    x: torch.Tensor  # the residual stream, float16 or float32 (updated in place by each unit)
     u: list[torch.Tensor]  # the bf16 operand of the next conv, two buffers (read while written)
     h: torch.Tensor  # bf16 activation between the two convs of an unfused residual unit
     # blocks whose residual units the fused kernel has no tile for at this shape (short rows with a
     # wide halo): they run as two launches
     unfused_blocks: set[int] = field(default_factory=set)
     front: dict[str, torch.Tensor] = field(default_factory=dict)  # a front's own buffers
+    partials: torch.Tensor | None = None  # x's storage as float32: the split-K partials
     # False once the split-K input conv was refused at this shape (many rows of a few frames:
     # no split tile holds their history rows); the input conv then runs unsplit
     in_conv_split: bool = True
@@ -210,12 +212,18 @@ class DacCodecDecoder:
     ``weights`` is the float32 master weight tree of ``configs.make_dac_weights``;
     ``weight_format`` "bf16" rounds every conv weight to bf16, "fp8" stores E4M3 weights with a
     float32 scale per output channel. Activations between convs are bf16, the residual stream
-    float32, accumulation float32.
+    float16 between launches (``residual_dtype``, or float32), accumulation float32.
     """
 
     def __init__(self, weights: dict[str, Any], config: DacDecoderConfig, *,
                  device: torch.device | str = "cuda", weight_format: str = "bf16",
-                 residual_stacks: bool = True):
+                 residual_stacks: bool = True, residual_dtype: torch.dtype = torch.float16):
+        if residual_dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"the residual stream is float16 or float32, not {residual_dtype}")
+        # the residual stream between launches: float16 by default (as the reference's GPU
+        # decoder keeps it, channels_last_decoder.py:114-122 with decode_dtype float16; every
+        # residual add and the stack's units still run in float32), or float32
+        self.residual_dtype = residual_dtype
         self.config = config
         self.device = torch.device(device)
         self.weight_format = weight_format
@@ -334,18 +342,26 @@ class DacCodecDecoder:
         if ws is None:
             dev = self.device
             length = frames * self.front_upsample
-            # x also holds the input conv's split-K partials
-            largest = length * self.in_conv.conv.n_cols * self.in_conv_splits
+            largest = length * self.in_conv.conv.n_cols
+            # x also holds the input conv's float32 split-K partials
+            partials = largest * self.in_conv_splits if self.in_conv_splits > 1 else 0
+            x_elems = 0
             for blk in self.blocks:
                 length *= blk.stride
                 largest = max(largest, length * blk.c_out)
+                x_elems = max(x_elems, length * blk.c_out)
+            size = self.residual_dtype.itemsize
+            x_elems = max(x_elems, -(-partials * 4 // size))
+            x_elems += x_elems % 2  # whole float32 words
+            x = torch.empty(batch * x_elems, dtype=self.residual_dtype, device=dev)
             ws = _Workspace(
                 z=None if self.codebooks is None else
                 torch.empty(batch, frames, self.codebooks.shape[2], dtype=torch.bfloat16,
                             device=dev),
-                x=torch.empty(batch * largest, dtype=torch.float32, device=dev),
+                x=x,
                 u=[torch.empty(batch * largest, dtype=torch.bfloat16, device=dev) for _ in range(2)],
                 h=torch.empty(batch * largest, dtype=torch.bfloat16, device=dev),
+                partials=x.view(torch.float32),
             )
             self._workspaces[key] = ws
         return ws
@@ -399,7 +415,7 @@ class DacCodecDecoder:
             if split:
                 # the partials go to the residual-stream buffer, unused until the first up conv
                 try:
-                    splitk_conv(z, ic.conv, u, k_splits=self.in_conv_splits, workspace=ws.x,
+                    splitk_conv(z, ic.conv, u, k_splits=self.in_conv_splits, workspace=ws.partials,
                                 activation=snake, act_a=ic.out_a, act_b=ic.out_b,
                                 **hist(ic.name))
                 except N.OmniCodecError as err:

@@ -146,9 +146,10 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
 
     def __init__(self, state: dict[str, torch.Tensor], config: Qwen3Code2WavConfig, *,
                  device: torch.device | str = "cuda", weight_format: str = "bf16",
-                 residual_stacks: bool = True):
+                 residual_stacks: bool = True, residual_dtype: torch.dtype = torch.float16):
         super().__init__(conv_stack_tree(state, config), config, device=device,
-                         weight_format=weight_format, residual_stacks=residual_stacks)
+                         weight_format=weight_format, residual_stacks=residual_stacks,
+                         residual_dtype=residual_dtype)
         cfg = config
         dev = self.device
         if cfg.head_dim != 64:
@@ -491,11 +492,11 @@ class Qwen3TTSCodecDecoder(Qwen3Code2WavDecoder):
 
     def __init__(self, state: dict[str, torch.Tensor], config: Qwen3TTSCodecConfig, *,
                  device: torch.device | str = "cuda", weight_format: str = "bf16",
-                 residual_stacks: bool = True):
+                 residual_stacks: bool = True, residual_dtype: torch.dtype = torch.float16):
         if getattr(config, "transconv_trim", "right") != "right":
             raise ValueError("the Qwen3-TTS decoder trims its transposed convs on the right")
         super().__init__(state, config, device=device, weight_format=weight_format,
-                         residual_stacks=residual_stacks)
+                         residual_stacks=residual_stacks, residual_dtype=residual_dtype)
         self.total_upsample = config.hop_length
         self.compiled_shapes: set[tuple[int, int]] = set()
 
