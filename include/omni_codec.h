@@ -100,8 +100,8 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 9: float16 residual streams (omni_conv_args.residual_dtype,
-                                      omni_residual_stack_args.x_dtype) */
+int omni_codec_abi_version(void); /* 10: omni_gemm (the code2wav front's linear layers with their
+                                       elementwise epilogues) */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -612,6 +612,53 @@ int omni_bias_scale_residual(float* r, int64_t rows, int64_t channels, const voi
                              int64_t out_stride, omni_stream_t stream);
 int omni_advance_positions(int64_t* positions, int64_t num_slots, const int64_t* slot_index,
                            int64_t rows, int64_t new_frames, int cold, omni_stream_t stream);
+
+/*
+ * omni_gemm: out = epilogue(a [rows][k] x w^T) for the code2wav front's linear layers, w [n][k]
+ * bf16 contiguous (a linear layer's weight [out_features][in_features]), a bf16 rows a_stride
+ * elements apart, float32 accumulation over k in one fixed order whatever rows is (a row's result
+ * does not depend on the rows batched with it). bias (float32 [n], optional) is added to the
+ * accumulator first. Epilogues:
+ *   OMNI_GEMM_STORE            out bf16 [rows][n] = acc + bias
+ *     (F.linear(normed, qkv_weight), sglang_omni/models/qwen3_omni/components/code2wav.py:267)
+ *   OMNI_GEMM_SILU_MUL         out bf16 [rows][n / 2]: w's rows interleaved in blocks of 16,
+ *     block 2q the gate rows 16q .. 16q + 15 and block 2q + 1 the matching up rows; out[row, i] =
+ *     silu(gate_i) * up_i (silu_and_mul(F.linear(normed, gate_up_weight)), code2wav.py:321)
+ *   OMNI_GEMM_GELU             out bf16 [rows][n] = GELU(acc + bias), erf form
+ *     (act(pwconv1(normed)), qwen3_omni/components/incremental_codec.py:174-176)
+ *   OMNI_GEMM_SCALED_RESIDUAL  out [rows][n] = residual + scale[c] * (acc + bias), one float32
+ *     fma per element, stored as float32 or rounded to bf16 (out_dtype); residual (float32) may
+ *     be out itself (addcmul(residual, layer_scale, F.linear(...)), code2wav.py:311-326;
+ *     residual + gamma * pwconv2(...), incremental_codec.py:174-180)
+ * out_dtype is OMNI_DTYPE_BF16, or OMNI_DTYPE_F32 for the scaled residual.
+ * k a multiple of 64, n of 64; a, w, bias, residual and scale 16-byte aligned with 16-byte row
+ * strides; out rows 8-byte (bf16) or 16-byte (float32) aligned. config 0 picks the tile; 1 - 6
+ * force one (1: 64 x 128 of 4 waves, 2: 64 x 64 of 4, 3: 64 x 128 of 8, 4: 64 x 64 of 8 (not
+ * for SILU_MUL), 5: 32 x 64 of 4, 6: 64 x 128 of 8 as 4 x 2; columns a multiple of the tile's,
+ * else OMNI_ERR_UNSUPPORTED). Every tile gives the same bits. rows = 0 does nothing.
+ */
+enum {
+  OMNI_GEMM_STORE = 0,
+  OMNI_GEMM_SILU_MUL = 1,
+  OMNI_GEMM_GELU = 2,
+  OMNI_GEMM_SCALED_RESIDUAL = 3
+};
+typedef struct omni_gemm_args {
+  const void* a;
+  int64_t a_stride;
+  const void* w;
+  int64_t rows, k, n;
+  const float* bias;
+  int epilogue;
+  int out_dtype;
+  int config;
+  const float* scale;
+  const float* residual;
+  int64_t residual_stride;
+  void* out;
+  int64_t out_stride;
+} omni_gemm_args;
+int omni_gemm(const omni_gemm_args* args, omni_stream_t stream);
 
 /*
  * omni_channel_embedding_sum: MOSS-TTS's fused multi-channel embedding

@@ -41,7 +41,7 @@ class OmniCodecError(RuntimeError):
 
 INVALID_ARG = 1
 UNSUPPORTED = 2
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # kernel families of omni_conv1d_fused (omni_conv1d_plan / omni_conv1d_fused_with)
 CONV_KERNEL_AUTO, CONV_KERNEL_DMA, CONV_KERNEL_STAGED, CONV_KERNEL_STAGED11, CONV_KERNEL_FUSED_UNIT = range(5)
@@ -167,6 +167,30 @@ class ResidualStackArgs(ctypes.Structure):
     ]
 
 
+class GemmArgs(ctypes.Structure):
+    """Mirror of ``omni_gemm_args`` in include/omni_codec.h."""
+
+    _fields_ = [
+        ("a", ctypes.c_void_p),
+        ("a_stride", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("bias", ctypes.c_void_p),
+        ("epilogue", ctypes.c_int),
+        ("out_dtype", ctypes.c_int),
+        ("config", ctypes.c_int),
+        ("scale", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
+        ("residual_stride", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("out_stride", ctypes.c_int64),
+    ]
+
+
+GEMM_STORE, GEMM_SILU_MUL, GEMM_GELU, GEMM_SCALED_RESIDUAL = 0, 1, 2, 3
+
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _PTR = ctypes.c_void_p
@@ -222,6 +246,7 @@ SIGNATURES: dict[str, list] = {
     "omni_bias_gelu": [_PTR, _I64, _I64, _I64, _PTR, _PTR],
     "omni_bias_scale_residual": [_PTR, _I64, _I64, _PTR, _I64, _PTR, _PTR, _PTR, _I64, _PTR],
     "omni_advance_positions": [_PTR, _I64, _PTR, _I64, _I64, _INT, _PTR],
+    "omni_gemm": [ctypes.POINTER(GemmArgs), _PTR],
     "omni_channel_embedding_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _PTR, _PTR, _INT, _I64, _PTR,
                                    _PTR],
 }

@@ -12,27 +12,26 @@ A decode step on channels-last activations:
     rvq_gather_sum (mean form)            codes -> h (float32 residual stream)
     per layer (8):
       rms_norm_residual                   h -> normed (bf16)
-      GEMM qkv (k = 1 conv kernel)        normed -> qkv
+      GEMM qkv                            normed -> qkv
       rope_kv_write                       rotary on q, k in place; new K / V into the rings
       window_attention                    q over the 72-frame window -> attn
-      GEMM o                              attn -> o
-      rms_norm_residual                   h += scale * o; normed = RMSNorm(h)
-      GEMM gate_up, silu_mul, GEMM down   normed -> d
-      rms_norm_residual                   h += scale * d; normed = RMSNorm(h) (next layer / final)
+      GEMM o, scaled residual epilogue    h += scale * (attn @ W_o^T)
+      rms_norm_residual                   normed = RMSNorm(h)
+      GEMM gate_up, silu_mul epilogue     normed -> act = silu(gate) * up
+      GEMM down, scaled residual epilogue h += scale * (act @ W_down^T)
+      rms_norm_residual                   normed = RMSNorm(h) (next layer / final)
     per upsampler (x2, x2):
       conv_dma (transposed, k = s)        normed -> r (float32, bias included)
       dwconv_layernorm                    r -> n (bf16; depthwise causal k7 with slot history)
-      GEMM pwconv1, bias_gelu, GEMM pwconv2, bias_scale_residual
-                                          r += gamma * (...); the next operand (bf16)
+      GEMM pwconv1, GELU epilogue         n -> p (bf16)
+      GEMM pwconv2, scaled residual epilogue
+                                          the next operand r + gamma * (p @ W2^T + b2) (bf16)
     the causal conv stack of ``DacCodecDecoder`` with SnakeBeta coefficients, transposed convs
     trimmed on both sides and the final clamp.
 
-The GEMMs run on the LDS-DMA conv kernel as k = 1 convs (the linear weight [out, in] packed once
-as a conv weight [out, in, 1]): bf16 operands, float32 accumulation in a fixed order (32-input
-chunks ascending; for the layers with long inputs and few outputs, split-K: slices of the input
-chunks summed in slice order, the slice count fixed per layer by its shape), rounded once to the
-bf16 output. The order does not depend on the row count, so a stream decoded in chunks gives the
-bits of its whole decode.
+The GEMMs run on ``omni_gemm`` (kernels/gemm.py): bf16 operands, float32 accumulation over the
+input features in one fixed order whatever the row count, the elementwise pass after each GEMM
+on the accumulators. So a stream decoded in chunks gives the bits of its whole decode.
 """
 
 from __future__ import annotations
@@ -43,7 +42,8 @@ from typing import Any
 import torch
 
 from ..kernels import code2wav_front as F
-from ..kernels.conv import fused_conv, gemm, pack_conv1d, pack_conv_transpose1d
+from ..kernels.conv import fused_conv, pack_conv1d, pack_conv_transpose1d
+from ..kernels.gemm import GELU, SCALED_RESIDUAL, linear, pack_linear
 from ..kernels.rvq import rvq_gather_sum
 from .configs import Qwen3Code2WavConfig, Qwen3TTSCodecConfig
 from .dac_codec import CodecStatePool, DacCodecDecoder, _Workspace
@@ -111,31 +111,6 @@ class Code2WavStatePool(CodecStatePool):
         self.frame_positions.index_fill_(0, slots, 0)
 
 
-def _k_splits(k: int, n: int) -> int:
-    """The split-K slice count of a [rows, k] x [k, n] GEMM, from its shape alone (never the row
-    count, which the summation order must not depend on): the layers with few output columns per
-    input take more slices, so that their few column tiles spread over more workgroups."""
-    splits = 1 if n >= 4096 else (4 if k >= 3072 else (2 if n >= 3072 else 4))
-    while splits > 1 and k % (64 * splits):  # each slice whole pairs of 32-channel chunks
-        splits //= 2
-    return splits
-
-
-def _linear(weight: torch.Tensor, device: torch.device):
-    """A linear layer's weight [out, in] as a packed k = 1 conv (bf16, no bias), with the split-K
-    slice count of its shape (``k_splits``)."""
-    packed = pack_conv1d(weight.float()[..., None], None).to(device)
-    packed.k_splits = _k_splits(weight.shape[1], weight.shape[0])
-    return packed
-
-
-def _gemm(x: torch.Tensor, packed, out: torch.Tensor, workspace: torch.Tensor) -> None:
-    """out [rows, out] (bf16) = x [rows, in] (bf16) @ W^T on the k = 1 conv kernel."""
-    rows = x.shape[0]
-    gemm(x.view(1, rows, x.shape[1]), packed, out.view(1, rows, out.shape[1]),
-         k_splits=packed.k_splits, workspace=workspace)
-
-
 class Qwen3Code2WavDecoder(DacCodecDecoder):
     """Qwen3-Omni code2wav on gfx950 HIP kernels (the transformer's and ConvNeXt's GEMMs as k = 1
     convs on the LDS-DMA conv kernel). ``state`` is a
@@ -197,15 +172,15 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             qkv = torch.cat([state[f"{p}.self_attn.{n}_proj.weight"] for n in "qkv"], dim=0)
             gate_up = torch.cat([state[f"{p}.mlp.gate_proj.weight"],
                                  state[f"{p}.mlp.up_proj.weight"]], dim=0)
-            # GEMM weights [out, in] packed as k = 1 convs (bf16)
+            # GEMM weights [out, in] as bf16 rows (gate / up interleaved for the silu epilogue)
             self.layers.append({
                 "in_norm": f32(state[f"{p}.input_layernorm.weight"]),
-                "qkv": _linear(qkv, dev),
-                "o": _linear(state[f"{p}.self_attn.o_proj.weight"], dev),
+                "qkv": pack_linear(qkv).to(dev),
+                "o": pack_linear(state[f"{p}.self_attn.o_proj.weight"]).to(dev),
                 "attn_scale": f32(state[f"{p}.self_attn_layer_scale.scale"]),
                 "post_norm": f32(state[f"{p}.post_attention_layernorm.weight"]),
-                "gate_up": _linear(gate_up, dev),
-                "down": _linear(state[f"{p}.mlp.down_proj.weight"], dev),
+                "gate_up": pack_linear(gate_up, gated=True).to(dev),
+                "down": pack_linear(state[f"{p}.mlp.down_proj.weight"]).to(dev),
                 "mlp_scale": f32(state[f"{p}.mlp_layer_scale.scale"]),
             })
         self.final_norm = f32(state["pre_transformer.norm.weight"])
@@ -226,10 +201,10 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                 "dw_bias": f32(state[f"{p}.dwconv.conv.bias"]),
                 "ln_weight": f32(state[f"{p}.norm.weight"]),
                 "ln_bias": f32(state[f"{p}.norm.bias"]),
-                "w1": _linear(state[f"{p}.pwconv1.weight"], dev),
-                "b1": f32(state[f"{p}.pwconv1.bias"]),
-                "w2": _linear(state[f"{p}.pwconv2.weight"], dev),
-                "b2": f32(state[f"{p}.pwconv2.bias"]),
+                "w1": pack_linear(state[f"{p}.pwconv1.weight"],
+                                  state[f"{p}.pwconv1.bias"]).to(dev),
+                "w2": pack_linear(state[f"{p}.pwconv2.weight"],
+                                  state[f"{p}.pwconv2.bias"]).to(dev),
                 "gamma": f32(state[f"{p}.gamma"]),
             })
             if self.upsamplers[-1]["up"].taps != 1:
@@ -266,14 +241,11 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
         m = batch * frames
         bf = torch.bfloat16
         width = self.q_width + 2 * self.kv_width
-        big = max(m * 2 * cfg.intermediate_size, m * width)
         buf = {
             "h": torch.empty(m, c, dtype=torch.float32, device=dev),
             "normed": torch.empty(m, c, dtype=bf, device=dev),
             "qkv": torch.empty(m, width, dtype=bf, device=dev),
             "attn": torch.empty(m, self.q_width, dtype=bf, device=dev),
-            "proj": torch.empty(m, c, dtype=bf, device=dev),
-            "wide": torch.empty(big, dtype=bf, device=dev),
             "act": torch.empty(m, cfg.intermediate_size, dtype=bf, device=dev),
         }
         if self.split_rvq:
@@ -285,18 +257,9 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             length *= up["factor"]
             buf[f"r{i}"] = torch.empty(batch, length, u, dtype=torch.float32, device=dev)
             buf[f"n{i}"] = torch.empty(batch, length, u, dtype=bf, device=dev)
-            buf[f"p1_{i}"] = torch.empty(batch * length, 4 * u, dtype=bf, device=dev)
-            buf[f"p2_{i}"] = torch.empty(batch * length, u, dtype=bf, device=dev)
+            buf[f"p1_{i}"] = torch.empty(batch * length, up["w1"].out_features, dtype=bf,
+                                          device=dev)
             buf[f"z{i}"] = torch.empty(batch, length, u, dtype=bf, device=dev)
-        # the split-K GEMMs' float32 partials: the largest slices x rows x columns of any site
-        sites = [(m, layer[name]) for layer in self.layers for name in ("qkv", "o", "gate_up", "down")]
-        length = frames
-        for up in self.upsamplers:
-            length *= up["factor"]
-            sites += [(batch * length, up["w1"]), (batch * length, up["w2"])]
-        need = max((p.k_splits * rows * p.n_cols for rows, p in sites if p.k_splits > 1),
-                   default=0)
-        buf["splitk"] = torch.empty(max(need, 4), dtype=torch.float32, device=dev)
         ws.front.update(buf)
         return ws.front
 
@@ -318,8 +281,7 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                 raise ValueError(f"{frames} new frames overflow the pool's {pool.ring_frames}-frame "
                                  f"rings (window {pool.retained_frames} + new frames)")
         h, normed, qkv = buf["h"], buf["normed"], buf["qkv"]
-        attn, proj, act = buf["attn"], buf["proj"], buf["act"]
-        gate_up = buf["wide"][: m * 2 * cfg.intermediate_size].view(m, 2 * cfg.intermediate_size)
+        attn, act = buf["attn"], buf["act"]
         k_books, _, dim = self.code_tables.shape
         tab = self.code_tables.element_size()
         with timer.launch("rvq", m * (k_books * dim * tab + dim * 4 + k_books * codes.element_size())):
@@ -352,7 +314,7 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                         "key_ring": pool.keys[i], "value_ring": pool.values[i],
                         "ring_frames": pool.ring_frames}
             with timer.launch("front_gemm", 2.0 * m * c * qkv.shape[1]):
-                _gemm(normed, layer["qkv"], qkv, buf["splitk"])
+                linear(normed, layer["qkv"], qkv)
             with timer.launch("front_elementwise", 0.0):
                 F.rope_kv_write(qkv, batch, heads, kv_heads, hd, self.inv_freq, cold=cold, **ring)
             # a first decode attends to its own frames: the keys are in qkv already
@@ -360,20 +322,20 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
             with timer.launch("front_attention", 4.0 * m * heads * hd * cfg.sliding_window):
                 F.window_attention(qkv, batch, heads, kv_heads, hd, cfg.sliding_window,
                                    hd ** -0.5, attn, cold=cold, **attend_ring)
+            # h += attn_scale * o(attn), mlp likewise: the scaled residual in the GEMM epilogue
             with timer.launch("front_gemm", 2.0 * m * self.q_width * c):
-                _gemm(attn, layer["o"], proj, buf["splitk"])
+                linear(attn, layer["o"], h, epilogue=SCALED_RESIDUAL, scale=layer["attn_scale"],
+                       residual=h)
             with timer.launch("front_elementwise", 0.0):
-                F.rms_norm_residual(h, layer["post_norm"], eps, normed, delta=proj,
-                                    scale=layer["attn_scale"])
-            with timer.launch("front_gemm", 2.0 * m * c * gate_up.shape[1]):
-                _gemm(normed, layer["gate_up"], gate_up, buf["splitk"])
-            with timer.launch("front_elementwise", 0.0):
-                F.silu_mul(gate_up, act)
+                F.rms_norm_residual(h, layer["post_norm"], eps, normed)
+            with timer.launch("front_gemm", 2.0 * m * c * 2 * act.shape[1]):
+                linear(normed, layer["gate_up"], act)
             with timer.launch("front_gemm", 2.0 * m * act.shape[1] * c):
-                _gemm(act, layer["down"], proj, buf["splitk"])
+                linear(act, layer["down"], h, epilogue=SCALED_RESIDUAL, scale=layer["mlp_scale"],
+                       residual=h)
             nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
             with timer.launch("front_elementwise", 0.0):
-                F.rms_norm_residual(h, nxt, eps, normed, delta=proj, scale=layer["mlp_scale"])
+                F.rms_norm_residual(h, nxt, eps, normed)
         x = normed.view(batch, frames, c)
         if self.output_proj is not None:
             op = self.output_proj
@@ -399,17 +361,14 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                                    up["ln_bias"], LN_EPS, n, **hist)
             rows = batch * length
             u = self.latent
-            p1, p2 = buf[f"p1_{i}"], buf[f"p2_{i}"]
-            with timer.launch("front_gemm", 2.0 * rows * u * 4 * u):
-                _gemm(n.view(rows, u), up["w1"], p1, buf["splitk"])
-            with timer.launch("front_elementwise", 0.0):
-                F.bias_gelu(p1, up["b1"])
-            with timer.launch("front_gemm", 2.0 * rows * 4 * u * u):
-                _gemm(p1, up["w2"], p2, buf["splitk"])
+            p1 = buf[f"p1_{i}"]
+            with timer.launch("front_gemm", 2.0 * rows * u * p1.shape[1]):
+                linear(n.view(rows, u), up["w1"], p1, epilogue=GELU)
+            # the next operand r + gamma * (pwconv2(p1) + b2), rounded once to bf16
             z = buf[f"z{i}"]
-            with timer.launch("front_elementwise", 0.0):
-                F.bias_scale_residual(r.view(rows, u), p2, up["b2"], up["gamma"],
-                                      out=z.view(rows, u))
+            with timer.launch("front_gemm", 2.0 * rows * p1.shape[1] * u):
+                linear(p1, up["w2"], z.view(rows, u), epilogue=SCALED_RESIDUAL,
+                       scale=up["gamma"], residual=r.view(rows, u))
             x = z
         return x, length
 
