@@ -11,12 +11,15 @@
 //     issue a stage's loads in a few instructions. Lane l of a DMA instruction fills the 16-byte
 //     LDS slot 64 * instr + l, so each lane loads the piece that belongs in its slot:
 //       - input rows [rows][32] (64-byte rows): instruction ii stages rows 16 ii .. 16 ii + 15,
-//         lane l the quarter l % 4 of row 16 ii + l / 4; the lane's source is x, the slot's
-//         history copy (rows left of position 0 when streaming, EXEC-masked per source) or
-//         nothing (causal zero padding, written once as zeros into both ring buffers);
-//       - weights [BCO][TAPS * 4 + 1] 16-byte slots per column (taps x 32 channels plus one pad
-//         slot, an odd row pitch, so the 16 column rows an MFMA operand read touches start on
-//         distinct banks); pad slots reload a real piece. E4M3 weights keep their bytes in LDS
+//         lane l slot l % 4 of row r = 16 ii + l / 4, which holds the quarter (l % 4) ^
+//         ((r / 2) % 4) of the row (so an MFMA operand read of 16 consecutive rows from any first
+//         row meets no LDS bank conflict); the lane's source is x, the slot's history copy (rows
+//         left of position 0 when streaming, EXEC-masked per source) or nothing (causal zero
+//         padding, written once as zeros into both ring buffers);
+//       - weights [BCO][TAPS * 4 + 2] 16-byte slots per column (taps x 32 channels plus two pad
+//         slots: a row pitch of 2 mod 4 slots, the pitch at which the 16 column rows an MFMA
+//         operand read touches meet no bank conflict); pad slots reload a real piece. E4M3
+//         weights keep their bytes in LDS
 //         ([BCO][TAPS * 2 + 1] slots, half the LDS bytes per operand read) and are widened to
 //         bf16 (exactly) as the MFMA operand is read; their per-column scale is applied in the
 //         epilogue.
@@ -48,9 +51,11 @@ struct DmaTile {
   static constexpr int BCO = Base::BCO;
   static constexpr int BP = Base::BP;
   static constexpr int NW = NT / 64;
-  // 16-byte slots per weight row: a tap's 32 channels take 4 (bf16) or 2 (E4M3), plus one pad
+  // 16-byte slots per weight row: a tap's 32 channels take 4 (bf16) or 2 (E4M3), plus pads to a
+  // pitch of 2 mod 4 slots (bf16: the pitch whose 16-row operand reads are free of LDS bank
+  // conflicts) or an odd pitch (E4M3, read 8 bytes a lane)
   static constexpr int WSLOTS = TAPS * (W8 ? 2 : 4);
-  static constexpr int P = WSLOTS + 1;
+  static constexpr int P = W8 ? WSLOTS + 1 : WSLOTS + 2;
   static constexpr int NIW = (BCO * P + 63) / 64;  // weight DMA instructions per chunk
   static constexpr int NIX = MAX_ROWS / 16;        // input-row DMA instructions per chunk
   static constexpr int W_PIECES = (NIW + NW - 1) / NW;
@@ -131,12 +136,13 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   const int rows = (m_end - m0) + nseg * halo;
   const int seg_rows = L + halo;
 
-  // Input-row DMA descriptors. Piece u of thread tid is row r = tid / 4 + u * NT / 4, quarter
-  // tid % 4 (instruction ii = wave + u * NW, lane l: row 16 ii + l / 4): its element offset at
-  // channel q8 of chunk 0 in x or in the history pool, its source (2 bits: 0 zeros, 1 x,
-  // 2 history, 3 not staged) and, when it is a sample of the new history this workgroup writes,
-  // its offset there.
-  const int q8 = (tid & 3) * 8;
+  // Input-row DMA descriptors. Piece u of thread tid is LDS slot tid % 4 of row r = tid / 4 +
+  // u * NT / 4 (instruction ii = wave + u * NW, lane l: row 16 ii + l / 4), which holds the row's
+  // channels lq8 .. lq8 + 7, lq8 = 8 ((tid % 4) ^ ((r / 2) % 4)): its element offset at channel
+  // lq8 of chunk 0 in x or in the history pool, its source (2 bits: 0 zeros, 1 x, 2 history,
+  // 3 not staged) and, when it is a sample of the new history this workgroup writes, its offset
+  // there.
+  const int q8 = (tid & 3) * 8;  // the LDS slot's element offset in its row
   int xoff[Tile::X_PIECES];
   int hwoff[Tile::X_PIECES];
   unsigned xmode = 0;
@@ -144,6 +150,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 #pragma unroll
   for (int u = 0; u < Tile::X_PIECES; ++u) {
     const int r = (tid >> 2) + u * (NT / 4);
+    const int lq8 = ((tid & 3) ^ ((r >> 1) & 3)) * 8;
     int off = 0;
     int hw = -1;
     unsigned mode = 3;
@@ -170,10 +177,10 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
         if (slot >= 0) parity = p.slot_parity[slot] & 1;
       }
       if (pos >= 0 && pos < XL) {
-        off = (int)(b * p.x_sb + (int64_t)pos * p.x_st) + q8;
+        off = (int)(b * p.x_sb + (int64_t)pos * p.x_st) + lq8;
         mode = 1;
       } else if (pos < 0 && slot >= 0 && !p.hist_cold) {
-        off = (int)(slot * p.hist_slot_stride + (parity * H + (H + pos)) * (int64_t)c_in) + q8;
+        off = (int)(slot * p.hist_slot_stride + (parity * H + (H + pos)) * (int64_t)c_in) + lq8;
         mode = 2;
       }
       if (may_write_history && slot >= 0 && pos >= XL - H && pos < XL) {
@@ -183,7 +190,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
         const bool owned = pos >= 0 ? (m >= m0 && m < m_end) : row_start;
         if (owned)
           hw = (int)(slot * p.hist_slot_stride + ((1 - parity) * H + (pos - (XL - H))) *
-                                                     (int64_t)c_in) + q8;
+                                                     (int64_t)c_in) + lq8;
       }
     }
     xoff[u] = off;
@@ -352,8 +359,11 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       }
       const int shift = j * dil;
 #pragma unroll
-      for (int t = 0; t < TP; ++t)
-        bv[t] = *reinterpret_cast<const bf16x8*>(xs + (xrow[t] + shift) * kChunk + lk);
+      for (int t = 0; t < TP; ++t) {
+        const int row = xrow[t] + shift;  // its quarter lane / 16 in slot (lane / 16) ^ ((row / 2) % 4)
+        bv[t] = *reinterpret_cast<const bf16x8*>(xs + row * kChunk +
+                                                 ((((lane >> 4) ^ (row >> 1)) & 3) << 3));
+      }
     };
     bf16x8 a[2][TCO], bv[2][TP];
     load_step(0, a[0], bv[0]);

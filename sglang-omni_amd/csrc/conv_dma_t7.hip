@@ -26,7 +26,7 @@ int launch_dma_taps7(const ConvParams& p, bool fp8, Choice& ch, hipStream_t stre
   // HiFiGAN's 128-channel stage: 128 columns x 192 positions, 8 waves of 64 x 48 (the ring fills
   // the 160 KiB)
   if (p.n_cols == 128 && p.k_splits == 1 && !fp8)
-    return launch_first_fit<DmaConfig<2, 4, 4, 3, 320, 7, 1>>(p, ch, stream);
+    return launch_first_fit<DmaConfig<2, 4, 4, 3, 288, 7, 1>>(p, ch, stream);
   if (p.k_splits > 1)  // split-K (bf16 weights): K slices of the 96 x 192 tiles (8 / 4 waves)
     return launch_first_fit<DmaConfig<2, 4, 3, 3, 368, 7, 1, false, true>,
                             DmaConfig<1, 4, 6, 3, 368, 7, 1, false, true>>(p, ch, stream);

@@ -14,12 +14,15 @@
 //     loaded once from HBM (float32, or a float16 residual stream widened exactly), updated in
 //     place by each unit's k = 1 conv.
 //   * the operand u_k = Snake(x_k) and the h tile between the two convs: bf16 in one LDS tile
-//     [C/32][guard + rows][32] (64-byte rows, the 16-byte slots rotated by (row / 4) % 4 so the
-//     accumulator-layout writes and the operand reads both spread over all banks); guard rows
-//     ahead of row 0 keep the taps of the first rows inside the tile.
+//     [C/32][guard + rows][32] (64-byte rows, 16-byte slot s of row r stored at s ^ ((r / 2) % 4),
+//     so an operand read of 16 consecutive rows from any first row meets no bank conflict);
+//     guard rows ahead of row 0 keep the taps of the first rows inside the tile.
 //   * weights: by LDS DMA into a two-buffer ring of stages (a 32-channel chunk of the dilated
 //     conv, or the k = 1 conv), the next stage's DMA running during this stage's MFMAs; bf16
-//     weights as they are, E4M3 weights as bytes widened to bf16 (exactly) when read.
+//     weights as they are (a column's taps in a 256-byte row, 16-byte slot s of column n at
+//     s ^ (n % 16); the k = 1 conv's 64-byte rows swizzled as the operand tile's, so the weight
+//     reads meet no bank conflict either), E4M3 weights as bytes widened to bf16 (exactly) when
+//     read.
 //   * long rows (sweep): a workgroup runs consecutive tiles of one stream row, and each operand's
 //     last halo rows pass from one tile to the next through LDS instead of being recomputed.
 //   * streaming: rows left of position 0 of a stream row take each unit's own history copy (or
@@ -111,7 +114,7 @@ struct StackParams {
 // LDS element offset of 16-byte slot `slot` of staged row `row` (guard included) in chunk kc.
 template <int UROWS>
 __device__ __forceinline__ int uaddr(int kc, int row, int slot) {
-  return (kc * UROWS + row) * kChunk + ((slot ^ ((row >> 2) & 3)) << 3);
+  return (kc * UROWS + row) * kChunk + ((slot ^ ((row >> 1) & 3)) << 3);
 }
 
 // The per-launch coefficient rows in LDS order: per unit kCoefRows rows of C (scale1, bias1,
@@ -157,14 +160,15 @@ struct StackTile {
   static constexpr int GUARD = SWEEP ? kSweepGuard : kGuard;
   static constexpr int UROWS = GUARD + R;
   // LDS DMA ring: two buffers, each holding one stage of weights as they are stored (bf16, or
-  // E4M3 bytes widened when read): the dilated conv's chunk kc ([C][ntaps * 32 elements + one
-  // 16-byte pad], rows an odd multiple of 16 bytes) for taps 0-3 or 4-6 (bf16) or all 7 taps
-  // (E4M3), or the k = 1 conv ([C/32][C][32]); a stage is whole 64-lane DMA instructions of 16
-  // bytes.
+  // E4M3 bytes widened when read): the dilated conv's chunk kc for taps 0-3 or 4-6 (bf16: [C]
+  // rows of 16 slots, slot s of row n at s ^ (n % 16), taps 4-6 using 12 of them) or all 7 taps
+  // (E4M3: [C][7 * 32 bytes + one 16-byte pad], an odd multiple of 16 bytes), or the k = 1 conv
+  // ([C/32][C][32]; bf16 rows swizzled as the operand tile's); a stage is whole 64-lane DMA
+  // instructions of 16 bytes.
   static constexpr int WE = W8 ? 1 : 2;              // bytes per weight
-  static constexpr int P_LO = W8 ? 7 * 2 + 1 : 4 * 4 + 1;  // 16-byte slots per weight row,
-                                                     // taps 0-6 (E4M3) or 0-3 (bf16), +1 pad
-  static constexpr int P_HI = 3 * 4 + 1;             // bf16 taps 4-6
+  static constexpr int P_LO = W8 ? 7 * 2 + 1 : 16;   // 16-byte slots per weight row, taps 0-6
+                                                     // (E4M3, +1 pad) or 0-3 (bf16)
+  static constexpr int P_HI = 16;                    // bf16 taps 4-6
   static constexpr int RING_SLOTS = (C * P_LO + 63) / 64 * 64;
   static constexpr int RING_ELEMS = RING_SLOTS * 8;
   static constexpr int W2_SLOTS = CH * C * 2 * WE;   // the k = 1 conv's weights
@@ -287,14 +291,15 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   constexpr int HI_PER_WAVE = (HI_INSTRS + NWAVES - 1) / NWAVES;
   uint32_t lo_off[LO_PER_WAVE], hi_off[HI_PER_WAVE > 0 ? HI_PER_WAVE : 1];
   {
-    // slot j of column row n holds bytes j * 16 .. of the column's taps t0 .. t0 + nt - 1
-    // (packed [C][7][32] per chunk)
+    // slot j of column row n holds bytes s * 16 .. of the column's taps t0 .. t0 + nt - 1
+    // (packed [C][7][32] per chunk), s = j (E4M3) or j ^ (n % 16) (bf16)
     auto slot_offset = [&](int di, int P, int t0, int nt) __attribute__((always_inline)) {
       const int slot = di * 64 + lane;
       const int n = slot / P;
       const int j = slot - n * P;
-      return (n < C && j < nt * 2 * Tile::WE)
-                 ? (uint32_t)((n * kTaps + t0) * kChunk * Tile::WE + j * 16) : 0u;
+      const int s = W_FP8 ? j : j ^ (n & 15);
+      return (n < C && s < nt * 2 * Tile::WE)
+                 ? (uint32_t)((n * kTaps + t0) * kChunk * Tile::WE + s * 16) : 0u;
     };
 #pragma unroll
     for (int i = 0; i < LO_PER_WAVE; ++i)
@@ -336,10 +341,13 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 #pragma unroll
         for (int i = 0; i < (W2_INSTRS + NWAVES - 1) / NWAVES; ++i) {
           const int di = wave + i * NWAVES;
+          // bf16: slot s of 64-byte row r (four slots) holds piece s ^ ((r / 2) % 4) of the row
+          const int slot = di * 64 + lane;
+          const int src = W_FP8 ? slot : (slot ^ ((slot >> 3) & 3));
           if (di < W2_INSTRS)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rs, (__attribute__((address_space(3))) void*)(buf + di * 64 * 8), 16,
-                (int)((uint32_t)(di * 64 + lane) * 16u), 0, 0, 0);
+                (int)((uint32_t)src * 16u), 0, 0, 0);
         }
       }
     }
@@ -353,10 +361,10 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   };
 
   // LDS addressing of the operand tile from the accumulator layout. Staged rows of this lane are
-  // row0 + 16 t, so the slot rotation (row / 4) % 4 is row0's for every t: each access is a
+  // row0 + 16 t, so the slot swizzle (row / 2) % 4 is row0's for every t: each access is a
   // per-lane base plus a compile-time offset.
   const int row0 = GUARD + wave_p * TP * 16 + lrow;  // staged row of t = 0 (guard included)
-  const int sw = (row0 >> 2) & 3;
+  const int sw = (row0 >> 1) & 3;
   // columns n = c * 16 + (lane / 16) * 4 .. + 3 of the lane: chunk c / 2, 16-byte slot
   // 2 * (c % 2) + lane / 32, element (lane / 16 % 2) * 4 within the slot
   const int put_base0 = row0 * kChunk + ((((lane >> 5)) ^ sw) << 3) + ((lane >> 4) & 1) * 4;
@@ -520,7 +528,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
 #pragma unroll
       for (int t = 0; t < TP; ++t) acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     {
-      // One weight stage of NTAPS taps, software-pipelined in a fixed issue order. The stage's
+      // One weight stage of NTAPS taps (E4M3 weights), software-pipelined in a fixed issue order. The stage's
       // weight tiles (tap-major, then column tile) pass through a ring of three registers: tile
       // i + 3 is read as soon as tile i's TP MFMAs have issued, two column tiles ahead of its
       // use; the next tap's TP operand tiles go to the second of two buffers while the current
@@ -533,7 +541,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         constexpr int NTAPS = decltype(ntaps)::value;
         constexpr int NTILES = NTAPS * TCO;
         // u16 elements per weight row of the stage
-        constexpr int P8 = (W_FP8 ? Tile::P_LO : NTAPS * 4 + 1) * 8;
+        constexpr int P8 = Tile::P_LO * 8;
         using WRaw = typename std::conditional<W_FP8, u32x2, bf16x8>::type;
         auto load_a = [&](int i) __attribute__((always_inline)) -> WRaw {
           const int jj = i / TCO;
@@ -548,7 +556,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         };
         auto load_b = [&](int jj, bf16x8 (&b)[TP]) __attribute__((always_inline)) {
           const int rj = row0 + (t0 + jj) * d - h;
-          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+          const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 1) & 3)) << 3);
 #pragma unroll
           for (int t = 0; t < TP; ++t)
             b[t] = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
@@ -587,20 +595,26 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         } else {
           // bf16 weights (taps 0-3 or 4-6 of the chunk; the lane's 8 weights of a tap: 16
           // bytes): one loop over the stage's taps, each reading its TP operand tiles and TCO
-          // weight tiles before its first MFMA, one LDS wait per tap (a pipelined, unrolled stage
-          // needs more registers than two waves per SIMD have beside the bf16 stages' addresses)
+          // weight tiles before its first MFMA, one LDS wait per tap (the pipelined stage above
+          // needs more registers than two waves per SIMD have with bf16 weights: 256 VGPRs and
+          // 368 bytes of spills)
           const int t0 = (r & 1) ? 4 : 0;
           const int nt = (r & 1) ? 3 : 4;
-          const int P8 = (nt * 4 + 1) * 8;  // u16 elements per weight row
-          const u16* wtap = wbuf + (wco0 + lrow) * P8 + lk;
+          constexpr int P8 = Tile::P_LO * 8;  // u16 elements per weight row
+          // tap jj's slot 4 jj + lane / 16 of column row n sits at (4 jj + lane / 16) ^ (n % 16),
+          // and n % 16 = lrow in every column tile
+          const u16* wrow = wbuf + (wco0 + lrow) * P8;
+          const int wq = ((lane >> 4) ^ lrow) & 3;
+          const int wt = lrow >> 2;
 #pragma unroll 1
           for (int jj = 0; jj < nt; ++jj) {
             const int rj = row0 + (t0 + jj) * d - h;
-            const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 2) & 3)) << 3);
+            const int bj = rj * kChunk + (((lane >> 4) ^ ((rj >> 1) & 3)) << 3);
             bf16x8 bv[TP], a[TCO];
 #pragma unroll
             for (int t = 0; t < TP; ++t)
               bv[t] = *reinterpret_cast<const bf16x8*>(ukc + bj + t * 16 * kChunk);
+            const u16* wtap = wrow + ((((jj ^ wt) << 2) | wq) << 3);
 #pragma unroll
             for (int c = 0; c < TCO; ++c) a[c] = *reinterpret_cast<const bf16x8*>(wtap + c * 16 * P8);
 #pragma unroll
@@ -610,7 +624,6 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
                 acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv[t], acc[c][t], 0, 0, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, TP + TCO, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, TP * TCO, 0);
-            wtap += kChunk;  // one tap: 32 weights
           }
         }
       }
@@ -651,8 +664,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
         if constexpr (W_FP8)  // the ring holds the E4M3 bytes: 32 per row
           a[c] = __builtin_bit_cast(bf16x8, fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(
                                                 w2s + row * (kChunk / 2) + lk / 2)));
-        else
-          a[c] = *reinterpret_cast<const bf16x8*>(w2s + row * kChunk + lk);
+        else  // slot lane / 16 of row `row` at (lane / 16) ^ ((row / 2) % 4)
+          a[c] = *reinterpret_cast<const bf16x8*>(
+              w2s + row * kChunk + ((((lane >> 4) ^ (row >> 1)) & 3) << 3));
       }
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
@@ -792,9 +806,9 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     for (int t = 0; t < TP; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     {
       const int rt = GUARD + wave_p * TP * 16 + (ln & 15);
-      const int bt = rt * kChunk + (((ln >> 4) ^ ((rt >> 2) & 3)) << 3);
+      const int bt = rt * kChunk + (((ln >> 4) ^ ((rt >> 1) & 3)) << 3);
       const int rg = GUARD - 16 + (ln & 15);
-      const int bg = rg * kChunk + (((ln >> 4) ^ ((rg >> 2) & 3)) << 3);
+      const int bg = rg * kChunk + (((ln >> 4) ^ ((rg >> 1) & 3)) << 3);
 #pragma unroll
       for (int kc = 0; kc < CH; ++kc) {
         const bf16x8 a = fin_a[kc];
