@@ -13,7 +13,8 @@
 //       - input rows [rows][32] (64-byte rows): instruction ii stages rows 16 ii .. 16 ii + 15,
 //         lane l slot l % 4 of row r = 16 ii + l / 4, which holds the quarter (l % 4) ^
 //         ((r / 2) % 4) of the row (so an MFMA operand read of 16 consecutive rows from any first
-//         row meets no LDS bank conflict); the lane's source is x, the slot's history copy (rows
+//         row meets no LDS bank conflict; bf16 tiles of a two-buffer ring), or the quarter l % 4
+//         (the others); the lane's source is x, the slot's history copy (rows
 //         left of position 0 when streaming, EXEC-masked per source) or nothing (causal zero
 //         padding, written once as zeros into both ring buffers);
 //       - weights [BCO][TAPS * 4 + 2] 16-byte slots per column (taps x 32 channels plus two pad
@@ -143,6 +144,10 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
   // 3 not staged) and, when it is a sample of the new history this workgroup writes, its offset
   // there.
   const int q8 = (tid & 3) * 8;  // the LDS slot's element offset in its row
+  // (the swizzle's address arithmetic on each operand read costs the one-buffer-ring tiles,
+  // sized for four workgroups per CU, and the 16-wave E4M3 tile spills: they keep the quarters
+  // in order)
+  constexpr bool kSwizzle = OCC == 0 && !W8;
   int xoff[Tile::X_PIECES];
   int hwoff[Tile::X_PIECES];
   unsigned xmode = 0;
@@ -150,7 +155,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 #pragma unroll
   for (int u = 0; u < Tile::X_PIECES; ++u) {
     const int r = (tid >> 2) + u * (NT / 4);
-    const int lq8 = ((tid & 3) ^ ((r >> 1) & 3)) * 8;
+    const int lq8 = kSwizzle ? ((tid & 3) ^ ((r >> 1) & 3)) * 8 : q8;
     int off = 0;
     int hw = -1;
     unsigned mode = 3;
@@ -361,8 +366,8 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
         const int row = xrow[t] + shift;  // its quarter lane / 16 in slot (lane / 16) ^ ((row / 2) % 4)
-        bv[t] = *reinterpret_cast<const bf16x8*>(xs + row * kChunk +
-                                                 ((((lane >> 4) ^ (row >> 1)) & 3) << 3));
+        bv[t] = *reinterpret_cast<const bf16x8*>(
+            xs + row * kChunk + (kSwizzle ? ((((lane >> 4) ^ (row >> 1)) & 3) << 3) : lk));
       }
     };
     bf16x8 a[2][TCO], bv[2][TP];

@@ -35,9 +35,10 @@ struct FusedDmaTile {
   static constexpr int BP = Base::BP;    // 192 positions
   static constexpr int NW = NT / 64;
   static constexpr int CH = BCO / kChunk;
-  // 16-byte slots per weight row of a 4-tap / 3-tap stage (plus one pad slot: odd row pitch)
-  static constexpr int P4 = 4 * 4 + 1;
-  static constexpr int P3 = 3 * 4 + 1;
+  // 16-byte slots per weight row of a 4-tap / 3-tap stage, plus two pad slots: a pitch of 2 mod 4
+  // slots, at which the 16 column rows of an MFMA operand read meet no LDS bank conflict
+  static constexpr int P4 = 4 * 4 + 2;
+  static constexpr int P3 = 3 * 4 + 2;
   static constexpr int NIW4 = (BCO * P4 + 63) / 64;  // weight DMA instructions of a stage
   static constexpr int NIW3 = (BCO * P3 + 63) / 64;
   static constexpr int W4_PIECES = (NIW4 + NW - 1) / NW;
@@ -103,10 +104,12 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
   const int rows = (m_end - m0) + nseg * halo;
   const int seg_rows = L + halo;
 
-  // Input-row DMA descriptors, as conv_dma_kernel's: piece u of thread tid is staged row
-  // r = tid / 4 + u * NT / 4, quarter tid % 4; its element offset at channel q8 of chunk 0 in x
-  // or in the history pool, its source (2 bits: 0 zeros, 1 x, 2 history, 3 not staged) and, when
-  // it is a sample of the new history this workgroup writes, its offset there.
+  // Input-row DMA descriptors, as conv_dma_kernel's but with the quarters in order (the swizzle's
+  // address arithmetic on every operand read costs this kernel registers it does not have):
+  // piece u of thread tid is staged row r = tid / 4 + u * NT / 4, quarter tid % 4; its element
+  // offset at channel q8 of chunk 0 in x or in the history pool, its source (2 bits: 0 zeros,
+  // 1 x, 2 history, 3 not staged) and, when it is a sample of the new history this workgroup
+  // writes, its offset there.
   const int q8 = (tid & 3) * 8;
   int xoff[Tile::X_PIECES];
   int hwoff[Tile::X_PIECES];
@@ -115,6 +118,7 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
   for (int u = 0; u < Tile::X_PIECES; ++u) {
     const int r = (tid >> 2) + u * (NT / 4);
+    const int lq8 = q8;
     int off = 0;
     int hw = -1;
     unsigned mode = 3;
@@ -141,10 +145,10 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
         if (slot >= 0) parity = p.slot_parity[slot] & 1;
       }
       if (pos >= 0 && pos < XL) {
-        off = (int)(b * p.x_sb + (int64_t)pos * p.x_st) + q8;
+        off = (int)(b * p.x_sb + (int64_t)pos * p.x_st) + lq8;
         mode = 1;
       } else if (pos < 0 && slot >= 0 && !p.hist_cold) {
-        off = (int)(slot * p.hist_slot_stride + (parity * H + (H + pos)) * (int64_t)BCO) + q8;
+        off = (int)(slot * p.hist_slot_stride + (parity * H + (H + pos)) * (int64_t)BCO) + lq8;
         mode = 2;
       }
       if (may_write_history && slot >= 0 && pos >= XL - H && pos < XL) {
@@ -152,7 +156,7 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
         const bool owned = pos >= 0 ? (m >= m0 && m < m_end) : row_start;
         if (owned)
           hw = (int)(slot * p.hist_slot_stride + ((1 - parity) * H + (pos - (XL - H))) *
-                                                     (int64_t)BCO) + q8;
+                                                     (int64_t)BCO) + lq8;
       }
     }
     xoff[u] = off;
@@ -243,15 +247,18 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
       }
     }
   };
-  // W2 ([C/32][C][32] as stored) into ring buffer b, a contiguous copy.
+  // W2 ([C/32][C][32] as stored) into ring buffer b: 64-byte rows, slot s of row r holding the
+  // row's piece s ^ ((r / 2) % 4)
   auto issue_w2 = [&](int b) __attribute__((always_inline)) {
     u16* w2s = buf_of(b);
 #pragma unroll
     for (int u = 0; u < Tile::W2_PIECES; ++u) {
       const int iw = wave + u * NW;
+      const int slot = iw * 64 + lane;
       if (iw < Tile::NIW2)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(w2_rsrc, (lds_ptr_t)(w2s + iw * 64 * 8), 16,
-                                                 (int)((uint32_t)(iw * 64 + lane) * 16u), 0, 0, 0);
+                                                 (int)((uint32_t)(slot ^ ((slot >> 3) & 3)) * 16u),
+                                                 0, 0, 0);
     }
   };
   // The new history samples of chunk kc (its input rows in buffer b), from LDS to the slot's
@@ -357,7 +364,7 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
       o.x = pack_bf16x2(y[0], y[1]);
       o.y = pack_bf16x2(y[2], y[3]);
       const int pos = wp0 + t * 16 + lrow;
-      const int slot = ((n & 31) >> 3) ^ ((pos >> 2) & 3);
+      const int slot = ((n & 31) >> 3) ^ ((pos >> 1) & 3);
       *reinterpret_cast<uint2*>(hs + ((n >> 5) * BP + pos) * kChunk + slot * 8 + (n & 7)) = o;
       acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -370,13 +377,14 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
     for (int c = 0; c < TCO; ++c) {
       const int row = kc * BCO + wco0 + c * 16 + lrow;
-      a[c] = *reinterpret_cast<const bf16x8*>(w2s + row * kChunk + lk);
+      a[c] = *reinterpret_cast<const bf16x8*>(w2s + row * kChunk +
+                                              ((((lane >> 4) ^ (row >> 1)) & 3) << 3));
     }
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
       const int pos = wp0 + t * 16 + lrow;
       const bf16x8 bv = *reinterpret_cast<const bf16x8*>(
-          hs + (kc * BP + pos) * kChunk + (((lane >> 4) ^ ((pos >> 2) & 3)) * 8));
+          hs + (kc * BP + pos) * kChunk + (((lane >> 4) ^ ((pos >> 1) & 3)) * 8));
 #pragma unroll
       for (int c = 0; c < TCO; ++c)
         acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);

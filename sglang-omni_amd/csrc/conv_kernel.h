@@ -118,10 +118,10 @@ struct ConvTile {
   static constexpr int X_PIECES = (MAX_ROWS * 4 + NT - 1) / NT;
   static constexpr int W_PIECES = (BCO * MAX_TAPS * 4 + NT - 1) / NT;
   static_assert(W_PIECES <= 32 && X_PIECES <= 16, "per-thread piece masks are 32-bit");
-  // Weights in LDS: one row per output column holding its taps x 32 channels, padded by 16 bytes
-  // so the 16 rows an operand read touches start on distinct banks (the pad makes the row pitch
-  // an odd multiple of 16 bytes).
-  static constexpr int64_t wrow(int64_t taps) { return taps * kChunk + 8; }
+  // Weights in LDS: one row per output column holding its taps x 32 channels, padded by 32 bytes
+  // to a pitch of 2 mod 4 16-byte slots, at which the 16 rows an operand read touches meet no
+  // LDS bank conflict.
+  static constexpr int64_t wrow(int64_t taps) { return taps * kChunk + 16; }
   // Epilogue: the accumulator tile goes through LDS as float32 rows of BCO (+ 4 pad) columns,
   // half the position waves at a time, so the stores to HBM are whole contiguous rows.
   static constexpr int EPITCH = BCO + 4;
@@ -726,7 +726,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
         o.x = pack_bf16x2(y[0], y[1]);
         o.y = pack_bf16x2(y[2], y[3]);
         const int pos = wp0 + t * 16 + lrow;
-        const int slot = ((n & 31) >> 3) ^ ((pos >> 2) & 3);
+        const int slot = ((n & 31) >> 3) ^ ((pos >> 1) & 3);
         *reinterpret_cast<uint2*>(hs + ((n >> 5) * BP + pos) * kChunk + slot * 8 + (n & 7)) = o;
         acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
@@ -738,7 +738,8 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
         u32x4 v;
         if constexpr (W_FP8) v = fp8x8_to_bf16x8(wr8[u]);
         else v = wr[u];
-        *reinterpret_cast<u32x4*>(w2s + piece * 8) = v;
+        // 64-byte rows of W2, slot s of row r holding the row's piece s ^ ((r / 2) % 4)
+        *reinterpret_cast<u32x4*>(w2s + (piece ^ ((piece >> 3) & 3)) * 8) = v;
       }
     }
     __syncthreads();
@@ -747,13 +748,14 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
       bf16x8 a[TCO];
 #pragma unroll
       for (int c = 0; c < TCO; ++c)
-        a[c] = *reinterpret_cast<const bf16x8*>(w2s + ((kc * BCO) + wco0 + c * 16 + lrow) * kChunk +
-                                                lk);
+        a[c] = *reinterpret_cast<const bf16x8*>(
+            w2s + ((kc * BCO) + wco0 + c * 16 + lrow) * kChunk +
+            ((((lane >> 4) ^ ((wco0 + c * 16 + lrow) >> 1)) & 3) << 3));
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
         const int pos = wp0 + t * 16 + lrow;
         const bf16x8 bv = *reinterpret_cast<const bf16x8*>(
-            hs + (kc * BP + pos) * kChunk + (((lane >> 4) ^ ((pos >> 2) & 3)) * 8));
+            hs + (kc * BP + pos) * kChunk + (((lane >> 4) ^ ((pos >> 1) & 3)) * 8));
 #pragma unroll
         for (int c = 0; c < TCO; ++c)
           acc[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c], bv, acc[c][t], 0, 0, 0);
