@@ -406,6 +406,11 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     return r < rows ? i0 - H + (r - seg_of(t, lr) * span) : -(1 << 30);
   };
   if (tile > 0) __syncthreads();  // the previous tile's reads of the tile, guard and ring are done
+  // A wave none of whose rows is staged (the short last tile of a sweep) skips the matrix and
+  // element work of every unit: no staged row reads a later row, so nothing reads its rows. It
+  // still issues its share of each weight stage's DMA, meets every barrier and moves its halo
+  // rows (the guard rows the first wave reads), and its SIMD's other wave runs alone.
+  const bool active = wave_p * TP * 16 < rows;
   if (!x_ready) {
     const auto xr = buffer_rsrc(p.x, p.x_bytes);
     const int ln = opaque_copy(lane);
@@ -456,6 +461,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
   // unit 0's operand
 #pragma unroll
   for (int c = 0; c < TCO; ++c) {
+    if (!active) break;
     const int n = wco0 + c * 16 + (lane >> 4) * 4;
     const f32x4 a = *reinterpret_cast<const f32x4*>(in0 + n);
     const f32x4 b = *reinterpret_cast<const f32x4*>(in0 + C + n);
@@ -585,6 +591,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
       for (int r = 0; r < Tile::CONV_STAGES; ++r) {
         const int g = k * Tile::STAGES + r;
         if (r > 0) stage_begin(g);  // stage 0 began at the top of the unit
+        if (!active) continue;
         const int kc = W_FP8 ? r : r >> 1;
         const u16* ukc = us + kc * UROWS * kChunk;
         const u16* wbuf = ws + (g & 1) * Tile::RING_ELEMS;
@@ -634,6 +641,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
     const int g2 = k * Tile::STAGES + Tile::CONV_STAGES;
     stage_begin(g2);
     const u16* w2s = ws + (g2 & 1) * Tile::RING_ELEMS;
+    if (active) {
     // (d) h = Snake(acc * scale + bias) over the operand tile; the k = 1 weights
     const float* cf = coef + k * kCoefRows * C;
 #pragma unroll
@@ -698,6 +706,7 @@ __global__ void __launch_bounds__(64 * WCO * WP) residual_stack_kernel(const Sta
             snake_rev(v[2], na[2], nb[2]), snake_rev(v[3], na[3], nb[3]));
       }
     }
+    }  // active
     halo_move(k + 1);
   }
   // In the sweep, the next tile's x (no halo rows ahead of it) is loaded now, while this tile's
