@@ -220,7 +220,8 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeParams p) {
 constexpr int kQueries = 16;     // queries per wave
 constexpr int kHeadDim = 64;
 constexpr int kMaxKeyTiles = 8;  // 16-key tiles: window - 1 + 16 <= 128 keys
-constexpr int kKRow = kHeadDim + 8;  // bf16 pitch of a K row in LDS (16-byte reads spread banks)
+constexpr int kKRow = kHeadDim + 16;  // bf16 pitch of a K row in LDS: 10 16-byte slots, a pitch
+                                      // of 2 mod 4 slots, at which 16-row reads meet no bank conflict
 
 struct AttnParams {
   const u16* qkv;
@@ -265,33 +266,57 @@ __global__ __launch_bounds__(64) void window_attention_kernel(AttnParams p) {
   const int64_t kp0 = max(p0 - (p.window - 1), (int64_t)0);
   const int nk = (int)(start + last_t - kp0 + 1);  // <= window - 1 + 16 <= ks_n
   const int kv_width = p.kv_heads * kHeadDim;
-  // stage K (row-major) and V (transposed), 8 bf16 per lane and step; rows >= nk are zeros
-  for (int e = lane; e < ks_n * (kHeadDim / 8); e += kWave) {
-    const int r = e >> 3;
-    const int c8 = (e & 7) * 8;
-    uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-    if (r < nk) {
-      const int64_t kpos = kp0 + r;
-      const u16* ksrc;
-      const u16* vsrc;
-      if (ring) {
-        const int64_t rr = (slot < 0 ? 0 : slot) * p.ring_frames + kpos % p.ring_frames;
-        ksrc = p.key_ring + rr * kv_width + kvh * kHeadDim + c8;
-        vsrc = p.value_ring + rr * kv_width + kvh * kHeadDim + c8;
-      } else {
-        const u16* tok = p.qkv + (b * p.frames + (kpos - start)) * p.qkv_stride;
-        ksrc = tok + (p.heads + kvh) * kHeadDim + c8;
-        vsrc = tok + (p.heads + p.kv_heads + kvh) * kHeadDim + c8;
-      }
-      kw = *reinterpret_cast<const uint4*>(ksrc);
-      vw = *reinterpret_cast<const uint4*>(vsrc);
-    }
-    *reinterpret_cast<uint4*>(ks + r * kKRow + c8) = kw;
-    const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+  // stage K (row-major) and V (transposed), 8 bf16 per lane and step; rows >= nk are zeros.
+  // Every step's loads are issued before the first LDS store, so the staging waits on one
+  // round trip to memory instead of one per step.
+  constexpr int kMaxSteps = kMaxKeyTiles * 16 * (kHeadDim / 8) / kWave;
+  uint4 kw[kMaxSteps], vw[kMaxSteps];
+  {
+    // ring row of key row r = lane / 8 + 8 i: (kp0 + r) mod ring_frames, advanced by 8 a step
+    // (ring_frames >= window - 1 + frames > 8)
+    const int rf = (int)p.ring_frames;
+    int rr = ring ? (int)((kp0 + (lane >> 3)) % p.ring_frames) : 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      vt[(c8 + 2 * i) * vpitch + r] = (u16)(vv[i] & 0xffff);
-      vt[(c8 + 2 * i + 1) * vpitch + r] = (u16)(vv[i] >> 16);
+    for (int i = 0; i < kMaxSteps; ++i) {
+      const int e = lane + i * kWave;
+      const int r = e >> 3;
+      const int c8 = (e & 7) * 8;
+      kw[i] = make_uint4(0, 0, 0, 0);
+      vw[i] = kw[i];
+      if (e < ks_n * (kHeadDim / 8) && r < nk) {
+        const u16* ksrc;
+        const u16* vsrc;
+        if (ring) {
+          const int64_t row = (slot < 0 ? 0 : slot) * p.ring_frames + rr;
+          ksrc = p.key_ring + row * kv_width + kvh * kHeadDim + c8;
+          vsrc = p.value_ring + row * kv_width + kvh * kHeadDim + c8;
+        } else {
+          const u16* tok = p.qkv + (b * p.frames + (kp0 + r - start)) * p.qkv_stride;
+          ksrc = tok + (p.heads + kvh) * kHeadDim + c8;
+          vsrc = tok + (p.heads + p.kv_heads + kvh) * kHeadDim + c8;
+        }
+        kw[i] = *reinterpret_cast<const uint4*>(ksrc);
+        vw[i] = *reinterpret_cast<const uint4*>(vsrc);
+      }
+      if (ring) {
+        rr += 8;
+        if (rr >= rf) rr -= rf;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxSteps; ++i) {
+    const int e = lane + i * kWave;
+    if (e < ks_n * (kHeadDim / 8)) {
+      const int r = e >> 3;
+      const int c8 = (e & 7) * 8;
+      *reinterpret_cast<uint4*>(ks + r * kKRow + c8) = kw[i];
+      const uint32_t vv[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vt[(c8 + 2 * j) * vpitch + r] = (u16)(vv[j] & 0xffff);
+        vt[(c8 + 2 * j + 1) * vpitch + r] = (u16)(vv[j] >> 16);
+      }
     }
   }
   // this lane's query row n (zeros past the last query) as the B operand, dims 8 g .. 8 g + 7
