@@ -100,8 +100,8 @@ enum {
 };
 
 const char* omni_codec_error_string(int status);
-int omni_codec_abi_version(void); /* 10: omni_gemm (the code2wav front's linear layers with their
-                                       elementwise epilogues) */
+int omni_codec_abi_version(void); /* 11: float16 mix streams (omni_conv_args.mix_a / mix_b in
+                                       residual_dtype); 10: omni_gemm */
 
 /* Device facts the host layer sizes its launches with: the gfx arch name (e.g. "gfx950"), LDS
    bytes per workgroup and compute-unit count. */
@@ -139,9 +139,9 @@ int omni_rvq_gather_sum(const void* codes, int codes_dtype, int64_t batch, int64
  *   out[b, i, n] = act(v)           (bf16 or float32; optional when sum_out is given)
  *
  * for i < length and n < n_cols. x holds x_length positions per row (x_length = 0 means length);
- * the residual, mix and sum_out tensors share the residual strides; residual and sum_out are
- * float32, or float16 with residual_dtype = OMNI_DTYPE_F16 (a residual stream kept in half
- * precision between launches, added in float32; then no mix); sum_out may alias residual
+ * the residual, mix and sum_out tensors share the residual strides; residual, mix and sum_out
+ * are float32, or float16 with residual_dtype = OMNI_DTYPE_F16 (residual streams kept in half
+ * precision between launches, widened exactly and added in float32); sum_out may alias residual
  * (each element is read before it is written by the same thread) but no output may alias x. A
  * causal Conv1d is taps = k, left_pad = (k-1)*d; a ConvTranspose1d of stride s is its polyphase
  * form (n = phase * c_out + co, so out viewed as [B, length * s, c_out] is the transposed conv's
@@ -190,8 +190,8 @@ typedef struct omni_conv_args {
   int history_cold;
   const void* residual; /* float32, or float16 (residual_dtype) */
   int64_t residual_stride_b, residual_stride_t;
-  const float* mix_a;
-  const float* mix_b;
+  const void* mix_a; /* float32, or float16 (residual_dtype) */
+  const void* mix_b;
   float mix_scale;
   void* sum_out; /* float32, or float16 (residual_dtype) */
   void* out;

@@ -20,7 +20,7 @@ extern "C" const char* omni_codec_error_string(int status) {
   }
 }
 
-extern "C" int omni_codec_abi_version(void) { return 10; }
+extern "C" int omni_codec_abi_version(void) { return 11; }
 
 extern "C" int omni_codec_capabilities(int device, char* arch, int arch_capacity,
                                        int64_t* lds_bytes, int64_t* compute_units) {

@@ -122,7 +122,7 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
   };
   if ((a->residual && !r_aligned(a->residual)) || (a->sum_out && !r_aligned(a->sum_out)))
     return OMNI_ERR_INVALID_ARG;
-  if (a->mix_a && (r_f16 || !a->mix_b || !aligned16(a->mix_a) || !aligned16(a->mix_b)))
+  if (a->mix_a && (!a->mix_b || !r_aligned(a->mix_a) || !r_aligned(a->mix_b)))
     return OMNI_ERR_INVALID_ARG;
   if (a->out && a->out_stride_t < a->n_cols) return OMNI_ERR_INVALID_ARG;
   if (a->out) {

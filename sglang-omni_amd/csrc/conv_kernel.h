@@ -67,11 +67,11 @@ struct ConvParams {
   int hist_cold;
   const void* residual;  // float32, or float16 when r_f16
   int64_t r_sb, r_st;  // shared by residual, mix_a, mix_b and sum_out
-  const float* mix_a;
-  const float* mix_b;
+  const void* mix_a;  // float32, or float16 with r_f16
+  const void* mix_b;
   float mix_scale;
   void* sum_out;  // float32, or float16 when r_f16
-  int r_f16;      // residual and sum_out are float16 (a half-precision residual stream; no mix)
+  int r_f16;      // residual, mix and sum_out are float16 (a half-precision residual stream)
   void* out;
   int out_bf16;
   int64_t o_sb, o_st;
@@ -299,8 +299,8 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
       const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
-        const f32x4 ma = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, roff[u], 0, 0));
-        const f32x4 mb = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, roff[u], 0, 0));
+        const f32x4 ma = load_residual4(ra, roff[u], p.r_f16);
+        const f32x4 mb = load_residual4(rb, roff[u], p.r_f16);
         v[u] = ((ma + mb) + v[u]) * p.mix_scale;
       }
     }

@@ -41,7 +41,7 @@ class OmniCodecError(RuntimeError):
 
 INVALID_ARG = 1
 UNSUPPORTED = 2
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # kernel families of omni_conv1d_fused (omni_conv1d_plan / omni_conv1d_fused_with)
 CONV_KERNEL_AUTO, CONV_KERNEL_DMA, CONV_KERNEL_STAGED, CONV_KERNEL_STAGED11, CONV_KERNEL_FUSED_UNIT = range(5)

@@ -231,8 +231,10 @@ def _conv_args(
         raise ValueError("residual / sum_out must be float32 or float16")
     if mix is not None:
         N.require_device(mix[0], mix[1])
-        if r_dtype != torch.float32:
-            raise ValueError("a mix takes a float32 residual stream")
+        if not aux:
+            r_dtype = mix[0].dtype
+            if r_dtype not in (torch.float32, torch.float16):
+                raise ValueError("mix streams must be float32 or float16")
         aux += [mix[0], mix[1]]
     for t in aux:
         if t.dtype != r_dtype or t.stride() != aux[0].stride():
@@ -357,9 +359,10 @@ def fused_conv(x: torch.Tensor, conv: PackedConv, out: torch.Tensor | None, *,
     x [B, >=x_length, C_in] bf16 or float32 (rows may sit in longer buffers; channel stride 1),
     activated per input channel by ``in_activation`` while it is staged; ``second`` is a k = 1
     conv (C_out -> C_out) fused behind this one with ``mid_activation`` between them;
-    out [B, length, n_cols] bf16 or float32; residual / sum_out (float32, or float16: a
-    half-precision residual stream, added in float32 and rounded once when stored) / mix
-    (float32 streams only) tensors with out's logical shape and one shared stride; history [slots, 2, left_pad, C_in] bf16 with int64
+    out [B, length, n_cols] bf16 or float32; residual / sum_out / mix (float32, or float16: a
+    half-precision residual stream, widened exactly, added in float32 and rounded once when
+    stored) tensors of one dtype with out's logical shape and one shared stride; history
+    [slots, 2, left_pad, C_in] bf16 with int64
     slot_index [B] and slot_parity [slots]. ``kernel`` / ``config`` name a kernel family and the
     1-based entry of its tile list (``omni_conv1d_fused_with``) instead of the size-based choice.
     """

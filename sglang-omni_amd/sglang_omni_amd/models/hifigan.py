@@ -7,8 +7,10 @@ ConvTranspose1d(k, u, padding (k-u)//2) -> mean of the multi-receptive-field Res
 LeakyReLU(0.01) -> conv_post to one channel k=7 -> tanh.
 
 Every conv is one ``omni_conv1d_fused`` launch whose epilogue applies the following LeakyReLU
-(so no activation kernel runs on its own); each ResBlock keeps its running sum in float32 and
-the last conv of the last ResBlock folds in the mean of the three blocks.
+(so no activation kernel runs on its own); each ResBlock keeps its running sum as a residual
+stream (float16 by default: stored in half precision between launches, widened exactly and
+added in float32; ``residual_dtype=torch.float32`` keeps it in float32) and the last conv of the
+last ResBlock folds in the mean of the three blocks.
 """
 
 from __future__ import annotations
@@ -28,9 +30,13 @@ class HifiGanVocoder:
     """mel [B, n_mels, T] -> waveform [B, 1, T * prod(rates)] float32."""
 
     def __init__(self, weights: dict[str, Any], config: HifiGanConfig, *,
-                 device: torch.device | str = "cuda", weight_format: str = "bf16"):
+                 device: torch.device | str = "cuda", weight_format: str = "bf16",
+                 residual_dtype: torch.dtype = torch.float16):
+        if residual_dtype not in (torch.float16, torch.float32):
+            raise ValueError("the residual streams are float16 or float32")
         self.config = config
         self.device = torch.device(device)
+        self.residual_dtype = residual_dtype
         fp8 = weight_format == "fp8"
         ref = reference_weights(weights, weight_format)
         dev = self.device
@@ -67,15 +73,15 @@ class HifiGanVocoder:
             raise ValueError("the MRF mean is fused for three ResBlocks per stage")
 
     def _workspace(self, elements: int) -> tuple[torch.Tensor, ...]:
-        """The intermediate activations of a call: four bf16 and three float32 flat buffers of
-        at least ``elements`` each, kept between calls and grown (never shrunk) when a call
-        needs more. Calls on one vocoder share them, so they must not overlap (one stream, or
-        calls ordered between streams)."""
+        """The intermediate activations of a call: four bf16 buffers and three residual streams
+        (``residual_dtype``), flat, of at least ``elements`` each, kept between calls and grown
+        (never shrunk) when a call needs more. Calls on one vocoder share them, so they must not
+        overlap (one stream, or calls ordered between streams)."""
         ws = getattr(self, "_ws", None)
         if ws is None or ws[0].numel() < elements:
-            bf, f32 = torch.bfloat16, torch.float32
+            bf, rd = torch.bfloat16, self.residual_dtype
             ws = tuple(torch.empty(elements, dtype=dt, device=self.device)
-                       for dt in (bf, bf, bf, bf, f32, f32, f32))
+                       for dt in (bf, bf, bf, bf, rd, rd, rd))
             self._ws = ws
         return ws
 

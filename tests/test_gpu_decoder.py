@@ -232,11 +232,13 @@ def test_fp8_weight_decoder_matches_the_dequantized_oracle(gpu):
     check_waveform(out, expected, 5e-3)
 
 
-def test_hifigan_matches_the_oracle(gpu):
+@pytest.mark.parametrize("residual_dtype", [torch.float16, torch.float32])
+def test_hifigan_matches_the_oracle(gpu, residual_dtype):
     """The HiFiGAN body (80 mels, 512 channels, rates 8/5/3/4, MRF k 3/7/11 d 1/3/5) on 20 mel
-    frames of log-mel ~ N(-5, 2), batch 2."""
+    frames of log-mel ~ N(-5, 2), batch 2, with float16 (the default) or float32 residual
+    streams."""
     weights = make_hifigan_weights(HIFIGAN_24K, seed=0)
-    vocoder = HifiGanVocoder(weights, HIFIGAN_24K, device=gpu)
+    vocoder = HifiGanVocoder(weights, HIFIGAN_24K, device=gpu, residual_dtype=residual_dtype)
     gen = torch.Generator().manual_seed(0)
     mel = torch.randn(2, 80, 20, generator=gen) * 2 - 5
     out = vocoder(mel.to(gpu))

@@ -142,13 +142,35 @@ def test_residual_stack_reads_and_writes_a_float16_stream(gpu, batch, length, fi
         assert torch.equal(f16, f32)
 
 
-def test_float16_streams_refuse_a_mix_and_misaligned_rows(gpu):
+def test_mix_of_float16_streams(gpu):
+    """The mean of three float16 streams (HiFiGAN's multi-receptive-field mix): each stream
+    widened exactly, the same float32 sum as with the widened streams, rounded once."""
+    gen = torch.Generator().manual_seed(33)
+    c, rows = 128, 1500
+    h = torch.randn(2, rows, c, generator=gen).to(torch.bfloat16).to(gpu)
+    conv = pack_conv1d(torch.randn(c, c, 7, generator=gen) / math.sqrt(7 * c),
+                       torch.randn(c, generator=gen) * 0.1, dilation=5).to(gpu)
+    x16, a16, b16 = ((torch.randn(2, rows, c, generator=gen) * 2).half().to(gpu)
+                     for _ in range(3))
+    outs = []
+    for dt in (torch.float16, torch.float32):
+        s = torch.full((2, rows, c), float("nan"), dtype=dt, device=gpu)
+        out = torch.empty(2, rows, c, dtype=torch.bfloat16, device=gpu)
+        fused_conv(h, conv, out, residual=x16.to(dt), sum_out=s, activation=N.ACT_LEAKY_RELU,
+                   slope=0.01, mix=(a16.to(dt), b16.to(dt), 1.0 / 3.0))
+        outs.append((out, s))
+    (o16, s16), (o32, s32) = outs
+    assert torch.equal(o16, o32)
+    assert torch.equal(s16, s32.half())
+
+
+def test_float16_streams_refuse_a_dtype_mix_and_misaligned_rows(gpu):
     gen = torch.Generator().manual_seed(31)
     h = torch.randn(1, 64, 128, generator=gen).to(torch.bfloat16).to(gpu)
     conv = pack_conv1d(torch.randn(128, 128, 1, generator=gen) / 12, None).to(gpu)
     x16 = torch.zeros(1, 64, 128, dtype=torch.float16, device=gpu)
     m = torch.zeros(1, 64, 128, device=gpu)
-    with pytest.raises(ValueError, match="float32 residual stream"):
+    with pytest.raises(ValueError, match="share one dtype"):
         fused_conv(h, conv, None, sum_out=x16, mix=(m, m, 0.5))
     # an 8-byte-misaligned float16 stream is refused by the library before any launch
     buf = torch.zeros(64 * 128 + 2, dtype=torch.float16, device=gpu)

@@ -55,7 +55,7 @@ def test_binding_covers_the_header_and_loads():
     lib = N.load_library()
     for name in N.SIGNATURES:
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
-    assert lib.omni_codec_abi_version() == N.ABI_VERSION == 10
+    assert lib.omni_codec_abi_version() == N.ABI_VERSION == 11
     assert lib.omni_codec_error_string(N.OK) == b"ok"
     assert b"invalid" in lib.omni_codec_error_string(1)
 
