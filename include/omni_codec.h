@@ -278,6 +278,17 @@ int omni_conv1d_splitk(const omni_conv_args* args, int64_t k_splits, float* work
 #define OMNI_SPLITK_SCRATCH_BYTES (64ll << 20)
 int omni_conv1d_splitk_noalloc(const omni_conv_args* args, int64_t k_splits, int kernel, int config,
                                omni_stream_t stream);
+/*
+ * omni_resblock_pair: a ResBlock pair of a 32-channel HiFiGAN stage in one launch, h = act1(c1(x))
+ * kept in LDS and y = c2(h) through c2's epilogue (hift_layers.py:95-110: xt = c1(act(x)), xt =
+ * c2(act(xt)), x = xt + x). c1 describes the first conv (x, weights, bias, dilation d <= 5,
+ * activation NONE or LEAKY_RELU, no output, residual or mix); c2 the second (no x: its operand is
+ * h; bias, residual, mix, sum_out, out and activation as omni_conv1d_fused takes them). Both 32
+ * channels, bf16 weights and operand, k = 3, 7 or 11 with "same" padding (left_pad = (k-1)*d/2 and
+ * (k-1)/2), no history, input activation or fused second conv; else OMNI_ERR_UNSUPPORTED. The
+ * result equals omni_conv1d_fused of c1 (into a bf16 h) then of c2, bit for bit.
+ */
+int omni_resblock_pair(const omni_conv_args* c1, const omni_conv_args* c2, omni_stream_t stream);
 int omni_conv1d_plan(const omni_conv_args* args, int kernel, int config, int* kernel_out,
                      int* config_out, int* configs_in_list, int64_t* workgroups);
 

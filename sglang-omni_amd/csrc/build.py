@@ -30,7 +30,7 @@ SOURCES = ["capi.hip", "rvq.hip", "conv.hip", "conv_k7_raw_wbf16.hip", "conv_k7_
            "conv_ru_wfp8.hip", "residual_stack.hip", "residual_stack_wbf16.hip",
            "residual_stack_wfp8.hip", "single_output_conv.hip", "codec_state.hip", "snake.hip", "hift.hip",
            "egress.hip", "code2wav_front.hip", "channel_embedding.hip", "conv_general.hip",
-           "gemm.hip"]
+           "gemm.hip", "resblock_pair.hip"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

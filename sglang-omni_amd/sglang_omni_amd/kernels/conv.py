@@ -382,6 +382,55 @@ def fused_conv(x: torch.Tensor, conv: PackedConv, out: torch.Tensor | None, *,
 _plan_log: list | None = None
 
 
+def resblock_pair_supported(c1: PackedConv, c2: PackedConv) -> bool:
+    """Whether ``resblock_pair`` takes this pair: 32 channels, bf16 weights, k = 3 / 7 / 11 with
+    "same" padding, c1 dilation <= 5, c2 dilation 1."""
+    k = c1.taps
+    return (c1.c_in == c1.c_out == c1.n_cols == 32 and c2.c_in == c2.c_out == c2.n_cols == 32
+            and c1.weight.dtype == c2.weight.dtype == torch.bfloat16 and k in (3, 7, 11)
+            and c2.taps == k and c2.dilation == 1 and c1.dilation <= 5
+            and c1.left_pad == (k - 1) * c1.dilation // 2 and c2.left_pad == (k - 1) // 2)
+
+
+def resblock_pair(x: torch.Tensor, c1: PackedConv, c2: PackedConv, out: torch.Tensor | None, *,
+                  slope1: float, **kw) -> torch.Tensor | None:
+    """A ResBlock pair of a 32-channel stage in one launch (``omni_resblock_pair``): h =
+    LeakyReLU(slope1)(c1(x)) stays on chip, then c2(h) with ``fused_conv``'s epilogue keywords
+    (residual, sum_out, mix, activation, slope) into out. Equals ``fused_conv(x, c1, h,
+    activation=LEAKY_RELU, slope=slope1)`` then ``fused_conv(h, c2, out, **kw)`` bit for bit."""
+    if not resblock_pair_supported(c1, c2):
+        raise ValueError("resblock_pair takes 32-channel bf16 pairs with k 3 / 7 / 11, same padding")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("the pair's operand is bf16")
+    # c2's arguments with x standing in for h (the same [B, L, 32] shape) for validation
+    a2 = _conv_args(x, c2, out, **kw)
+    a2.x = None
+    a1 = N.ConvArgs()
+    a1.x = x.data_ptr()
+    a1.x_dtype = N.DTYPE_BF16
+    a1.x_stride_b = x.stride(0)
+    a1.x_stride_t = x.stride(1)
+    a1.batch = x.shape[0]
+    a1.length = x.shape[1]
+    a1.c_in = c1.c_in
+    a1.weight = c1.weight.data_ptr()
+    a1.weight_dtype = N.DTYPE_BF16
+    a1.n_cols = c1.n_cols
+    a1.c_out = c1.c_out
+    a1.taps = c1.taps
+    a1.dilation = c1.dilation
+    a1.left_pad = c1.left_pad
+    a1.bias = N.ptr(c1.bias)
+    a1.out_dtype = N.DTYPE_BF16
+    a1.residual_dtype = N.DTYPE_F32
+    a1.activation = N.ACT_LEAKY_RELU
+    a1.act_slope = float(slope1)
+    lib = N.load_library()
+    N.check(lib.omni_resblock_pair(ctypes.byref(a1), ctypes.byref(a2), N.stream_handle(x.device)),
+            "omni_resblock_pair")
+    return out
+
+
 @contextmanager
 def recording_plans():
     """Collect the ``ConvPlan`` of every ``fused_conv`` call made inside the block (in call

@@ -20,7 +20,8 @@ from typing import Any
 import torch
 
 from .. import _native as N
-from ..kernels.conv import PackedConv, fused_conv, pack_conv1d, pack_conv_transpose1d
+from ..kernels.conv import (PackedConv, fused_conv, pack_conv1d, pack_conv_transpose1d,
+                            resblock_pair, resblock_pair_supported)
 from ..kernels.single_output_conv import single_output_conv
 from ..quantization import reference_weights
 from .configs import HifiGanConfig
@@ -31,12 +32,14 @@ class HifiGanVocoder:
 
     def __init__(self, weights: dict[str, Any], config: HifiGanConfig, *,
                  device: torch.device | str = "cuda", weight_format: str = "bf16",
-                 residual_dtype: torch.dtype = torch.float16):
+                 residual_dtype: torch.dtype = torch.float16, resblock_pairs: bool = True):
         if residual_dtype not in (torch.float16, torch.float32):
             raise ValueError("the residual streams are float16 or float32")
         self.config = config
         self.device = torch.device(device)
         self.residual_dtype = residual_dtype
+        # the 32-channel stage's ResBlock pairs as one launch each (omni_resblock_pair)
+        self.pairs = resblock_pairs
         fp8 = weight_format == "fp8"
         ref = reference_weights(weights, weight_format)
         dev = self.device
@@ -124,23 +127,35 @@ class HifiGanVocoder:
             pn = view(act_p, length, cout)
             for j, pairs in enumerate(st["blocks"]):
                 xj = view(xb[j], length, cout) if j < 2 else None
+                src = q
                 for m, (c1, c2) in enumerate(pairs):
-                    src = q if m == 0 else rv
-                    fused_conv(src, c1, hv, activation=lrelu, slope=self.slope)
+                    # (k = 11 pairs measured slower as one launch: 540-610 against 435 us for
+                    # the two launches at 16 x 240 000 samples, the tile's 2 x 30-row x halo)
+                    paired = self.pairs and c1.taps < 11 and resblock_pair_supported(c1, c2)
                     last_m = m + 1 == len(pairs)
                     resid = xstage if m == 0 else (xj if j < 2 else xstage)
                     if not last_m:
-                        # running sum of this block; block 2 reuses the stage buffer in place
+                        # running sum of this block; block 2 reuses the stage buffer in place.
+                        # A pair reads its operand's neighbours' halo rows, so it writes the next
+                        # operand into the other buffer (h stays on chip, so hv is free)
                         target = xj if j < 2 else xstage
-                        fused_conv(hv, c2, rv, activation=lrelu, slope=self.slope, residual=resid,
-                                   sum_out=target)
+                        nxt = (hv if src is rv else rv) if paired else rv
+                        c2_out, kw = nxt, dict(activation=lrelu, slope=self.slope,
+                                               residual=resid, sum_out=target)
                     elif j < 2:
-                        fused_conv(hv, c2, None, residual=resid, sum_out=xj)
+                        c2_out, kw = None, dict(residual=resid, sum_out=xj)
                     else:
                         slope = self.final_slope if last_stage else self.slope
-                        fused_conv(hv, c2, pn, activation=lrelu, slope=slope, residual=resid,
-                                   mix=(view(xb[0], length, cout), view(xb[1], length, cout),
-                                        1.0 / 3.0))
+                        c2_out, kw = pn, dict(activation=lrelu, slope=slope, residual=resid,
+                                              mix=(view(xb[0], length, cout),
+                                                   view(xb[1], length, cout), 1.0 / 3.0))
+                    if paired:
+                        # the 32-channel pairs: h stays on chip
+                        resblock_pair(src, c1, c2, c2_out, slope1=self.slope, **kw)
+                    else:
+                        fused_conv(src, c1, hv, activation=lrelu, slope=self.slope)
+                        fused_conv(hv, c2, c2_out, **kw)
+                    src = c2_out
             p = pn
         wave = torch.empty(batch, 1, length, dtype=torch.float32, device=dev)
         single_output_conv(p, self.post_weight, self.post_bias, wave, activation=N.ACT_TANH,
