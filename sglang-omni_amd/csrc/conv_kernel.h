@@ -69,7 +69,6 @@ struct ConvParams {
   int64_t r_sb, r_st;  // shared by residual, mix_a, mix_b and sum_out
   const void* mix_a;  // float32, or float16 with r_f16
   const void* mix_b;
-  float mix_scale;
   void* sum_out;  // float32, or float16 when r_f16
   int r_f16;      // residual, mix and sum_out are float16 (a half-precision residual stream)
   void* out;
@@ -79,6 +78,7 @@ struct ConvParams {
   const float* act_a;
   const float* act_b;
   float slope;
+  float mix_scale;
   int p_tiles, n_tiles;
   // split-K (LDS-DMA k = 1 convs only): k_splits slices of whole 32-channel chunks, slice s
   // writing its float32 partial tile [positions][n_cols] at partial + s * positions * n_cols
