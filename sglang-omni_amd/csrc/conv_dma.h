@@ -276,19 +276,22 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
                                                      (int)woff[u], (int)wbase, 0, 0);
         }
         const uint32_t xbase = (uint32_t)(kc * kChunk * 2);
+        // the rows from x, then, in a loop of their own, those from the history pool (one loop
+        // with both DMAs becomes one DMA whose buffer descriptor differs between lanes, a loop of
+        // readfirstlane per instruction)
 #pragma unroll
         for (int u = 0; u < Tile::X_PIECES; ++u) {
           const int ii = wave + u * NW;
-          if (ii < Tile::NIX) {
-            const unsigned mode = (xmode >> (2 * u)) & 3u;
-            lds_ptr_t dst = (lds_ptr_t)(xs + ii * 64 * 8);
-            if (mode == 1u)
-              __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, dst, 16, (int)((uint32_t)xoff[u] * 2u),
-                                                       (int)xbase, 0, 0);
-            else if (mode == 2u)
-              __builtin_amdgcn_raw_ptr_buffer_load_lds(h_rsrc, dst, 16, (int)((uint32_t)xoff[u] * 2u),
-                                                       (int)xbase, 0, 0);
-          }
+          if (ii < Tile::NIX && ((xmode >> (2 * u)) & 3u) == 1u)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_ptr_t)(xs + ii * 64 * 8), 16,
+                                                     (int)((uint32_t)xoff[u] * 2u), (int)xbase, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < Tile::X_PIECES; ++u) {
+          const int ii = wave + u * NW;
+          if (ii < Tile::NIX && ((xmode >> (2 * u)) & 3u) == 2u)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(h_rsrc, (lds_ptr_t)(xs + ii * 64 * 8), 16,
+                                                     (int)((uint32_t)xoff[u] * 2u), (int)xbase, 0, 0);
         }
       }
     }
