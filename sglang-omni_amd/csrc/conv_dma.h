@@ -276,9 +276,10 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
                                                      (int)woff[u], (int)wbase, 0, 0);
         }
         const uint32_t xbase = (uint32_t)(kc * kChunk * 2);
-        // the rows from x, then, in a loop of their own, those from the history pool (one loop
-        // with both DMAs becomes one DMA whose buffer descriptor differs between lanes, a loop of
-        // readfirstlane per instruction)
+        // the rows from x, then those from the history pool, whose DMA carries the non-temporal
+        // hint (aux 2): DMAs that differ only in their buffer descriptor are merged by the
+        // compiler into one whose descriptor differs between lanes, a readfirstlane loop per
+        // instruction
 #pragma unroll
         for (int u = 0; u < Tile::X_PIECES; ++u) {
           const int ii = wave + u * NW;
@@ -291,7 +292,7 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
           const int ii = wave + u * NW;
           if (ii < Tile::NIX && ((xmode >> (2 * u)) & 3u) == 2u)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(h_rsrc, (lds_ptr_t)(xs + ii * 64 * 8), 16,
-                                                     (int)((uint32_t)xoff[u] * 2u), (int)xbase, 0, 0);
+                                                     (int)((uint32_t)xoff[u] * 2u), (int)xbase, 0, 2);
         }
       }
     }

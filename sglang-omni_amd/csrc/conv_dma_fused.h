@@ -241,9 +241,11 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
         if (mode == 1u)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, dst, 16, (int)((uint32_t)xoff[u] * 2u),
                                                    (int)xbase, 0, 0);
-        else if (mode == 2u)
+        else if (mode == 2u)  // with the non-temporal hint (aux 2), which keeps the compiler
+                              // from merging the two DMAs into one whose buffer descriptor
+                              // differs between lanes (a readfirstlane loop)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(h_rsrc, dst, 16, (int)((uint32_t)xoff[u] * 2u),
-                                                   (int)xbase, 0, 0);
+                                                   (int)xbase, 0, 2);
       }
     }
   };
