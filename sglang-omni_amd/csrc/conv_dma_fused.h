@@ -393,8 +393,10 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
     }
   }
 
-  conv_epilogue<typename Tile::Base, Tile::WAVES_P, TCO, TP>(p, acc, lds, coef, kScale2, kBias2, 0,
-                                                             m0, m_end, wave_p, wco0);
+  // (no mix: the launcher refuses it)
+  conv_epilogue<typename Tile::Base, Tile::WAVES_P, TCO, TP, false>(p, acc, lds, coef, kScale2,
+                                                                    kBias2, 0, m0, m_end, wave_p,
+                                                                    wco0);
 }
 
 struct FusedDmaConfig {
@@ -410,10 +412,10 @@ struct FusedDmaConfig {
   }
 
   // A 192-channel unit (k7 conv of C_in = C_out = 192, then the k1 conv 192 -> 192) whose staged
-  // rows fit.
+  // rows fit, with no mix in its epilogue (the register-staged kernels take that).
   static bool fits(const ConvParams& p) {
     return p.taps == 7 && p.n_cols == Tile::BCO && p.c_out == Tile::BCO && p.c_in == Tile::BCO &&
-           p.weight2 != nullptr && rows_needed(p) <= Tile::MAX_ROWS;
+           p.weight2 != nullptr && p.mix_a == nullptr && rows_needed(p) <= Tile::MAX_ROWS;
   }
 
   static int64_t workgroups(const ConvParams& p) {

@@ -220,8 +220,9 @@ __device__ __forceinline__ void store_residual4(f32x4 v, __amdgpu_buffer_rsrc_t 
 // the weight scale and bias and writes float32 rows into LDS; (2) the workgroup walks those rows
 // 16 bytes per thread, so the residual / mix loads and the sum_out / out stores are whole
 // contiguous rows of HBM. `lds` must be free for Tile::EPI_ROWS x Tile::EPITCH floats (the first
-// pass begins with a barrier); `coef` holds the tile's coefficient table.
-template <typename Tile, int WAVES_P, int TCO, int TP>
+// pass begins with a barrier); `coef` holds the tile's coefficient table. MIX = false: a kernel
+// whose launcher refuses the mix leaves out its code (and the registers it takes).
+template <typename Tile, int WAVES_P, int TCO, int TP, bool MIX = true>
 __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[TCO][TP], u16* lds,
                                               const float* coef, int coef_scale, int coef_bias,
                                               int n0, int m0, int m_end, int wave_p, int wco0) {
@@ -294,7 +295,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
 #pragma unroll
       for (int u = 0; u < NU; ++u) v[u] += widen_residual4(res[u], p.r_f16);
     }
-    if (p.mix_a) {
+    if (MIX && p.mix_a) {
       const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
       const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
 #pragma unroll
