@@ -222,8 +222,8 @@ __device__ __forceinline__ void store_residual4(f32x4 v, __amdgpu_buffer_rsrc_t 
 // contiguous rows of HBM. `lds` must be free for Tile::EPI_ROWS x Tile::EPITCH floats (the first
 // pass begins with a barrier); `coef` holds the tile's coefficient table. MIX = false: a kernel
 // whose launcher refuses the mix leaves out its code (and the registers it takes).
-template <typename Tile, int WAVES_P, int TCO, int TP, bool MIX = true>
-__device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[TCO][TP], u16* lds,
+template <typename Tile, int WAVES_P, int TCO, int TP, bool MIX, bool F16>
+__device__ __forceinline__ void conv_epilogue_body(const ConvParams& p, f32x4 (&acc)[TCO][TP], u16* lds,
                                               const float* coef, int coef_scale, int coef_bias,
                                               int n0, int m0, int m_end, int wave_p, int wco0) {
   constexpr int NT = Tile::NT;
@@ -252,7 +252,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
   // fit 32 bits (the byte extents are below 2 GiB).
   const bool packed = p.r_sb == (int64_t)L * p.r_st && p.o_sb == (int64_t)L * p.o_st;
   const uint32_t r_st = (uint32_t)p.r_st, o_st = (uint32_t)p.o_st;
-  const uint32_t rsize = p.r_f16 ? 2u : 4u;  // bytes per residual-stream element
+  const uint32_t rsize = F16 ? 2u : 4u;  // bytes per residual-stream element
   const bool live = walker && n_q < n_cols;
   // element offsets of flat position m in the residual-shaped tensors and in out
   auto offsets = [&](int m, uint32_t& re, uint32_t& oe) __attribute__((always_inline)) {
@@ -290,25 +290,25 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
       if (!have_res) {
         const auto rr = buffer_rsrc(p.residual, p.r_bytes);
 #pragma unroll
-        for (int u = 0; u < NU; ++u) res[u] = load_residual4_raw(rr, roff[u], p.r_f16);
+        for (int u = 0; u < NU; ++u) res[u] = load_residual4_raw(rr, roff[u], F16);
       }
 #pragma unroll
-      for (int u = 0; u < NU; ++u) v[u] += widen_residual4(res[u], p.r_f16);
+      for (int u = 0; u < NU; ++u) v[u] += widen_residual4(res[u], F16);
     }
     if (MIX && p.mix_a) {
       const auto ra = buffer_rsrc(p.mix_a, p.r_bytes);
       const auto rb = buffer_rsrc(p.mix_b, p.r_bytes);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
-        const f32x4 ma = load_residual4(ra, roff[u], p.r_f16);
-        const f32x4 mb = load_residual4(rb, roff[u], p.r_f16);
+        const f32x4 ma = load_residual4(ra, roff[u], F16);
+        const f32x4 mb = load_residual4(rb, roff[u], F16);
         v[u] = ((ma + mb) + v[u]) * p.mix_scale;
       }
     }
     if (p.sum_out) {
       const auto rs = buffer_rsrc(p.sum_out, p.r_bytes);
 #pragma unroll
-      for (int u = 0; u < NU; ++u) store_residual4(v[u], rs, roff[u], p.r_f16);
+      for (int u = 0; u < NU; ++u) store_residual4(v[u], rs, roff[u], F16);
     }
     if (p.out != nullptr) {
       const int act = p.act;
@@ -357,7 +357,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
           uint32_t re, oe;
           offsets(mp + min(r, prow - 1), re, oe);
           const uint32_t off = live && r < prow ? re * rsize : kOutOfRange;
-          pre[u] = load_residual4_raw(rr, off, p.r_f16);
+          pre[u] = load_residual4_raw(rr, off, F16);
         }
       }
     }
@@ -394,6 +394,20 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[
       }
     }
   }
+}
+
+// The residual stream's dtype is a compile-time constant of each copy of the epilogue, so its
+// loads, stores and widening take no per-row select.
+template <typename Tile, int WAVES_P, int TCO, int TP, bool MIX = true>
+__device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x4 (&acc)[TCO][TP], u16* lds,
+                                              const float* coef, int coef_scale, int coef_bias,
+                                              int n0, int m0, int m_end, int wave_p, int wco0) {
+  if (p.r_f16)
+    conv_epilogue_body<Tile, WAVES_P, TCO, TP, MIX, true>(p, acc, lds, coef, coef_scale, coef_bias,
+                                                          n0, m0, m_end, wave_p, wco0);
+  else
+    conv_epilogue_body<Tile, WAVES_P, TCO, TP, MIX, false>(p, acc, lds, coef, coef_scale,
+                                                           coef_bias, n0, m0, m_end, wave_p, wco0);
 }
 
 // Input modes: bf16 used as is; bf16 activated while staged; float32 activated while staged.
