@@ -311,28 +311,38 @@ __device__ __forceinline__ void conv_epilogue_body(const ConvParams& p, f32x4 (&
       for (int u = 0; u < NU; ++u) store_residual4(v[u], rs, roff[u], F16);
     }
     if (p.out != nullptr) {
+      // the activation, then the stores, each branch taken once for the NU rows (a branch per
+      // row keeps the compiler from grouping the rows' stores)
       const int act = p.act;
+      if (act == OMNI_ACT_SNAKE) {
 #pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        f32x4 y = v[u];
-        if (act == OMNI_ACT_SNAKE) {
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = snake_rev(y[e], act_a[e], act_b[e]);
-        } else if (act == OMNI_ACT_LEAKY_RELU) {
+          for (int e = 0; e < 4; ++e) v[u][e] = snake_rev(v[u][e], act_a[e], act_b[e]);
+      } else if (act == OMNI_ACT_LEAKY_RELU) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = y[e] >= 0.f ? y[e] : y[e] * p.slope;
-        } else if (act != OMNI_ACT_NONE) {
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = apply_act(act, y[e], 0.f, 0.f, p.slope);
-        }
-        const auto ro = buffer_rsrc(p.out, p.o_bytes);
-        if (p.out_bf16) {
+          for (int e = 0; e < 4; ++e) v[u][e] = v[u][e] >= 0.f ? v[u][e] : v[u][e] * p.slope;
+      } else if (act != OMNI_ACT_NONE) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[u][e] = apply_act(act, v[u][e], 0.f, 0.f, p.slope);
+      }
+      const auto ro = buffer_rsrc(p.out, p.o_bytes);
+      if (p.out_bf16) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
           const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 2;
           __builtin_amdgcn_raw_buffer_store_b64(
-              u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, oo, 0, 0);
-        } else {
+              u32x2{pack_bf16x2(v[u][0], v[u][1]), pack_bf16x2(v[u][2], v[u][3])}, ro, oo, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
           const uint32_t oo = ooff[u] == kOutOfRange ? kOutOfRange : ooff[u] * 4;
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, oo, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), ro, oo, 0, 0);
         }
       }
     }
