@@ -255,17 +255,25 @@ __device__ __forceinline__ void conv_epilogue_body(const ConvParams& p, f32x4 (&
   const uint32_t rsize = F16 ? 2u : 4u;  // bytes per residual-stream element
   const bool live = walker && n_q < n_cols;
   // element offsets of flat position m in the residual-shaped tensors and in out
-  auto offsets = [&](int m, uint32_t& re, uint32_t& oe) __attribute__((always_inline)) {
+  // (for NU positions at once: the packed / general choice is one branch for all of them)
+  auto offsets = [&](const auto& m, auto& re, auto& oe) __attribute__((always_inline)) {
+    constexpr int NU = sizeof(m) / sizeof(m[0]);
     if (packed) {
-      re = (uint32_t)m * r_st + n_q;
-      oe = (uint32_t)m * o_st + n_q;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        re[u] = (uint32_t)m[u] * r_st + n_q;
+        oe[u] = (uint32_t)m[u] * o_st + n_q;
+      }
     } else {
-      int b = (int)((float)m * inv_l);  // m / L, corrected below
-      int i = m - b * L;
-      if (i < 0) { --b; i += L; }
-      if (i >= L) { ++b; i -= L; }
-      re = (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q);
-      oe = (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        int b = (int)((float)m[u] * inv_l);  // m / L, corrected below
+        int i = m[u] - b * L;
+        if (i < 0) { --b; i += L; }
+        if (i >= L) { ++b; i -= L; }
+        re[u] = (uint32_t)(b * p.r_sb + (int64_t)i * p.r_st + n_q);
+        oe[u] = (uint32_t)(b * p.o_sb + (int64_t)i * p.o_st + n_q);
+      }
     }
   };
   // Finish the NU rows r0 + u * RSTEP of a pass (positions from mp, prow rows; r0 < prow): read
@@ -276,15 +284,16 @@ __device__ __forceinline__ void conv_epilogue_body(const ConvParams& p, f32x4 (&
     constexpr int NU = decltype(nu)::value;
     uint32_t roff[NU], ooff[NU];
     f32x4 v[NU];
+    int ms[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) ms[u] = mp + min(r0 + u * RSTEP, prow - 1);
+    offsets(ms, roff, ooff);
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-      const int r = min(r0 + u * RSTEP, prow - 1);
-      uint32_t re, oe;
-      offsets(mp + r, re, oe);
       const bool ok = live && r0 + u * RSTEP < prow;
-      roff[u] = ok ? re * rsize : kOutOfRange;
-      ooff[u] = ok ? oe : kOutOfRange;
-      v[u] = *reinterpret_cast<const f32x4*>(ep + r * EPITCH + q * 4);
+      roff[u] = ok ? roff[u] * rsize : kOutOfRange;
+      ooff[u] = ok ? ooff[u] : kOutOfRange;
+      v[u] = *reinterpret_cast<const f32x4*>(ep + (ms[u] - mp) * EPITCH + q * 4);
     }
     if (p.residual) {
       if (!have_res) {
@@ -361,12 +370,14 @@ __device__ __forceinline__ void conv_epilogue_body(const ConvParams& p, f32x4 (&
         const auto rr = buffer_rsrc(p.residual, p.r_bytes);
         const int mp = m0 + pass * Tile::EPI_ROWS;
         const int prow = min(Tile::EPI_ROWS, m_end - mp);
+        int ms[UR];
+        uint32_t re[UR], oe[UR];
+#pragma unroll
+        for (int u = 0; u < UR; ++u) ms[u] = mp + min(r_first + u * RSTEP, prow - 1);
+        offsets(ms, re, oe);
 #pragma unroll
         for (int u = 0; u < UR; ++u) {
-          const int r = r_first + u * RSTEP;
-          uint32_t re, oe;
-          offsets(mp + min(r, prow - 1), re, oe);
-          const uint32_t off = live && r < prow ? re * rsize : kOutOfRange;
+          const uint32_t off = live && r_first + u * RSTEP < prow ? re[u] * rsize : kOutOfRange;
           pre[u] = load_residual4_raw(rr, off, F16);
         }
       }
