@@ -349,28 +349,35 @@ static __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu
   const u16* w2s = buf_of(STAGES & 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's W2 DMA
   __syncthreads();
+  // (the activation a compile-time constant of each copy: one branch for the whole tile)
+  auto put_h = [&](auto act_c) __attribute__((always_inline)) {
+    constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-  for (int c = 0; c < TCO; ++c) {
-    const int n = wco0 + c * 16 + ch_in_tile;
-    const f32x4 sc = *reinterpret_cast<const f32x4*>(coef + kScale * BCO + n);
-    const f32x4 bi = *reinterpret_cast<const f32x4*>(coef + kBias * BCO + n);
-    const f32x4 ma = *reinterpret_cast<const f32x4*>(coef + kMidA * BCO + n);
-    const f32x4 mb = *reinterpret_cast<const f32x4*>(coef + kMidB * BCO + n);
+    for (int c = 0; c < TCO; ++c) {
+      const int n = wco0 + c * 16 + ch_in_tile;
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(coef + kScale * BCO + n);
+      const f32x4 bi = *reinterpret_cast<const f32x4*>(coef + kBias * BCO + n);
+      const f32x4 ma = *reinterpret_cast<const f32x4*>(coef + kMidA * BCO + n);
+      const f32x4 mb = *reinterpret_cast<const f32x4*>(coef + kMidB * BCO + n);
 #pragma unroll
-    for (int t = 0; t < TP; ++t) {
-      float y[4];
+      for (int t = 0; t < TP; ++t) {
+        float y[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        y[e] = operand_act(p.mid_act, acc[c][t][e] * sc[e] + bi[e], ma[e], mb[e], p.mid_slope);
-      uint2 o;
-      o.x = pack_bf16x2(y[0], y[1]);
-      o.y = pack_bf16x2(y[2], y[3]);
-      const int pos = wp0 + t * 16 + lrow;
-      const int slot = ((n & 31) >> 3) ^ ((pos >> 1) & 3);
-      *reinterpret_cast<uint2*>(hs + ((n >> 5) * BP + pos) * kChunk + slot * 8 + (n & 7)) = o;
-      acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int e = 0; e < 4; ++e)
+          y[e] = operand_act(ACT, acc[c][t][e] * sc[e] + bi[e], ma[e], mb[e], p.mid_slope);
+        uint2 o;
+        o.x = pack_bf16x2(y[0], y[1]);
+        o.y = pack_bf16x2(y[2], y[3]);
+        const int pos = wp0 + t * 16 + lrow;
+        const int slot = ((n & 31) >> 3) ^ ((pos >> 1) & 3);
+        *reinterpret_cast<uint2*>(hs + ((n >> 5) * BP + pos) * kChunk + slot * 8 + (n & 7)) = o;
+        acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
-  }
+  };
+  if (p.mid_act == OMNI_ACT_SNAKE) put_h(std::integral_constant<int, OMNI_ACT_SNAKE>{});
+  else if (p.mid_act == OMNI_ACT_LEAKY_RELU) put_h(std::integral_constant<int, OMNI_ACT_LEAKY_RELU>{});
+  else put_h(std::integral_constant<int, OMNI_ACT_NONE>{});
   __syncthreads();  // h complete, W2 visible to every wave
   // ---- the k1 conv over h
 #pragma unroll
