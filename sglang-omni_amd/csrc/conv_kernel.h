@@ -740,33 +740,41 @@ __global__ void __launch_bounds__(64 * WAVES_CO * WAVES_P)
 
   if constexpr (FUSE2) {
     // h = mid_act(acc * scale + bias) as bf16 into LDS [BCO/32][BP][32], the four 16-byte slots
-    // of a 64-byte row rotated by (row / 4) % 4 so that the column writes of 16 positions and the
-    // operand reads of 16 rows both spread over all banks; W2 into [BCO/32][BCO][32]
+    // of a 64-byte row rotated by (row / 2) % 4 so that the operand reads of 16 rows meet no bank
+    // conflict; W2 into [BCO/32][BCO][32]. (The activation is a compile-time constant of each
+    // copy of the loop: one branch per tile, not one per element.)
     u16* hs = lds;
     u16* w2s = lds + BCO * BP;
     __syncthreads();
+    auto put_h = [&](auto act_c) __attribute__((always_inline)) {
+      constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-    for (int c = 0; c < TCO; ++c) {
-      const int n = wco0 + c * 16 + ch_in_tile;  // n0 = 0: one column tile holds every channel
-      const f32x4 sc = *reinterpret_cast<const f32x4*>(coef + kScale * BCO + n);
-      const f32x4 bi = *reinterpret_cast<const f32x4*>(coef + kBias * BCO + n);
-      const f32x4 ma = *reinterpret_cast<const f32x4*>(coef + kMidA * BCO + n);
-      const f32x4 mb = *reinterpret_cast<const f32x4*>(coef + kMidB * BCO + n);
+      for (int c = 0; c < TCO; ++c) {
+        const int n = wco0 + c * 16 + ch_in_tile;  // n0 = 0: one column tile holds every channel
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(coef + kScale * BCO + n);
+        const f32x4 bi = *reinterpret_cast<const f32x4*>(coef + kBias * BCO + n);
+        const f32x4 ma = *reinterpret_cast<const f32x4*>(coef + kMidA * BCO + n);
+        const f32x4 mb = *reinterpret_cast<const f32x4*>(coef + kMidB * BCO + n);
 #pragma unroll
-      for (int t = 0; t < TP; ++t) {
-        float y[4];
+        for (int t = 0; t < TP; ++t) {
+          float y[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          y[e] = operand_act(p.mid_act, acc[c][t][e] * sc[e] + bi[e], ma[e], mb[e], p.mid_slope);
-        uint2 o;
-        o.x = pack_bf16x2(y[0], y[1]);
-        o.y = pack_bf16x2(y[2], y[3]);
-        const int pos = wp0 + t * 16 + lrow;
-        const int slot = ((n & 31) >> 3) ^ ((pos >> 1) & 3);
-        *reinterpret_cast<uint2*>(hs + ((n >> 5) * BP + pos) * kChunk + slot * 8 + (n & 7)) = o;
-        acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int e = 0; e < 4; ++e)
+            y[e] = operand_act(ACT, acc[c][t][e] * sc[e] + bi[e], ma[e], mb[e], p.mid_slope);
+          uint2 o;
+          o.x = pack_bf16x2(y[0], y[1]);
+          o.y = pack_bf16x2(y[2], y[3]);
+          const int pos = wp0 + t * 16 + lrow;
+          const int slot = ((n & 31) >> 3) ^ ((pos >> 1) & 3);
+          *reinterpret_cast<uint2*>(hs + ((n >> 5) * BP + pos) * kChunk + slot * 8 + (n & 7)) = o;
+          acc[c][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
-    }
+    };
+    if (p.mid_act == OMNI_ACT_SNAKE) put_h(std::integral_constant<int, OMNI_ACT_SNAKE>{});
+    else if (p.mid_act == OMNI_ACT_LEAKY_RELU)
+      put_h(std::integral_constant<int, OMNI_ACT_LEAKY_RELU>{});
+    else put_h(std::integral_constant<int, OMNI_ACT_NONE>{});
 #pragma unroll
     for (int u = 0; u < W2_PIECES; ++u) {
       const int piece = tid + u * NT;
