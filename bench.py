@@ -231,7 +231,7 @@ def bench_streaming(args, device) -> dict:
 # same counter's reading for `bench.py --only copy` (a 1 GiB copy reads FETCH_SIZE = 512 MiB,
 # WRITE_SIZE = 1024 MiB: fetch x 2, write x 1). Measured, not computed here: re-measure after a
 # change to the kernel (profiles/residual_stack96_pmc.md holds the runs and their commands).
-PMC_TRAFFIC_BYTES = {"stack96": round((146094.47 * 2 + 5892.49) * 1024)}
+PMC_TRAFFIC_BYTES = {"stack96": round((146298.25 * 2 + 5894.0) * 1024)}
 PMC_TRAFFIC_SOURCE = {"stack96": "profiles/residual_stack96_pmc.md: rocprofv3 FETCH_SIZE + "
                                  "WRITE_SIZE of `bench.py --only stack96`, copy-calibrated"}
 
