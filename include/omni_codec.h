@@ -672,6 +672,21 @@ typedef struct omni_gemm_args {
 int omni_gemm(const omni_gemm_args* args, omni_stream_t stream);
 
 /*
+ * omni_gemm_rope_kv: the qkv GEMM with omni_rope_kv_write in its epilogue, one launch for
+ * F.linear(normed, qkv_weight) then apply_rope_inplace_with_kvcache (sglang_omni/models/
+ * qwen3_omni/components/code2wav.py:267, :205-215). args as for omni_gemm with epilogue
+ * OMNI_GEMM_STORE, out_dtype bf16 and n = (heads + 2 kv_heads) * head_dim: out (the qkv rows,
+ * rows = batch * frames) gets what omni_gemm then omni_rope_kv_write on out leave there, bit for
+ * bit, and the rings what omni_rope_kv_write writes. head_dim 64 (else OMNI_ERR_UNSUPPORTED);
+ * n a multiple of 128; config 0 or 1 (64 x 128 tiles of 4 waves) or 6 (of 8 waves).
+ */
+int omni_gemm_rope_kv(const omni_gemm_args* args, int64_t frames, int64_t heads,
+                      int64_t kv_heads, int64_t head_dim, const float* inv_freq,
+                      const int64_t* slot_index, const int64_t* positions, int cold,
+                      int64_t num_slots, void* key_ring, void* value_ring, int64_t ring_frames,
+                      omni_stream_t stream);
+
+/*
  * omni_channel_embedding_sum: MOSS-TTS's fused multi-channel embedding
  * (moss_tts/channel_embedding.py:13-50). out[r, :] = sum over c = 0 .. channels-1, in that
  * order, of tables[c][ids[r, c], :], the running total rounded to `dtype` (bf16, f16 or f32)

@@ -21,6 +21,7 @@
 // One wave per row wherever a row is reduced (RMSNorm, LayerNorm): the channels sit in
 // registers, 4 per lane per 256-channel group, and the reduction is a wave shuffle.
 #include "common.h"
+#include "rope.h"
 
 namespace {
 
@@ -70,20 +71,6 @@ OMNI_DEVICE void store_bf16x8(u16* p, const float v[8]) {
   w.z = (uint32_t)float_to_bits_bf16(v[4]) | ((uint32_t)float_to_bits_bf16(v[5]) << 16);
   w.w = (uint32_t)float_to_bits_bf16(v[6]) | ((uint32_t)float_to_bits_bf16(v[7]) << 16);
   *reinterpret_cast<uint4*>(p) = w;
-}
-
-// A row's start position in its stream: 0 for a first decode (or no slot state), else the
-// slot's frame count. Rows whose slot is out of range read position 0 and write no state.
-OMNI_DEVICE int64_t row_start(const int64_t* slot_index, const int64_t* positions, int cold,
-                              int64_t num_slots, int64_t b, int64_t* slot_out) {
-  int64_t slot = -1;
-  if (slot_index) {
-    slot = slot_index[b];
-    if (slot < 0 || slot >= num_slots) slot = -1;
-  }
-  *slot_out = slot;
-  if (cold || !positions || slot < 0) return 0;
-  return positions[slot];
 }
 
 // ------------------------------------------------------------------------------ RMSNorm
@@ -184,12 +171,9 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeParams p) {
     const int head = item / half;
     const int i = item - head * half;
     const int col = head * p.head_dim + i;  // q heads, then k heads, are contiguous
-    float s, c;
-    sincosf(fpos * p.inv_freq[i], &s, &c);
-    const float x1 = bits_to_float_bf16(row[col]);
-    const float x2 = bits_to_float_bf16(row[col + half]);
-    const u16 y1 = float_to_bits_bf16(x1 * c - x2 * s);
-    const u16 y2 = float_to_bits_bf16(x2 * c + x1 * s);
+    u16 y1, y2;
+    rope_pair(bits_to_float_bf16(row[col]), bits_to_float_bf16(row[col + half]),
+              fpos * p.inv_freq[i], &y1, &y2);
     row[col] = y1;
     row[col + half] = y2;
     if (ring && head >= p.heads) {

@@ -25,6 +25,7 @@
 // same bits.
 #include "common.h"
 #include "omni_codec.h"
+#include "rope.h"
 
 namespace {
 
@@ -49,6 +50,16 @@ struct GemmParams {
   uint32_t out_bytes;
   int out_stride;
   int row_tiles, col_tiles;
+  // the rotary epilogue (omni_gemm_rope_kv): rows are batch * frames tokens, out the qkv rows
+  int frames, heads, kv_heads;
+  const float* inv_freq;
+  const int64_t* slot_index;
+  const int64_t* positions;
+  int cold;
+  int64_t num_slots;
+  u16* key_ring;
+  u16* value_ring;
+  int64_t ring_frames;
 };
 
 OMNI_DEVICE uint32_t pack_bf16x2(float a, float b) {
@@ -75,9 +86,123 @@ struct GemmTile {
   static_assert((BM * kRowSlots / 64) % NW == 0 && (BN * kRowSlots / 64) % NW == 0, "DMA split");
 };
 
-template <int WM, int WN, int TM, int TN, int S>
+// The rotary epilogue of the qkv GEMM: a wave's 64 columns are one head (q heads, then k heads,
+// then v heads), and lane (g, n) holds columns 16 j + 4 g + e of tile j, so the neox pair (i,
+// i + 32) of a q or k head sits in the same lane, in tiles j and j + 2. Each value is rounded to
+// bf16 first, as the stored qkv would be, then turned at its token's position and rounded again;
+// the rotated k and the v of each token also go to its slot's ring row. What the epilogue reads
+// besides the accumulators (the rows' slots, then their positions, inv_freq, the bias) is loaded
+// before and during the K loop: at the end it would be two dependent round trips to memory.
+template <int TM>
+struct RopeRows {
+  int64_t slot[TM];  // slot_index of the row's stream (-1: none, or out of range)
+  int64_t pos[TM];   // the row's position: its stream's start + its frame
+  f32x4 inv[2];      // inv_freq of the lane's pairs 16 j + 4 g + e, j = 0, 1
+  f32x4 bias[4];     // the lane's bias of tiles 0 .. 3 (zeros without a bias)
+};
+
+// Before the first DMA: the slots, inv_freq and the bias, as buffer loads whose absent operands
+// read zeros (no branch around a load: the wait for the slots then covers only these loads).
+template <int TM>
+OMNI_DEVICE void rope_rows_start(const GemmParams& p, int row0, int c0, int ln, RopeRows<TM>& r) {
+  const int g4 = (ln >> 4) * 4;
+  const auto srs = buffer_rsrc(p.slot_index, p.slot_index ? (uint32_t)(p.rows / p.frames) * 8u : 0u);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = row0 + i * 16 + (ln & 15);
+    const bool ok = row < p.rows && p.slot_index != nullptr;
+    const u32x2 w = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs, ok ? (uint32_t)(row / p.frames) * 8u : kOutOfRange, 0, 0));
+    const int64_t slot = ok ? (int64_t)(((uint64_t)w[1] << 32) | w[0]) : -1;
+    r.slot[i] = (slot < 0 || slot >= p.num_slots) ? -1 : slot;
+  }
+  const auto frs = buffer_rsrc(p.inv_freq, 128u);
+  const auto brs = buffer_rsrc(p.bias, p.bias ? (uint32_t)p.n * 4u : 0u);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    r.inv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(frs, (uint32_t)(16 * j + g4) * 4u, 0, 0));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    r.bias[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, (uint32_t)(c0 + 16 * j + g4) * 4u, 0, 0));
+}
+
+// After the first DMAs are issued: each row's position (0 for a first decode or no slot).
+template <int TM>
+OMNI_DEVICE void rope_rows_positions(const GemmParams& p, int row0, int ln, RopeRows<TM>& r) {
+  const auto prs = buffer_rsrc(p.positions, p.positions ? (uint32_t)p.num_slots * 8u : 0u);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = row0 + i * 16 + (ln & 15);
+    const bool warm = !p.cold && p.positions != nullptr && r.slot[i] >= 0;
+    const u32x2 w = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(prs, warm ? (uint32_t)r.slot[i] * 8u : kOutOfRange, 0, 0));
+    const int64_t start = warm ? (int64_t)(((uint64_t)w[1] << 32) | w[0]) : 0;
+    r.pos[i] = start + (row < p.rows ? row % p.frames : 0);
+  }
+}
+
+template <int TM>
+OMNI_DEVICE void rope_kv_epilogue(const GemmParams& p, const f32x4 (&acc)[TM][4],
+                                  const RopeRows<TM>& r, int row0, int c0, int ln,
+                                  __amdgpu_buffer_rsrc_t orsrc) {
+  const int head = c0 >> 6;
+  const int qk_heads = p.heads + p.kv_heads;
+  const int kv_width = p.kv_heads * 64;
+  const int g4 = (ln >> 4) * 4;
+  // acc + bias as the plain store forms it (no add without a bias: -0 stays -0)
+  f32x4 v[TM][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) v[i][j] = p.bias ? acc[i][j] + r.bias[j] : acc[i][j];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = row0 + i * 16 + (ln & 15);
+    const bool row_ok = row < p.rows;
+    const int64_t pos = r.pos[i];
+    const bool ring = row_ok && r.slot[i] >= 0 && p.key_ring != nullptr;
+    const int64_t ring_row = ring ? r.slot[i] * p.ring_frames + pos % p.ring_frames : 0;
+    if (head < qk_heads) {
+      const float fpos = (float)pos;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ci = 16 * j + g4;  // the pair index of element 0
+        u16 y1[4], y2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x1 = bits_to_float_bf16(float_to_bits_bf16(v[i][j][e]));
+          const float x2 = bits_to_float_bf16(float_to_bits_bf16(v[i][j + 2][e]));
+          rope_pair(x1, x2, fpos * r.inv[j][e], &y1[e], &y2[e]);
+        }
+        const u32x2 v1 = {(uint32_t)y1[0] | ((uint32_t)y1[1] << 16), (uint32_t)y1[2] | ((uint32_t)y1[3] << 16)};
+        const u32x2 v2 = {(uint32_t)y2[0] | ((uint32_t)y2[1] << 16), (uint32_t)y2[2] | ((uint32_t)y2[3] << 16)};
+        const uint32_t off = row_ok ? (uint32_t)(row * p.out_stride + c0 + ci) * 2u : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b64(v1, orsrc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(v2, orsrc, row_ok ? off + 64u : kOutOfRange, 0, 0);
+        if (ring && head >= p.heads) {
+          u16* k = p.key_ring + ring_row * kv_width + (c0 - p.heads * 64) + ci;
+          *reinterpret_cast<u32x2*>(k) = v1;
+          *reinterpret_cast<u32x2*>(k + 32) = v2;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ci = 16 * j + g4;
+        const u32x2 o = {pack_bf16x2(v[i][j][0], v[i][j][1]), pack_bf16x2(v[i][j][2], v[i][j][3])};
+        const uint32_t off = row_ok ? (uint32_t)(row * p.out_stride + c0 + ci) * 2u : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b64(o, orsrc, off, 0, 0);
+        if (ring)
+          *reinterpret_cast<u32x2*>(p.value_ring + ring_row * kv_width + (c0 - qk_heads * 64) + ci) = o;
+      }
+    }
+  }
+}
+
+template <int WM, int WN, int TM, int TN, int S, bool ROPE = false>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const GemmParams p) {
   using T = GemmTile<WM, WN, TM, TN, S>;
+  static_assert(!ROPE || TN == 4, "the rotary epilogue takes one 64-column head per wave");
   extern __shared__ __attribute__((aligned(16))) u16 lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -145,9 +270,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const GemmParams p) 
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  RopeRows<ROPE ? TM : 1> rope;
+  if constexpr (ROPE) rope_rows_start<TM>(p, m0 + wm * TM * 16, n0 + wn * TN * 16, lane, rope);
 #pragma unroll
   for (int kt = 0; kt < S - 1; ++kt)
     if (kt < stages) issue(kt);
+  if constexpr (ROPE) rope_rows_positions<TM>(p, m0 + wm * TM * 16, lane, rope);
   for (int kt = 0; kt < stages; ++kt) {
     // this wave's DMA of stage kt is complete once at most the later stages' instructions are
     // outstanding; then every wave's (the barrier), which also ends every read of the buffer that
@@ -182,6 +310,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const GemmParams p) 
   // 4 (lane / 16) .. + 3 of tile (i, j)
   const auto orsrc = buffer_rsrc(p.out, p.out_bytes);
   const int ln = opaque_copy(lane);
+  if constexpr (ROPE) {
+    rope_kv_epilogue<TM>(p, acc, rope, m0 + wm * TM * 16, n0 + wn * TN * 16, ln, orsrc);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int row = m0 + wm * TM * 16 + i * 16 + (ln & 15);
@@ -245,12 +377,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(const GemmParams p) 
   }
 }
 
-template <int WM, int WN, int TM, int TN, int S>
+template <int WM, int WN, int TM, int TN, int S, bool ROPE = false>
 int launch(GemmParams p, hipStream_t stream) {
   using T = GemmTile<WM, WN, TM, TN, S>;
   p.row_tiles = (p.rows + T::BM - 1) / T::BM;
   p.col_tiles = (p.n + T::BN - 1) / T::BN;
-  auto k = gemm_kernel<WM, WN, TM, TN, S>;
+  auto k = gemm_kernel<WM, WN, TM, TN, S, ROPE>;
   static const bool raised = [&] {
     return hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)T::lds_bytes()) == hipSuccess;
@@ -279,14 +411,15 @@ bool aligned_to(const void* ptr, int bytes) {
   return (reinterpret_cast<uintptr_t>(ptr) & (uintptr_t)(bytes - 1)) == 0;
 }
 
-}  // namespace
-
-extern "C" int omni_gemm(const omni_gemm_args* a, omni_stream_t stream) {
+// The checks and kernel parameters shared by the entry points; kNothingToDo (with *out
+// untouched): rows = 0.
+constexpr int kNothingToDo = -1;  // no OMNI_ERR_* code
+int gemm_params(const omni_gemm_args* a, GemmParams* out) {
   if (a == nullptr || a->a == nullptr || a->w == nullptr || a->out == nullptr)
     return OMNI_ERR_INVALID_ARG;
   if (a->rows < 0 || a->k <= 0 || a->n <= 0 || a->k % kBK != 0 || a->n % 64 != 0)
     return OMNI_ERR_INVALID_ARG;
-  if (a->rows == 0) return OMNI_OK;
+  if (a->rows == 0) return kNothingToDo;
   const int epi = a->epilogue;
   if (epi != OMNI_GEMM_STORE && epi != OMNI_GEMM_SILU_MUL && epi != OMNI_GEMM_GELU &&
       epi != OMNI_GEMM_SCALED_RESIDUAL)
@@ -320,7 +453,8 @@ extern "C" int omni_gemm(const omni_gemm_args* a, omni_stream_t stream) {
   const int64_t limit = 0x7fffffffLL;
   if (a_bytes >= limit || w_bytes >= limit || o_bytes >= limit || r_bytes >= limit)
     return OMNI_ERR_UNSUPPORTED;
-  GemmParams p{};
+  GemmParams& p = *out;
+  p = GemmParams{};
   p.a = a->a;
   p.a_bytes = (uint32_t)a_bytes;
   p.a_stride = (int)a->a_stride;
@@ -339,6 +473,16 @@ extern "C" int omni_gemm(const omni_gemm_args* a, omni_stream_t stream) {
   p.out = a->out;
   p.out_bytes = (uint32_t)o_bytes;
   p.out_stride = (int)a->out_stride;
+  return OMNI_OK;
+}
+
+}  // namespace
+
+extern "C" int omni_gemm(const omni_gemm_args* a, omni_stream_t stream) {
+  GemmParams p;
+  const int rc = gemm_params(a, &p);
+  if (rc != OMNI_OK) return rc == kNothingToDo ? OMNI_OK : rc;
+  const int epi = a->epilogue;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // The tiles (rows x columns: waves, ring stages, LDS): 1: 64 x 128: 4, 3, 72 KiB; 2: 64 x 64:
   // 4, 4, 64 KiB; 3: 64 x 128: 8 (2 x 4), 3, 72 KiB; 4: 64 x 64: 8 (2 x 4), 4, 64 KiB; 5: 32 x
@@ -368,4 +512,47 @@ extern "C" int omni_gemm(const omni_gemm_args* a, omni_stream_t stream) {
     default: break;
   }
   return OMNI_ERR_INVALID_ARG;
+}
+
+extern "C" int omni_gemm_rope_kv(const omni_gemm_args* a, int64_t frames, int64_t heads,
+                                 int64_t kv_heads, int64_t head_dim, const float* inv_freq,
+                                 const int64_t* slot_index, const int64_t* positions, int cold,
+                                 int64_t num_slots, void* key_ring, void* value_ring,
+                                 int64_t ring_frames, omni_stream_t stream) {
+  // the checks of omni_rope_kv_write, and a plain bf16 store of exactly the q, k, v columns
+  if (a == nullptr || a->epilogue != OMNI_GEMM_STORE || a->out_dtype != OMNI_DTYPE_BF16)
+    return OMNI_ERR_INVALID_ARG;
+  if (!inv_freq || frames < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads)
+    return OMNI_ERR_INVALID_ARG;
+  if (head_dim != 64) return OMNI_ERR_UNSUPPORTED;
+  if (a->n != (heads + 2 * kv_heads) * head_dim || a->rows % frames) return OMNI_ERR_INVALID_ARG;
+  if ((key_ring != nullptr) != (value_ring != nullptr)) return OMNI_ERR_INVALID_ARG;
+  if (key_ring && (!slot_index || ring_frames < 1)) return OMNI_ERR_INVALID_ARG;
+  if (!cold && (!slot_index || !positions)) return OMNI_ERR_INVALID_ARG;
+  GemmParams p;
+  const int rc = gemm_params(a, &p);
+  if (rc != OMNI_OK) return rc == kNothingToDo ? OMNI_OK : rc;
+  p.frames = (int)frames;
+  p.heads = (int)heads;
+  p.kv_heads = (int)kv_heads;
+  p.inv_freq = inv_freq;
+  p.slot_index = slot_index;
+  p.positions = positions;
+  p.cold = cold ? 1 : 0;
+  p.num_slots = num_slots;
+  p.key_ring = static_cast<u16*>(key_ring);
+  p.value_ring = static_cast<u16*>(value_ring);
+  p.ring_frames = ring_frames;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // one 64-column head per wave: 64 x 128 tiles of 4 waves (2 x 2, each 32 rows) or of 8 (4 x
+  // 2, each 16 rows). At 768 x 1024 -> 3072 with rings: 15.3 and 16.1 us (the two-launch form
+  // 19.5 us; its GEMM alone 11.1 - 12.1 us, the ring writes ~2.2 us of the difference)
+  const int config = a->config == 0 ? 1 : a->config;
+  if (a->n % 128 != 0) return OMNI_ERR_UNSUPPORTED;
+  switch (config) {
+    case 1: return launch<2, 2, 2, 4, 3, true>(p, s);
+    case 6: return launch<4, 2, 1, 4, 3, true>(p, s);
+    default: break;
+  }
+  return OMNI_ERR_UNSUPPORTED;
 }

@@ -247,6 +247,8 @@ SIGNATURES: dict[str, list] = {
     "omni_bias_scale_residual": [_PTR, _I64, _I64, _PTR, _I64, _PTR, _PTR, _PTR, _I64, _PTR],
     "omni_advance_positions": [_PTR, _I64, _PTR, _I64, _I64, _INT, _PTR],
     "omni_gemm": [ctypes.POINTER(GemmArgs), _PTR],
+    "omni_gemm_rope_kv": [ctypes.POINTER(GemmArgs), _I64, _I64, _I64, _I64, _PTR, _PTR, _PTR, _INT,
+                          _I64, _PTR, _PTR, _I64, _PTR],
     "omni_resblock_pair": [ctypes.POINTER(ConvArgs), ctypes.POINTER(ConvArgs), _PTR],
     "omni_channel_embedding_sum": [_PTR, _INT, _I64, _I64, _I64, _I64, _PTR, _PTR, _INT, _I64, _PTR,
                                    _PTR],

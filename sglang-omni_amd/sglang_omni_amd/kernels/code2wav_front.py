@@ -31,6 +31,18 @@ def _num_slots(positions: torch.Tensor | None, key_ring: torch.Tensor | None,
     return counts.pop() if counts else 0
 
 
+def _check_rings(key_ring: torch.Tensor | None, value_ring: torch.Tensor | None,
+                 kv_width: int) -> None:
+    """The K / V rings: both or neither, contiguous bf16 [slots * ring_frames, kv_width]."""
+    if (key_ring is None) != (value_ring is None):
+        raise ValueError("key_ring and value_ring come together")
+    for ring in (key_ring, value_ring):
+        if ring is not None and (ring.dtype != torch.bfloat16 or ring.dim() != 2
+                                 or not ring.is_contiguous() or ring.shape[1] != kv_width
+                                 or ring.shape != key_ring.shape):
+            raise ValueError(f"the rings must be contiguous bf16 [slots * ring_frames, {kv_width}]")
+
+
 def rms_norm_residual(h: torch.Tensor, weight: torch.Tensor, eps: float, normed: torch.Tensor, *,
                       delta: torch.Tensor | None = None,
                       scale: torch.Tensor | None = None) -> torch.Tensor:
@@ -68,6 +80,7 @@ def rope_kv_write(qkv: torch.Tensor, batch: int, heads: int, kv_heads: int, head
     if qkv.shape[0] % max(batch, 1):
         raise ValueError("qkv rows must be batch * frames")
     frames = qkv.shape[0] // max(batch, 1)
+    _check_rings(key_ring, value_ring, kv_heads * head_dim)
     num_slots = _num_slots(positions, key_ring, ring_frames)
     lib = N.load_library()
     N.check(lib.omni_rope_kv_write(qkv.data_ptr(), batch, frames, qkv.stride(0), heads, kv_heads,

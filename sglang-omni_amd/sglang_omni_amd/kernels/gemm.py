@@ -13,6 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _native as N
+from .code2wav_front import _check_rings, _num_slots
 
 STORE, SILU_MUL, GELU, SCALED_RESIDUAL = (N.GEMM_STORE, N.GEMM_SILU_MUL, N.GEMM_GELU,
                                           N.GEMM_SCALED_RESIDUAL)
@@ -97,11 +98,18 @@ def linear(x: torch.Tensor, weight: LinearWeight, out: torch.Tensor, *,
             raise ValueError("residual must be float32 like out, with contiguous rows")
         if scale.dtype != torch.float32 or scale.shape != (weight.out_features,):
             raise ValueError("scale must be float32 [out_features]")
+    args = _gemm_args(x, weight, out, epilogue, scale, residual, config)
+    lib = N.load_library()
+    N.check(lib.omni_gemm(ctypes.byref(args), N.stream_handle(x.device)), "omni_gemm")
+    return out
+
+
+def _gemm_args(x, weight, out, epilogue, scale, residual, config):
     args = N.GemmArgs()
     args.a = x.data_ptr()
     args.a_stride = x.stride(0)
     args.w = weight.weight.data_ptr()
-    args.rows = rows
+    args.rows = x.shape[0]
     args.k = weight.in_features
     args.n = weight.weight.shape[0]
     args.bias = N.ptr(weight.bias)
@@ -113,6 +121,43 @@ def linear(x: torch.Tensor, weight: LinearWeight, out: torch.Tensor, *,
     args.residual_stride = 0 if residual is None else residual.stride(0)
     args.out = out.data_ptr()
     args.out_stride = out.stride(0)
+    return args
+
+
+def linear_rope_kv(x: torch.Tensor, weight: LinearWeight, qkv: torch.Tensor, batch: int,
+                   heads: int, kv_heads: int, head_dim: int, inv_freq: torch.Tensor, *,
+                   slot_index: torch.Tensor | None = None, positions: torch.Tensor | None = None,
+                   cold: bool = True, key_ring: torch.Tensor | None = None,
+                   value_ring: torch.Tensor | None = None, ring_frames: int = 0,
+                   config: int = 0) -> torch.Tensor:
+    """qkv = x @ W^T (+ bias) with the rotary embedding of its q and k heads and the new K / V
+    rows into the rings in the GEMM's epilogue: the bits of ``linear(x, weight, qkv)`` followed
+    by ``code2wav_front.rope_kv_write(qkv, batch, ...)``, in one launch (qkv_proj then
+    apply_rope_inplace_with_kvcache, code2wav.py:267, :205-215). Returns qkv."""
+    N.require_device(x, weight.weight, weight.bias, qkv, inv_freq, slot_index, positions,
+                     key_ring, value_ring)
+    if weight.gated:
+        raise ValueError("the qkv weight is not gated")
+    if qkv.dtype != torch.bfloat16:
+        raise ValueError("qkv must be bf16")
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be bf16 [rows, in_features] with contiguous rows")
+    rows = x.shape[0]
+    if x.shape[1] != weight.in_features:
+        raise ValueError(f"x has {x.shape[1]} features, the weight takes {weight.in_features}")
+    if qkv.dim() != 2 or qkv.shape != (rows, weight.out_features) or qkv.stride(1) != 1:
+        raise ValueError(f"qkv must be [{rows}, {weight.out_features}] with contiguous rows")
+    if batch < 1 or rows % batch:
+        raise ValueError("x rows must be batch * frames")
+    if slot_index is not None and (slot_index.dtype != torch.int64 or slot_index.numel() < batch):
+        raise ValueError("slot_index must be int64 with one entry per batch row")
+    _check_rings(key_ring, value_ring, kv_heads * head_dim)
+    num_slots = _num_slots(positions, key_ring, ring_frames)
+    args = _gemm_args(x, weight, qkv, STORE, None, None, config)
     lib = N.load_library()
-    N.check(lib.omni_gemm(ctypes.byref(args), N.stream_handle(x.device)), "omni_gemm")
-    return out
+    N.check(lib.omni_gemm_rope_kv(ctypes.byref(args), rows // batch, heads, kv_heads, head_dim,
+                                  inv_freq.data_ptr(), N.ptr(slot_index), N.ptr(positions),
+                                  int(cold), num_slots, N.ptr(key_ring), N.ptr(value_ring),
+                                  ring_frames, N.stream_handle(x.device)),
+            "omni_gemm_rope_kv")
+    return qkv

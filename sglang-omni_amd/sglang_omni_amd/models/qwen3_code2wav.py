@@ -12,8 +12,8 @@ A decode step on channels-last activations:
     rvq_gather_sum (mean form)            codes -> h (float32 residual stream)
     per layer (8):
       rms_norm_residual                   h -> normed (bf16)
-      GEMM qkv                            normed -> qkv
-      rope_kv_write                       rotary on q, k in place; new K / V into the rings
+      GEMM qkv, rotary epilogue           normed -> qkv, q and k rotated at their positions;
+                                          the new K / V rows into the rings
       window_attention                    q over the 72-frame window -> attn
       GEMM o, scaled residual epilogue    h += scale * (attn @ W_o^T)
       rms_norm_residual                   normed = RMSNorm(h)
@@ -43,7 +43,7 @@ import torch
 
 from ..kernels import code2wav_front as F
 from ..kernels.conv import fused_conv, pack_conv1d, pack_conv_transpose1d
-from ..kernels.gemm import GELU, SCALED_RESIDUAL, linear, pack_linear
+from ..kernels.gemm import GELU, SCALED_RESIDUAL, linear, linear_rope_kv, pack_linear
 from ..kernels.rvq import rvq_gather_sum
 from .configs import Qwen3Code2WavConfig, Qwen3TTSCodecConfig
 from .dac_codec import CodecStatePool, DacCodecDecoder, _Workspace
@@ -188,6 +188,10 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
         self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2,
                                                                 dtype=torch.float32)
                                                    / cfg.head_dim))).to(dev).contiguous()
+        # one launch for the qkv GEMM and the rotary embedding where a wave's 64 columns are one
+        # head (64-wide heads, q + k + v columns a multiple of 128); else two, with the same bits
+        qkv_cols = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+        self.fused_rope = cfg.head_dim == 64 and qkv_cols % 128 == 0
         self.upsamplers = []
         for i, factor in enumerate(cfg.upsampling_ratios):
             p = f"upsample.{i}.1"
@@ -313,10 +317,17 @@ class Qwen3Code2WavDecoder(DacCodecDecoder):
                 ring = {"slot_index": slots, "positions": pool.frame_positions,
                         "key_ring": pool.keys[i], "value_ring": pool.values[i],
                         "ring_frames": pool.ring_frames}
-            with timer.launch("front_gemm", 2.0 * m * c * qkv.shape[1]):
-                linear(normed, layer["qkv"], qkv)
-            with timer.launch("front_elementwise", 0.0):
-                F.rope_kv_write(qkv, batch, heads, kv_heads, hd, self.inv_freq, cold=cold, **ring)
+            if self.fused_rope:
+                # the rotary embedding and the K / V ring writes in the qkv GEMM's epilogue
+                with timer.launch("front_gemm", 2.0 * m * c * qkv.shape[1]):
+                    linear_rope_kv(normed, layer["qkv"], qkv, batch, heads, kv_heads, hd,
+                                   self.inv_freq, cold=cold, **ring)
+            else:
+                with timer.launch("front_gemm", 2.0 * m * c * qkv.shape[1]):
+                    linear(normed, layer["qkv"], qkv)
+                with timer.launch("front_elementwise", 0.0):
+                    F.rope_kv_write(qkv, batch, heads, kv_heads, hd, self.inv_freq, cold=cold,
+                                    **ring)
             # a first decode attends to its own frames: the keys are in qkv already
             attend_ring = {} if cold else ring
             with timer.launch("front_attention", 4.0 * m * heads * hd * cfg.sliding_window):

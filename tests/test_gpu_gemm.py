@@ -2,7 +2,9 @@
 float32 reference of the same op on the same bf16 operands: every epilogue (STORE, SILU_MUL with
 the 16-row interleave of a merged gate / up weight, GELU, SCALED_RESIDUAL into float32 in place and
 into bf16), every tile, ragged row counts and strided rows; then the property the streaming decode
-relies on: a row's bits do not depend on the rows batched with it, nor on the tile."""
+relies on: a row's bits do not depend on the rows batched with it, nor on the tile. Last, the qkv
+GEMM with the rotary embedding and the K / V ring writes in its epilogue (``linear_rope_kv``)
+against ``linear`` followed by ``rope_kv_write``: the same bits in qkv and in the rings."""
 
 from __future__ import annotations
 
@@ -13,8 +15,9 @@ import pytest
 import torch
 
 from sglang_omni_amd import _native as N
+from sglang_omni_amd.kernels import code2wav_front as F
 from sglang_omni_amd.kernels.gemm import (GELU, SCALED_RESIDUAL, SILU_MUL, STORE, linear,
-                                          pack_linear)
+                                          linear_rope_kv, pack_linear)
 
 pytestmark = pytest.mark.gpu
 
@@ -164,3 +167,77 @@ def test_contract(gpu):
     assert lib.omni_gemm(ctypes.byref(args), N.stream_handle(gpu)) == N.INVALID_ARG
     args.k, args.out_dtype = 1024, N.DTYPE_F32  # float32 out only for the scaled residual
     assert lib.omni_gemm(ctypes.byref(args), N.stream_handle(gpu)) == N.INVALID_ARG
+
+
+def _inv_freq(gpu, theta=10000.0):
+    return (1.0 / (theta ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))).to(gpu)
+
+
+@pytest.mark.parametrize("batch,frames,heads,kv_heads,bias,config",
+                         [(3, 11, 4, 2, False, 0), (64, 12, 16, 16, False, 0),
+                          (2, 37, 2, 1, True, 1), (1, 1, 4, 4, True, 6), (5, 40, 8, 4, False, 1)])
+def test_rope_kv_epilogue_first_decode(gpu, batch, frames, heads, kv_heads, bias, config):
+    """A first decode (cold, no rings): the rotated q and k at positions 0 .. frames - 1."""
+    rows, k, n = batch * frames, 1024, (heads + 2 * kv_heads) * 64
+    x, w, b = _operands(rows, k, n, rows + n, gpu, bias=bias)
+    lw = pack_linear(w, b).to(gpu)
+    ref = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+    linear(x, lw, ref)
+    F.rope_kv_write(ref, batch, heads, kv_heads, 64, _inv_freq(gpu))
+    got = torch.full((rows, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+    linear_rope_kv(x, lw, got, batch, heads, kv_heads, 64, _inv_freq(gpu), config=config)
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("cold", [False, True])
+def test_rope_kv_epilogue_rings(gpu, cold):
+    """Rows at their slots' positions (one far along, one slot out of range, one slot -1): qkv
+    and both rings hold the bits of the two-launch form, other ring rows untouched."""
+    batch, frames, heads, kv_heads, ring_frames, slots = 4, 7, 4, 2, 10, 6
+    rows, k, n = batch * frames, 512, (heads + 2 * kv_heads) * 64
+    x, w, b = _operands(rows, k, n, 21, gpu, bias=True)
+    lw = pack_linear(w, b).to(gpu)
+    positions = torch.tensor([0, 40, 7, 1000, 123457, 3], dtype=torch.int64, device=gpu)
+    index = torch.tensor([3, 1, -1, 9], dtype=torch.int64, device=gpu)
+    g = torch.Generator().manual_seed(22)
+    keys = torch.randn(slots * ring_frames, kv_heads * 64, generator=g).to(torch.bfloat16).to(gpu)
+    values = torch.randn(slots * ring_frames, kv_heads * 64, generator=g).to(torch.bfloat16).to(gpu)
+    ring = dict(slot_index=index, positions=positions, cold=cold, ring_frames=ring_frames)
+    ref = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+    k_ref, v_ref = keys.clone(), values.clone()
+    linear(x, lw, ref)
+    F.rope_kv_write(ref, batch, heads, kv_heads, 64, _inv_freq(gpu), key_ring=k_ref,
+                    value_ring=v_ref, **ring)
+    got = torch.full((rows, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+    k_got, v_got = keys.clone(), values.clone()
+    linear_rope_kv(x, lw, got, batch, heads, kv_heads, 64, _inv_freq(gpu), key_ring=k_got,
+                   value_ring=v_got, **ring)
+    assert torch.equal(got, ref)
+    assert torch.equal(k_got, k_ref) and torch.equal(v_got, v_ref)
+    assert not torch.equal(k_got, keys)  # the in-range rows were written
+
+
+def test_rope_kv_epilogue_contract(gpu):
+    x, w, _ = _operands(24, 512, 512, 23, gpu)
+    lw = pack_linear(w).to(gpu)
+    qkv = torch.empty(24, 512, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="rings"):
+        linear_rope_kv(x, lw, qkv, 2, 4, 2, 64, _inv_freq(gpu), slot_index=torch.zeros(
+            2, dtype=torch.int64, device=gpu), key_ring=torch.empty(
+            40, 64, dtype=torch.bfloat16, device=gpu), value_ring=torch.empty(
+            40, 64, dtype=torch.bfloat16, device=gpu), ring_frames=10)
+    with pytest.raises(ValueError, match="batch"):
+        linear_rope_kv(x, lw, qkv, 5, 4, 2, 64, _inv_freq(gpu))
+    # n must be (heads + 2 kv_heads) * 64; head_dim 64 only
+    lib = N.load_library()
+    args = N.GemmArgs()
+    args.a, args.a_stride, args.w = x.data_ptr(), 512, lw.weight.data_ptr()
+    args.rows, args.k, args.n = 24, 512, 512
+    args.out, args.out_stride, args.out_dtype = qkv.data_ptr(), 512, N.DTYPE_BF16
+    inv = _inv_freq(gpu)
+    call = lambda heads, kv, hd: lib.omni_gemm_rope_kv(
+        ctypes.byref(args), 12, heads, kv, hd, inv.data_ptr(), None, None, 1, 0, None, None, 0,
+        N.stream_handle(gpu))
+    assert call(2, 2, 64) == N.INVALID_ARG
+    assert call(4, 2, 32) == N.UNSUPPORTED
+    assert call(4, 2, 64) == N.OK
