@@ -91,45 +91,60 @@ struct RmsParams {
   int64_t normed_stride;
 };
 
+// One wave per row. Every load of the row (h, and the weights) is issued before the first use
+// of any of them, and the residual add's stores come after all of them: a store into h between
+// two groups' loads would keep the compiler from moving the later loads above it, one memory
+// round trip per 256-channel group. GROUPS > 0 fixes the group count (unrolled, no guards);
+// GROUPS = 0 reads it from p.groups. The sum of squares runs group by group, element by element,
+// in both forms.
+template <int GROUPS>
 __global__ __launch_bounds__(256) void rms_norm_residual_kernel(RmsParams p) {
+  constexpr int NG = GROUPS > 0 ? GROUPS : kMaxGroups;
+  const int groups = GROUPS > 0 ? GROUPS : p.groups;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.rows) return;
   float* hr = p.h + row * p.channels;
-  float v[kMaxGroups][4];
-  float ss = 0.f;
+  f32x4 x[NG], w[NG];
 #pragma unroll
-  for (int g = 0; g < kMaxGroups; ++g) {
-    if (g < p.groups) {
+  for (int g = 0; g < NG; ++g) {
+    if (GROUPS > 0 || g < groups) {
       const int c = (g * kWave + lane) * 4;
-      const float4 x = *reinterpret_cast<const float4*>(hr + c);
-      float a[4] = {x.x, x.y, x.z, x.w};
-      if (p.delta) {
-        float d[4];
-        load_bf16x4(p.delta + row * p.delta_stride + c, d);
-        const float4 s = *reinterpret_cast<const float4*>(p.scale + c);
-        a[0] += s.x * d[0];
-        a[1] += s.y * d[1];
-        a[2] += s.z * d[2];
-        a[3] += s.w * d[3];
-        *reinterpret_cast<float4*>(hr + c) = make_float4(a[0], a[1], a[2], a[3]);
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[g][k] = a[k];
-        ss += a[k] * a[k];
-      }
+      x[g] = *reinterpret_cast<const f32x4*>(hr + c);
+      w[g] = *reinterpret_cast<const f32x4*>(p.weight + c);
     }
   }
+  if (p.delta) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (GROUPS > 0 || g < groups) {
+        const int c = (g * kWave + lane) * 4;
+        float d[4];
+        load_bf16x4(p.delta + row * p.delta_stride + c, d);
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(p.scale + c);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[g][k] += sc[k] * d[k];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+      if (GROUPS > 0 || g < groups)
+        *reinterpret_cast<f32x4*>(hr + (g * kWave + lane) * 4) = x[g];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+    if (GROUPS > 0 || g < groups)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ss += x[g][k] * x[g][k];
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)p.channels + p.eps);
 #pragma unroll
-  for (int g = 0; g < kMaxGroups; ++g) {
-    if (g < p.groups) {
+  for (int g = 0; g < NG; ++g) {
+    if (GROUPS > 0 || g < groups) {
       const int c = (g * kWave + lane) * 4;
-      const float4 w = *reinterpret_cast<const float4*>(p.weight + c);
-      const float o[4] = {w.x * (v[g][0] * inv), w.y * (v[g][1] * inv), w.z * (v[g][2] * inv),
-                          w.w * (v[g][3] * inv)};
+      const float o[4] = {w[g][0] * (x[g][0] * inv), w[g][1] * (x[g][1] * inv),
+                          w[g][2] * (x[g][2] * inv), w[g][3] * (x[g][3] * inv)};
       store_bf16x4(p.normed + row * p.normed_stride + c, o);
     }
   }
@@ -621,7 +636,9 @@ extern "C" int omni_rms_norm_residual(float* h, int64_t rows, int64_t channels, 
   if (rows == 0) return OMNI_OK;
   RmsParams p{h, rows, (int)channels, (int)(channels / 256), static_cast<const u16*>(delta),
               delta_stride, scale, weight, eps, static_cast<u16*>(normed), normed_stride};
-  hipLaunchKernelGGL(rms_norm_residual_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0,
+  // 1024 channels (the code2wav pre-transformers' hidden size) unrolled, others generic
+  hipLaunchKernelGGL(p.groups == 4 ? rms_norm_residual_kernel<4> : rms_norm_residual_kernel<0>,
+                     dim3(blocks_for(rows, 4)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
