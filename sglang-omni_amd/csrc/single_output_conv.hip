@@ -229,6 +229,12 @@ __global__ void __launch_bounds__(kPositions) single_output_conv_bf16_kernel(con
     v[u] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, xo, 0, 0) |
            __builtin_amdgcn_raw_buffer_load_b128(h_rsrc, ho, 0, 0);
   }
+  // the weights [taps][C] go to LDS behind the rows (at most 8 x 128 floats: one float4 a
+  // thread), loaded with the rows, so the tap loop reads no global memory
+  float* ws = reinterpret_cast<float*>(xs + rows * PITCH);
+  const int wq = p.taps * C / 4;
+  f32x4 wv = {0.f, 0.f, 0.f, 0.f};
+  if (tid < wq) wv = *reinterpret_cast<const f32x4*>(p.weight + 4 * tid);
 #pragma unroll
   for (int u = 0; u < PIECES; ++u) {
     const int piece = tid + u * kPositions;
@@ -236,6 +242,7 @@ __global__ void __launch_bounds__(kPositions) single_output_conv_bf16_kernel(con
     const int c = (piece - r * G) * 8;
     if (r < rows) *reinterpret_cast<u32x4*>(xs + r * PITCH + c) = v[u];
   }
+  if (tid < wq) *reinterpret_cast<f32x4*>(ws + 4 * tid) = wv;
   if (hwrite >= 0) {
     // the last ctx samples of history ++ input, each written by the workgroup whose positions
     // hold it (those left of 0 by the first)
@@ -255,7 +262,7 @@ __global__ void __launch_bounds__(kPositions) single_output_conv_bf16_kernel(con
   float acc = 0.f;
   const u16* xrow = xs + tid * PITCH;
   for (int j = 0; j < p.taps; ++j) {
-    const float* wrow = p.weight + j * C;
+    const float* wrow = ws + j * C;
 #pragma unroll
     for (int c = 0; c < C; c += 8) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(xrow + j * PITCH + c);
@@ -283,7 +290,7 @@ int launch_soc_fast(const SocFastParams& p, hipStream_t s, dim3 grid) {
     return e == hipSuccess;
   }();
   (void)raised;
-  const size_t lds = (size_t)(kPositions + p.taps - 1) * (G * 8 + 8) * 2;
+  const size_t lds = (size_t)(kPositions + p.taps - 1) * (G * 8 + 8) * 2 + (size_t)p.taps * G * 8 * 4;
   hipLaunchKernelGGL(k, grid, dim3(kPositions), lds, s, p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
@@ -405,7 +412,8 @@ extern "C" int omni_single_output_conv(const void* x, int x_dtype, int64_t x_str
   if (x_dtype == OMNI_DTYPE_BF16 && in_activation == OMNI_ACTIVATION_NONE && !context_in_buffer &&
       (channels == 32 || channels == 64 || channels == 96 || channels == 128) &&
       taps <= kFastMaxTaps && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && x_stride_t % 8 == 0 &&
-      x_stride_b % 8 == 0 && (!hist_pool || (reinterpret_cast<uintptr_t>(hist_pool) & 15) == 0)) {
+      x_stride_b % 8 == 0 && (!hist_pool || (reinterpret_cast<uintptr_t>(hist_pool) & 15) == 0) &&
+      (reinterpret_cast<uintptr_t>(weight) & 15) == 0) {
     // 32-bit element offsets and buffer extents
     const int64_t x_bytes = ((batch - 1) * x_stride_b + (length - 1) * x_stride_t + channels) * 2;
     const int64_t hist_bytes = hist_pool ? hist_num_slots * hist_slot_stride * 2 : 0;
