@@ -463,7 +463,12 @@ struct DwParams {
   int pos_blocks;  // workgroups of positions per batch row (one more writes the new history)
 };
 
+// GROUPS > 0 fixes the 256-channel group count (unrolled, the groups' loads issued together);
+// GROUPS = 0 reads it from p.groups.
+template <int GROUPS>
 __global__ __launch_bounds__(256) void dwconv_layernorm_kernel(DwParams p) {
+  constexpr int NG = GROUPS > 0 ? GROUPS : kMaxGroups;
+  const int groups = GROUPS > 0 ? GROUPS : p.groups;
   const int64_t b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int C = p.channels;
@@ -477,43 +482,66 @@ __global__ __launch_bounds__(256) void dwconv_layernorm_kernel(DwParams p) {
       (slot >= 0 && !p.cold) ? p.hist + slot * p.hist_slot_stride + parity * kDwHistory * C
                              : nullptr;
   const float* xb = p.x + b * p.x_stride_b;
+  // this row's samples and its slot's old history as buffers (the launcher keeps a row's
+  // samples under 2 GiB); without a history its buffer is empty and reads zeros
+  const auto x_rsrc = buffer_rsrc(xb, (uint32_t)(p.length * C * 4));
+  const auto h_rsrc = buffer_rsrc(hread, hread ? (uint32_t)(kDwHistory * C * 4) : 0u);
   if ((int)blockIdx.x == p.pos_blocks) {
-    // the new history: the last 6 samples of (old history ++ this call's samples)
+    // the new history: the last 6 samples of (old history ++ this call's samples); every load
+    // before the first store (one at a time, each waited on, they were the launch's longest path)
     if (slot < 0) return;
     float* hw = p.hist + slot * p.hist_slot_stride + (1 - parity) * kDwHistory * C;
-    for (int e = threadIdx.x; e < kDwHistory * C; e += blockDim.x) {
+    auto source = [&](int e) {
       const int s = e / C;
       const int c = e - s * C;
-      const int64_t q = p.length + s;  // index into (history ++ samples)
-      float v;
-      if (q >= kDwHistory) v = xb[(q - kDwHistory) * C + c];
-      else v = hread ? hread[q * C + c] : 0.f;
-      hw[s * C + c] = v;
+      const int q = (int)p.length + s;  // index into (history ++ samples)
+      const uint32_t xo = q >= kDwHistory ? (uint32_t)((q - kDwHistory) * C + c) * 4u : kOutOfRange;
+      const uint32_t ho = q < kDwHistory ? (uint32_t)(q * C + c) * 4u : kOutOfRange;
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rsrc, xo, 0, 0) |
+                                           __builtin_amdgcn_raw_buffer_load_b32(h_rsrc, ho, 0, 0));
+    };
+    if constexpr (GROUPS > 0) {
+      constexpr int PER = kDwHistory * GROUPS;  // kDwHistory * C / 256 elements a thread
+      float hv[PER];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) hv[u] = source((int)threadIdx.x + u * 256);
+#pragma unroll
+      for (int u = 0; u < PER; ++u) hw[threadIdx.x + u * 256] = hv[u];
+    } else {
+      for (int e = threadIdx.x; e < kDwHistory * C; e += blockDim.x) hw[e] = source(e);
     }
     return;
   }
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= p.length) return;
-  float v[kMaxGroups][4];
+  float v[NG][4];
   float sum = 0.f;
 #pragma unroll
-  for (int g = 0; g < kMaxGroups; ++g) {
-    if (g < p.groups) {
+  for (int g = 0; g < NG; ++g) {
+    if (GROUPS > 0 || g < groups) {
       const int c = (g * kWave + lane) * 4;
       const float4 bias = *reinterpret_cast<const float4*>(p.bias + c);
       float a[4] = {bias.x, bias.y, bias.z, bias.w};
+      // the group's 7 taps and 7 weight vectors loaded into arrays before the first product:
+      // both sources of a tap loaded unconditionally, the one that does not hold it (or both,
+      // for a zero) at an out-of-range offset that reads zeros (loads under branches, or into
+      // one reused register, were issued one tap at a time)
+      float4 xt[kDwTaps], wt[kDwTaps];
 #pragma unroll
       for (int j = 0; j < kDwTaps; ++j) {
-        const int64_t pos = t - kDwHistory + j;
-        float4 x;
-        if (pos >= 0) x = *reinterpret_cast<const float4*>(xb + pos * C + c);
-        else if (hread) x = *reinterpret_cast<const float4*>(hread + (kDwHistory + pos) * C + c);
-        else x = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 w = *reinterpret_cast<const float4*>(p.weight + j * C + c);
-        a[0] += w.x * x.x;
-        a[1] += w.y * x.y;
-        a[2] += w.z * x.z;
-        a[3] += w.w * x.w;
+        const int pos = (int)t - kDwHistory + j;
+        const uint32_t xo = pos >= 0 ? (uint32_t)(pos * C + c) * 4u : kOutOfRange;
+        const uint32_t ho = pos < 0 ? (uint32_t)((kDwHistory + pos) * C + c) * 4u : kOutOfRange;
+        xt[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, xo, 0, 0) |
+                                               __builtin_amdgcn_raw_buffer_load_b128(h_rsrc, ho, 0, 0));
+        wt[j] = *reinterpret_cast<const float4*>(p.weight + j * C + c);
+      }
+#pragma unroll
+      for (int j = 0; j < kDwTaps; ++j) {
+        a[0] += wt[j].x * xt[j].x;
+        a[1] += wt[j].y * xt[j].y;
+        a[2] += wt[j].z * xt[j].z;
+        a[3] += wt[j].w * xt[j].w;
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -525,8 +553,8 @@ __global__ __launch_bounds__(256) void dwconv_layernorm_kernel(DwParams p) {
   const float mean = wave_sum(sum) / (float)C;
   float var = 0.f;
 #pragma unroll
-  for (int g = 0; g < kMaxGroups; ++g)
-    if (g < p.groups)
+  for (int g = 0; g < NG; ++g)
+    if (GROUPS > 0 || g < groups)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float d = v[g][k] - mean;
@@ -535,8 +563,8 @@ __global__ __launch_bounds__(256) void dwconv_layernorm_kernel(DwParams p) {
   const float inv = rsqrtf(wave_sum(var) / (float)C + p.eps);
   u16* ob = p.out + b * p.out_stride_b + t * C;
 #pragma unroll
-  for (int g = 0; g < kMaxGroups; ++g) {
-    if (g < p.groups) {
+  for (int g = 0; g < NG; ++g) {
+    if (GROUPS > 0 || g < groups) {
       const int c = (g * kWave + lane) * 4;
       const float4 w = *reinterpret_cast<const float4*>(p.ln_weight + c);
       const float4 bb = *reinterpret_cast<const float4*>(p.ln_bias + c);
@@ -741,7 +769,7 @@ extern "C" int omni_dwconv_layernorm(const float* x, int64_t batch, int64_t leng
   if (!aligned(x, 16) || !aligned(out, 8) || (hist_pool && !aligned(hist_pool, 16)))
     return OMNI_ERR_INVALID_ARG;
   if (batch == 0 || length == 0) return OMNI_OK;
-  if (batch > 65535) return OMNI_ERR_UNSUPPORTED;
+  if (batch > 65535 || length * channels * 4 > 0x7fffffffLL) return OMNI_ERR_UNSUPPORTED;
   DwParams p{};
   p.x = x;
   p.x_stride_b = x_stride_b;
@@ -763,7 +791,8 @@ extern "C" int omni_dwconv_layernorm(const float* x, int64_t batch, int64_t leng
   p.out_stride_b = out_stride_b;
   p.pos_blocks = (int)blocks_for(length, 4);
   dim3 grid((unsigned)(p.pos_blocks + 1), (unsigned)batch);
-  hipLaunchKernelGGL(dwconv_layernorm_kernel, grid, dim3(256), 0,
+  hipLaunchKernelGGL(p.groups == 4 ? dwconv_layernorm_kernel<4> : dwconv_layernorm_kernel<0>,
+                     grid, dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), p);
   OMNI_LAUNCH_CHECK();
   return OMNI_OK;
