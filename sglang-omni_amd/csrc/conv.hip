@@ -234,6 +234,9 @@ int make_conv_params(const omni_conv_args* a, ConvParams& p, bool& x_f32, bool& 
 // slice order) * scale[n] + bias[n % c_out]), the activation (none, Snake with per-channel
 // act_a / act_b, LeakyReLU) and the store (bf16 rounded to nearest even, or float32) as the conv
 // epilogue applies them. One thread per 4 columns of one position.
+// SPLITS > 0 fixes the slice count: every slice's partial is loaded before the first add (in a
+// loop each add waited for its load); SPLITS = 0 reads it from `splits`. Slices add in order.
+template <int SPLITS>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(
     const float* partial, int splits, int64_t slice, int n_cols, int c_out, int length,
     int quads, const float* scale, const float* bias, int act, const float* act_a,
@@ -244,8 +247,18 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(
   const int m = e / nq;
   const int n = (e - m * nq) * 4;
   const float* src = partial + (int64_t)m * n_cols + n;
-  f32x4 v = *reinterpret_cast<const f32x4*>(src);
-  for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4*>(src + s * slice);
+  f32x4 v;
+  if constexpr (SPLITS > 0) {
+    f32x4 part[SPLITS];
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s) part[s] = *reinterpret_cast<const f32x4*>(src + s * slice);
+    v = part[0];
+#pragma unroll
+    for (int s = 1; s < SPLITS; ++s) v += part[s];
+  } else {
+    v = *reinterpret_cast<const f32x4*>(src);
+    for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4*>(src + s * slice);
+  }
   f32x4 sc = f32x4{1.f, 1.f, 1.f, 1.f}, bi = f32x4{0.f, 0.f, 0.f, 0.f};
   if (scale) sc = *reinterpret_cast<const f32x4*>(scale + n);
   if (bias) {
@@ -321,7 +334,8 @@ int conv_entry(const omni_conv_args* a, int kernel, int config, bool launch, int
   int r = dispatch(p, x_f32, fp8, fuse2, family, ch, reinterpret_cast<hipStream_t>(stream));
   if (r == OMNI_OK && launch && k_splits > 1) {
     const int quads = (int)(positions * a->n_cols / 4);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(p.k_splits == 4 ? splitk_reduce_kernel<4> : splitk_reduce_kernel<0>,
+                       dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), p.partial, p.k_splits,
                        positions * a->n_cols, p.n_cols, p.c_out, p.length, quads, p.wscale,
                        p.bias, p.act, p.act_a, p.act_b, p.slope, p.out, p.out_bf16, p.o_sb,
