@@ -587,7 +587,8 @@ int omni_waveform_egress(const float* wave, int64_t rows, int64_t samples,
  *   float32, tap 6 on the current sample) over x [batch][length][channels] float32 with slot
  *   history (pool [slots][2][6][channels] float32, copy slot_parity & 1 read, the other written),
  *   plus bias, then LayerNorm(eps) with ln_weight / ln_bias, written as bf16
- *   (incremental_codec.py:160-175, modeling_qwen3_omni_moe.py:3231-3264).
+ *   (incremental_codec.py:160-175, modeling_qwen3_omni_moe.py:3231-3264). A row's samples
+ *   (length * channels * 4 bytes) below 2 GiB, else OMNI_ERR_UNSUPPORTED.
  * omni_bias_gelu: y = GELU(y + bias[col]) in place (erf form), bf16.
  * omni_bias_scale_residual: r[row, c] += gamma[c] * (y[row, c] + bias[c]) (r float32
  *   contiguous, y bf16); if out, also out[row, c] = bf16(r[row, c]).
