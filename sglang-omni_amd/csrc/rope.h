@@ -26,7 +26,9 @@ OMNI_DEVICE int64_t row_start(const int64_t* slot_index, const int64_t* position
 // the integer revolutions removed exactly (hi - rint(hi) is exact for |hi| < 2^23), so the
 // reduced argument is the float nearest the angle's true fraction of a turn (within 3e-8
 // revolutions for the angles position * inv_freq of positions up to 2e5, checked against exact
-// arithmetic), however large the angle. A general-argument sincosf costs several times more.
+// arithmetic), however large the angle: a short branch-free sequence in place of the general
+// sincosf's range reduction (the qkv GEMM's rotary epilogue measured the same launch time with
+// either; its cost is elsewhere).
 constexpr float kRevHi = 0.15915493667125702f;
 constexpr float kRevLo = 6.4206382432985265e-09f;
 OMNI_DEVICE void sincos_rev(float angle, float* s, float* c) {
