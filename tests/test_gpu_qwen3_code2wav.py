@@ -308,6 +308,35 @@ def test_small_decoder_streams_like_the_whole_decode(small, gpu):
     assert torch.equal(again, parts[0][:1])
 
 
+def test_small_decoder_rotary_epilogue_gives_the_two_launch_bits(small, gpu):
+    """The qkv GEMM with the rotary embedding and the ring writes in its epilogue
+    (omni_gemm_rope_kv) and the GEMM followed by the rotary kernel give the same waveform bits,
+    whole and streamed through the K / V rings."""
+    state, dec = small
+    assert dec.fused_rope  # 64-wide heads, (4 + 2 * 2) * 64 qkv columns
+
+    def run():
+        codes = _codes(SMALL, 3, 26, 11).to(gpu)
+        whole = dec.from_indices(codes).cpu()
+        pool = dec.new_state_pool(num_slots=4)
+        index = torch.tensor([3, 0, 1], dtype=torch.int64, device=gpu)
+        parts, s = [], 0
+        for n in (5, 9, 12):
+            parts.append(dec.decode_slots(codes[..., s:s + n], pool, index,
+                                          first_decode=s == 0).cpu())
+            s += n
+        return whole, torch.cat(parts, dim=-1)
+
+    fused = run()
+    dec.fused_rope = False
+    try:
+        two_launch = run()
+    finally:
+        dec.fused_rope = True
+    assert torch.equal(fused[0], two_launch[0])
+    assert torch.equal(fused[1], two_launch[1])
+
+
 def test_small_decoder_rows_at_different_positions_keep_their_streams(small, gpu):
     """Two streams at different positions (12 and 20 frames in) continue in one decode: each
     row reads its own slot's ring window and histories (code2wav.py:417-460 with per-slot frame
