@@ -77,6 +77,8 @@ def check_waveform(actual: torch.Tensor, expected: torch.Tensor, max_abs: float 
 
 
 def test_rms_norm_residual(gpu):
+    # 1024 channels with the residual add (the unrolled kernel), 256 without (the generic one),
+    # then each kernel on the other case
     g = torch.Generator().manual_seed(0)
     h = torch.randn(37, 1024, generator=g) * 3
     delta = bf16r(torch.randn(37, 1024, generator=g))
@@ -97,6 +99,23 @@ def test_rms_norm_residual(gpu):
     F.rms_norm_residual(h2, torch.ones(256, device=gpu), 1e-6, n2)
     assert torch.equal(h2, before)
     torch.testing.assert_close(n2.float().cpu(), Q.rms_norm(before.cpu(), torch.ones(256), 1e-6),
+                               rtol=2 ** -8, atol=1e-6)
+    h3 = (torch.randn(9, 1024, generator=g) * 2).to(gpu)
+    n3 = torch.empty(9, 1024, dtype=torch.bfloat16, device=gpu)
+    before3 = h3.clone()
+    F.rms_norm_residual(h3, weight.to(gpu), 1e-5, n3)
+    assert torch.equal(h3, before3)
+    torch.testing.assert_close(n3.float().cpu(), Q.rms_norm(before3.cpu(), weight, 1e-5),
+                               rtol=2 ** -8, atol=1e-6)
+    h4 = torch.randn(6, 512, generator=g)
+    d4 = bf16r(torch.randn(6, 512, generator=g))
+    s4 = torch.rand(512, generator=g)
+    h4d = h4.to(gpu)
+    n4 = torch.empty(6, 512, dtype=torch.bfloat16, device=gpu)
+    F.rms_norm_residual(h4d, torch.ones(512, device=gpu), 1e-5, n4,
+                        delta=d4.to(torch.bfloat16).to(gpu), scale=s4.to(gpu))
+    torch.testing.assert_close(h4d.cpu(), h4 + s4 * d4, rtol=1e-6, atol=1e-5)
+    torch.testing.assert_close(n4.float().cpu(), Q.rms_norm(h4 + s4 * d4, torch.ones(512), 1e-5),
                                rtol=2 ** -8, atol=1e-6)
 
 
@@ -236,9 +255,10 @@ def test_silu_mul_bias_gelu_and_scale_residual(gpu):
     assert torch.equal(z.cpu(), rd.cpu().to(torch.bfloat16))
 
 
-def test_dwconv_layernorm_whole_and_streamed(gpu):
+@pytest.mark.parametrize("c", [512, 1024])  # the generic kernel and the unrolled 1024-channel one
+def test_dwconv_layernorm_whole_and_streamed(gpu, c):
     g = torch.Generator().manual_seed(4)
-    batch, length, c = 2, 23, 512
+    batch, length = 2, 23
     x = torch.randn(batch, length, c, generator=g)
     w = torch.randn(c, 1, 7, generator=g) * 0.4
     bias = torch.randn(c, generator=g) * 0.1
